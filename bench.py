@@ -1,0 +1,206 @@
+#!/usr/bin/env python3
+"""Benchmark of the force hot path on one MI355X: EAM/alloy fp64 at 131,072 atoms.
+
+One step is what PairJaxKokkos::compute does each MD step (cpp/pair_jax_kokkos.cpp:989-1102):
+pack atoms, pack the cutoff-filtered edges from the Kokkos-layout neighbour list, the EAM
+energy + forces + virial pass with the force add into the engine's f, and the host readback of
+energy, virial and the edge count. Inputs (x, types, the neighbour list) are resident in HBM
+before the timed region; the list is built once on the host (the engine's job, not timed).
+
+Prints one JSON line: atom-steps/s, per-stage kernel times from HIP events recorded inside the
+library on the launch stream, the roofline of the dominant kernel and the CPU baseline (the
+oracle's single-threaded restatement of the same step on a bounded sample of steps).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "lammps-jax_amd"))
+
+METRIC = "EAM fp64 atom-steps/s @131k atoms; achieved HBM GB/s (% of peak)"
+HBM_PEAK_GBS = 8000.0
+
+
+def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: int,
+                words: int) -> float:
+    """Algorithmic (compulsory, unique) HBM bytes of one launch of a stage.
+
+    R list rows, A = owned + ghost atoms, N owned, E packed edges, entries = list entries read,
+    S bytes per model scalar, words = validity words per row."""
+    rec = 4 * S  # atom record: x, y, z, species
+    if stage == "pack_atoms":
+        return A * (24 + 4) + A * (rec + 4)
+    if stage == "pack_count":
+        return 8 * R + 4 * entries + 24 * A + 8 * R + 4 * R * words
+    if stage == "pack_write":
+        return 8 * R + 4 * R * words + 9 * E
+    if stage == "eam_density":
+        return 8 * R + 4 * E + rec * A + 2 * S * N
+    if stage == "eam_force":
+        return 8 * R + 4 * E + rec * A + S * A + 48 * N
+    if stage == "lj_rows":
+        return 8 * R + 4 * E + rec * A + 48 * N
+    if stage == "forward_fp":
+        return (A - N) * (4 + 2 * S)
+    return 0.0
+
+
+def survey_bytes(*, R, A, N, E, entries, S) -> dict:
+    """Whole-step algorithmic bytes in the survey's accounting (edge arrays 9 B/edge per sweep)."""
+    b_pack = 8 * R + 4 * entries + 24 * A + 9 * E
+    b_eam = 18 * E + 28 * A + 2 * S * N + 48 * A
+    return {"pack": b_pack, "eam": b_eam, "total": b_pack + b_eam}
+
+
+def cpu_baseline(wl, sysm, lst, max_atoms, max_edges, budget_s: float, max_steps: int) -> dict:
+    """The oracle (single-threaded C++ restatement) doing the same step: pack + one-sided EAM."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle as O
+
+    nall, nl = sysm.nall, sysm.nlocal
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < max_steps and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        pos, sp = O.pack_atoms(sysm.x, sysm.type, nall, max_atoms, 8)
+        s, r, m, _, _ = O.pack_neighbors(sysm.x, lst, max_atoms=max_atoms, max_edges=max_edges,
+                                         nlocal=nl, cutoff=wl.cutoff)
+        O.eam_compute(wl.tables, pos, sp, nlocal=nl, nghost=sysm.nghost, senders=s, receivers=r,
+                      mask=m, mode=O.ONESIDED, ghost_owner=sysm.ghost_owner)
+        times.append(time.perf_counter() - t0)
+    per_step = sum(times) / len(times)
+    return {
+        "value": nl / per_step,
+        "unit": "atom-steps/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{len(times)} full steps of {wl.name} (pack + one-sided EAM E/F/virial), "
+                  f"{per_step * 1e3:.1f} ms/step, single thread, host {platform.processor() or platform.machine()}",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="eam_alloy_131k")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (one GPU per box); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from lammps_jax_amd import systems
+    from lammps_jax_amd.pair import PairJax
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    t_setup = time.perf_counter()
+    wl = systems.make_workload(args.workload)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=wl.list_kind)
+    model = ("eam", wl.tables) if wl.model == "eam" else ("lj", wl.lj)
+    nall = sysm.nall
+    max_atoms = ((nall * 21 // 20) + 1023) // 1024 * 1024  # 5% headroom, like an exported bundle
+    pj = PairJax(sysm, model, precision=wl.precision, accumulation=wl.accumulation,
+                 n_hops=wl.n_hops, max_atoms=max_atoms, edges_per_atom=wl.edges_per_atom,
+                 device="cuda:0")
+    setup_s = time.perf_counter() - t_setup
+    print(f"[bench] {wl.name}: N={sysm.nlocal} ghosts={sysm.nghost} list entries={lst['entries']} "
+          f"max_atoms={max_atoms} max_edges={pj.max_edges} setup {setup_s:.1f}s", file=sys.stderr,
+          flush=True)
+
+    for _ in range(args.warmup):
+        info = pj.compute()
+    torch.cuda.synchronize(dev)
+    pj.h.timing_enable(True)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        info = pj.compute()
+    torch.cuda.synchronize(dev)
+    elapsed = time.perf_counter() - t0
+    stages = pj.h.timing()
+    pj.h.timing_enable(False)
+    print(f"[bench] timed {args.steps} steps in {elapsed:.4f}s", file=sys.stderr, flush=True)
+
+    N, A, E = sysm.nlocal, nall, info.edge_count
+    R = lst["inum"] + (lst["gnum"] if wl.n_hops > 1 else 0)
+    S = wl.precision
+    words = (lst["maxneighs"] + 31) // 32
+    stage_us = {k: 1e3 * tot / cnt for k, (tot, cnt) in stages.items()}
+    device_us = sum(stage_us.values())
+    kernel_stages = {k: v for k, v in stage_us.items() if stage_bytes(
+        k, R=R, A=A, N=N, E=E, entries=lst["entries"], S=S, words=words) > 0}
+    dom = max(kernel_stages, key=kernel_stages.get)
+    dom_bytes = stage_bytes(dom, R=R, A=A, N=N, E=E, entries=lst["entries"], S=S, words=words)
+    achieved = dom_bytes / (stage_us[dom] * 1e-6) / 1e9
+    sb = survey_bytes(R=R, A=A, N=N, E=E, entries=lst["entries"], S=S)
+    ms_per_step = 1e3 * elapsed / args.steps
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(wl, sysm, lst, max_atoms, pj.max_edges, args.cpu_budget, 50)
+
+    line = {
+        "metric": METRIC,
+        "value": N * args.steps / elapsed,
+        "unit": "atom-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64" if S == 8 else "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": wl.name,
+            "atoms": N,
+            "ghosts": sysm.nghost,
+            "list_entries": lst["entries"],
+            "edges": E,
+            "edge_capacity_per_atom": wl.edges_per_atom,
+            "accumulation": wl.accumulation,
+            "step": "pack_atoms + pack_edges + model E/F/virial + f add + host readback",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom,
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "stages_us": {k: round(v, 2) for k, v in sorted(stage_us.items())},
+        "device_us_per_step": round(device_us, 2),
+        "step_roofline": {
+            "survey_bytes_per_step": sb["total"],
+            "device_us": round(device_us, 2),
+            "frac_of_hbm_peak": sb["total"] / (device_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        },
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

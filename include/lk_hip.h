@@ -1,0 +1,186 @@
+/*
+ * lk_hip.h — C ABI of the MI355X (gfx950) force hot path behind `pair_style jax/kk`.
+ *
+ * One handle is the device state of one pair-style instance on one GPU: the bundle contract,
+ * the model (EAM/alloy tables or LJ 12-6 parameters), the staging and packed-edge buffers
+ * sized once from the contract capacities (never resized), and the per-step results.
+ *
+ * Every entry point is stream-ordered on the caller's HIP stream (the Kokkos execution space
+ * stream in a LAMMPS build); only lk_step_result synchronises. Pointers named x, f, ilist,
+ * numneigh and neighbors are device pointers owned by the caller (the engine) and are never
+ * freed here. Errors return a status code; lk_last_error gives the message. Nothing throws
+ * across this boundary.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository root):
+ *   lk_create / lk_destroy   PairJaxKokkos::allocate_device_buffers (cpp/pair_jax_kokkos.cpp:355-398)
+ *                            plus the contract checks of lammps_jax::load_bundle_file
+ *                            (cpp/lammps_jax_model.cpp:227-314)
+ *   lk_set_eam / lk_set_lj   the exported program: python/lammps_jax/eam.py:265-333 (setfl EAM),
+ *                            examples/export_model.py:16-50 (LJ), compiled at
+ *                            pjrt::Runtime::initialize (cpp/pjrt/runtime.cpp:291-334)
+ *   lk_pack_atoms            PairJaxKokkos::pack_atoms (cpp/pair_jax_kokkos.cpp:794-809)
+ *   lk_pack_edges            PairJaxKokkos::pack_edges (cpp/pair_jax_kokkos.cpp:811-874)
+ *   lk_compute               Runtime::execute_energy_force / execute_force
+ *                            (cpp/pjrt/runtime.cpp:442-473) followed by add_model_forces
+ *                            (cpp/pair_jax_kokkos.cpp:959-987) and the f.r virial
+ *                            (cpp/pair_jax_kokkos.cpp:1092-1100)
+ *   lk_step_result           the host reads after execution: exec.fence + edge count/overflow
+ *                            (cpp/pair_jax_kokkos.cpp:1063-1081) and eng_vdwl (cpp:1083)
+ */
+#ifndef LK_HIP_H
+#define LK_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define LK_OK 0
+#define LK_ERR_ARGUMENT 1
+#define LK_ERR_DEVICE 2
+#define LK_ERR_CAPACITY 3
+#define LK_ERR_STATE 4
+#define LK_ERR_UNSUPPORTED 5
+
+/* contract precision (lammps_jax_model.h:31-34): bytes per model scalar */
+#define LK_FLOAT32 4
+#define LK_FLOAT64 8
+
+/* newton mode (lammps_jax_model.h:24-28) */
+#define LK_NEWTON_ANY 0
+#define LK_NEWTON_ON 1
+#define LK_NEWTON_OFF 2
+
+/* edge pairing (export.py:548-549): full, half, half-unique */
+#define LK_PAIRING_FULL 0
+#define LK_PAIRING_HALF 1
+#define LK_PAIRING_HALF_UNIQUE 2
+
+/*
+ * Accumulation scheme of the model pass.
+ *   LK_ACCUM_PLAIN     the sparse-edge atom-force bundle (wrap_energy_fn, export.py:153-209):
+ *                      sender += g, receiver -= g, ghost rows filled for the reverse comm.
+ *   LK_ACCUM_HALF      the communicating half-edge bundle (eam.py:303-317): density to both
+ *                      ends, ghost density partials folded into their owners.
+ *   LK_ACCUM_ONESIDED  the full-list row scheme (eam_pallas.py:181-249 with a full list): each
+ *                      owned row sums its own density and its whole force; ghost F' comes from
+ *                      the owner; ghost rows get no force; the virial is summed per pair.
+ */
+#define LK_ACCUM_PLAIN 0
+#define LK_ACCUM_HALF 1
+#define LK_ACCUM_ONESIDED 2
+
+/* lk_compute flags: eflag_global and vflag_fdotr of PairJaxKokkos::compute (cpp:989-1003) */
+#define LK_ENERGY 1
+#define LK_VIRIAL 2
+
+typedef struct lk_handle lk_handle;
+
+/* The bundle contract (lammps_jax_model.h:43-76), sparse-edge layout. */
+typedef struct lk_contract {
+  int max_atoms;     /* owned + ghost rows */
+  int max_edges;     /* packed edge slots */
+  int n_species;     /* 0: species-blind */
+  int precision;     /* LK_FLOAT32 | LK_FLOAT64 */
+  int newton;        /* LK_NEWTON_* */
+  int pairing;       /* LK_PAIRING_* */
+  int n_hops;        /* receptive field in cutoffs */
+  int pair_sum;      /* pair-sum energy bundle: duplicate reverse edges on half lists */
+  int comm;          /* bundle exchanges rows mid-program (comm_widths non-empty) */
+  int edge_force;    /* force_output edge-force */
+  int newton_pair;   /* the run's newton pair setting (force->newton_pair) */
+  int half_list;     /* the LAMMPS list is a half list (PairJaxKokkos::half_list, cpp:425-431) */
+  double cutoff;     /* model cutoff (init_one) */
+} lk_contract;
+
+/* setfl EAM tables: PairEAM::interpolate coefficients (eam.py:115-135), float64. */
+typedef struct lk_eam_tables {
+  int n_el;
+  int nrho;
+  int nr;
+  double drho;
+  double dr;
+  double cutoff;
+  const double *embedding; /* [n_el][nrho][4] */
+  const double *density;   /* [n_el][nr][4] */
+  const double *pair;      /* [n_el*(n_el+1)/2][nr][4], rows hold r*phi */
+} lk_eam_tables;
+
+/* LJ 12-6, truncated, unshifted (export_model.py:16-50). */
+typedef struct lk_lj_params {
+  double epsilon;
+  double sigma;
+  double cutoff;
+  double edge_energy_scale; /* 0.5 on full lists */
+} lk_lj_params;
+
+/* Host-visible results of the last step (valid after lk_step_result). */
+typedef struct lk_step_info {
+  double energy;     /* scale * model energy; add to eng_vdwl */
+  double virial[6];  /* xx yy zz xy xz yz, add to virial[] */
+  int edge_count;    /* packed-edge demand count */
+  int edge_overflow; /* 1: demand exceeded max_edges (collective abort in LAMMPS) */
+} lk_step_info;
+
+/* Validates the contract and allocates every device buffer from its capacities. */
+int lk_create(const lk_contract *contract, lk_handle **out);
+void lk_destroy(lk_handle *h);
+const char *lk_last_error(const lk_handle *h);
+
+/* Model upload (one per handle). Tables are narrowed to the contract precision. */
+int lk_set_eam(lk_handle *h, const lk_eam_tables *tables);
+int lk_set_lj(lk_handle *h, const lk_lj_params *params);
+/* Selects the accumulation scheme (LK_ACCUM_*); checked against the contract. */
+int lk_set_accumulation(lk_handle *h, int accum);
+
+/*
+ * Single-rank exchange description: ghost row nlocal+g images owned row ghost_owner[g]
+ * (host array, copied). Stands in for LAMMPS forward/reverse comm of per-atom model rows
+ * when one rank owns every atom; multi-rank builds exchange through the engine instead.
+ */
+int lk_set_ghost_map(lk_handle *h, int nlocal, int nghost, const int *ghost_owner);
+
+/* x: LAMMPS positions [nall][3] double (device); type: 1-based LAMMPS types (device). */
+int lk_pack_atoms(lk_handle *h, void *stream, const double *x, const int *type, int nall);
+
+/*
+ * Cutoff-filters and compacts the Kokkos neighbour list into the packed edge arrays.
+ * ilist [inum+gnum], numneigh [nall], neighbors: LayoutLeft, entry (i, jj) at
+ * neighbors[jj * nb_stride + i]; special-bond bits are masked off. Rows scanned are
+ * inum (+ gnum when n_hops > 1), clamped to max_atoms. The edge count and overflow flag stay on
+ * the device until lk_step_result.
+ */
+int lk_pack_edges(lk_handle *h, void *stream, const double *x, const int *ilist,
+                  const int *numneigh, const int *neighbors, long nb_stride, int inum, int gnum,
+                  int maxneighs, int nlocal);
+
+/*
+ * Energy and gradient of the model on the packed edges, added into the engine's force array:
+ * f[i] += scale * F[i] (f: double [nall][3], device). flags: LK_ENERGY | LK_VIRIAL.
+ */
+int lk_compute(lk_handle *h, void *stream, int nlocal, int nghost, int flags, double scale,
+               double *f);
+
+/* Synchronises the stream and returns energy, virial and the pack counts of the last step. */
+int lk_step_result(lk_handle *h, void *stream, lk_step_info *out);
+
+/*
+ * Stage timing, the counterpart of the reference's Kokkos kernel labels (LAMMPSJAX::*,
+ * cpp/pair_jax_kokkos.cpp:530-1095) for profiling tools: when enabled, HIP events bracket each
+ * launch and lk_step_result accumulates the elapsed time per stage. lk_timing_read returns the
+ * stage at `index` (LK_ERR_ARGUMENT past the last one). Enabling resets the totals.
+ */
+int lk_timing_enable(lk_handle *h, int on);
+int lk_timing_read(lk_handle *h, int index, char *name, int name_len, double *total_ms,
+                   long *count);
+
+/* Device pointers of the handle's buffers (for tests and for engines that read them). */
+int lk_edge_buffers(lk_handle *h, int **senders, int **receivers, unsigned char **mask);
+int lk_staging_buffers(lk_handle *h, void **atoms, int **species);
+int lk_model_buffers(lk_handle *h, void **rho, void **fp);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LK_HIP_H */

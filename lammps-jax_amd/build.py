@@ -1,0 +1,89 @@
+"""Builds the native libraries of the package in-tree.
+
+liblkhip.so      the gfx950 HIP kernels and the extern "C" boundary (include/lk_hip.h)
+liblkharness.so  the single-rank LAMMPS stand-in (ghosts, Kokkos-layout neighbour lists)
+
+Both land next to the Python package so a repository snapshot carries them to a GPU host.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+REPO = ROOT.parent
+CSRC = ROOT / "csrc"
+PKG = ROOT / "lammps_jax_amd"
+BUILD = ROOT / "_build"
+
+HIP_SOURCES = ["lk_api.hip", "lk_pack.hip", "lk_eam.hip", "lk_lj.hip"]
+HIP_HEADERS = ["lk_device.h", "lk_internal.h"]
+
+OFFLOAD_ARCH = os.environ.get("LK_OFFLOAD_ARCH", "gfx950")
+HIPCC_FLAGS = [
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # packed-fp32 instructions stay off: plain scalar code only
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{REPO / 'include'}",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found; the HIP kernels need ROCm's hipcc")
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"build step failed: {' '.join(cmd[:3])} ...")
+
+
+def build_hip() -> Path:
+    """Compiles every .hip source for gfx950 and links liblkhip.so."""
+    BUILD.mkdir(exist_ok=True)
+    hipcc = _hipcc()
+    objs = []
+
+    def compile_one(src: str) -> Path:
+        obj = BUILD / (Path(src).stem + ".o")
+        _run([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        return obj
+
+    with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as pool:
+        objs = list(pool.map(compile_one, HIP_SOURCES))
+    out = PKG / "liblkhip.so"
+    tmp = PKG / "liblkhip.so.tmp"
+    _run([hipcc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    tmp.replace(out)
+    return out
+
+
+def build_harness() -> Path:
+    """Compiles the host-side LAMMPS stand-in with OpenMP."""
+    out = PKG / "liblkharness.so"
+    tmp = PKG / "liblkharness.so.tmp"
+    _run(["g++", "-O3", "-fopenmp", "-fPIC", "-shared", "-std=c++17",
+          str(CSRC / "harness" / "lk_harness.cpp"), "-o", str(tmp)])
+    tmp.replace(out)
+    return out
+
+
+def build_all() -> list[Path]:
+    return [build_hip(), build_harness()]
+
+
+if __name__ == "__main__":
+    for path in build_all():
+        print(path)

@@ -1,0 +1,461 @@
+// extern "C" boundary of the hot path. Validation follows the reference's contract checks
+// (cpp/lammps_jax_model.cpp:271-313) and the per-step flow of PairJaxKokkos::compute
+// (cpp/pair_jax_kokkos.cpp:989-1102); buffers follow allocate_device_buffers (cpp:355-398).
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <iterator>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "lk_device.h"
+#include "lk_internal.h"
+
+struct lk_handle {
+  lk::Handle h;
+};
+
+namespace {
+
+using lk::Handle;
+
+int fail(Handle &h, int code, const std::string &msg)
+{
+  h.error = msg;
+  return code;
+}
+
+int hip_fail(Handle &h, hipError_t e, const char *what)
+{
+  h.error = std::string(what) + ": " + hipGetErrorString(e);
+  return LK_ERR_DEVICE;
+}
+
+template <typename T>
+hipError_t dalloc(T **p, size_t count)
+{
+  *p = nullptr;
+  if (count == 0) count = 1;
+  return hipMalloc(reinterpret_cast<void **>(p), count * sizeof(T));
+}
+
+__global__ void k_fill_int(int *p, long n, int v)
+{
+  const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+void free_all(Handle &h)
+{
+  void *ptrs[] = {h.d_rtab,      h.d_etab,      h.d_atoms,       h.d_species,   h.d_senders,
+                  h.d_receivers, h.d_mask,      h.d_row_count,   h.d_row_atom,  h.d_tile_count,
+                  h.d_tile_off,  h.d_bits,      h.d_fp,          h.d_rho,       h.d_partials,
+                  h.d_result,    h.d_ghost_owner};
+  for (void *p : ptrs)
+    if (p) (void)hipFree(p);
+  if (h.h_result) (void)hipHostFree(h.h_result);
+  for (hipEvent_t ev : h.event_pool) (void)hipEventDestroy(ev);
+  h.event_pool.clear();
+}
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+int ensure_bits(Handle &h, int maxneighs)
+{
+  const int words = (maxneighs + 31) / 32;
+  if (words <= h.bits_words) return LK_OK;
+  // Lists grow rarely (LAMMPS reallocates d_neighbors only when a row outgrows it); the
+  // validity-bit buffer follows, outside any captured region.
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(h, e, "hipDeviceSynchronize");
+  if (h.d_bits) (void)hipFree(h.d_bits);
+  h.d_bits = nullptr;
+  e = dalloc(&h.d_bits, static_cast<size_t>(words) * h.contract.max_atoms);
+  if (e != hipSuccess) return hip_fail(h, e, "hipMalloc(validity bits)");
+  h.bits_words = words;
+  return LK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lk_create(const lk_contract *c, lk_handle **out)
+{
+  if (!out) return LK_ERR_ARGUMENT;
+  *out = nullptr;
+  auto *wrap = new lk_handle();
+  Handle &h = wrap->h;
+  if (!c) {
+    *out = wrap;
+    return fail(h, LK_ERR_ARGUMENT, "contract is null");
+  }
+  h.contract = *c;
+  *out = wrap;
+  // cpp/lammps_jax_model.cpp:277-279
+  if (c->max_atoms <= 0 || c->max_edges <= 0)
+    return fail(h, LK_ERR_ARGUMENT, "Invalid fixed capacities in bundle");
+  if (c->precision != LK_FLOAT32 && c->precision != LK_FLOAT64)
+    return fail(h, LK_ERR_ARGUMENT, "Unsupported LAMMPS-JAX precision; expected float32 or float64");
+  if (c->n_hops < 1) return fail(h, LK_ERR_ARGUMENT, "Invalid n_hops in bundle");
+  if (c->n_species < 0) return fail(h, LK_ERR_ARGUMENT, "Invalid n_species in bundle");
+  if (c->cutoff < 0) return fail(h, LK_ERR_ARGUMENT, "cutoff must be non-negative");
+  const bool half_edges = c->pairing != LK_PAIRING_FULL;
+  if (c->pairing == LK_PAIRING_HALF && c->comm)
+    return fail(h, LK_ERR_ARGUMENT,
+                "Communicating half-edge bundles now pack each boundary pair on one rank; "
+                "re-export this bundle");
+  if (c->pairing == LK_PAIRING_HALF_UNIQUE && !c->comm)
+    return fail(h, LK_ERR_ARGUMENT,
+                "Unique-boundary bundles need a communication schedule; the partner rank's "
+                "density share arrives through reverse comm");
+  if (half_edges && c->n_hops == 1 && !c->comm)
+    return fail(h, LK_ERR_ARGUMENT,
+                "Half-edge bundles require n_hops > 1 or a communication schedule; the "
+                "single-hop packer does not deduplicate edge directions");
+  if (c->n_hops > 1 && (c->newton != LK_NEWTON_ON || c->edge_force))
+    return fail(h, LK_ERR_ARGUMENT,
+                "Bundles with n_hops > 1 require newton on and atom-force output; ghost force "
+                "rows must flow back through the LAMMPS reverse communication");
+  if (c->comm && c->n_hops != 1)
+    return fail(h, LK_ERR_ARGUMENT,
+                "Communicating bundles require a one-cutoff ghost shell (n_hops = 1)");
+  if (c->comm && c->newton != LK_NEWTON_ON && (half_edges || c->edge_force))
+    return fail(h, LK_ERR_ARGUMENT,
+                "Communicating bundles require newton on unless they pair fully and return atom "
+                "forces; ghost force rows flow back through the LAMMPS reverse communication");
+  if (c->edge_force)
+    return fail(h, LK_ERR_UNSUPPORTED, "edge-force output is not implemented by this build");
+  // init_style newton checks (cpp/pair_jax_kokkos.cpp:668-673)
+  if (c->newton == LK_NEWTON_ON && !c->newton_pair)
+    return fail(h, LK_ERR_ARGUMENT,
+                "LAMMPS-JAX bundle was exported for newton pair on; this run uses newton off");
+  if (c->newton == LK_NEWTON_OFF && c->newton_pair)
+    return fail(h, LK_ERR_ARGUMENT,
+                "LAMMPS-JAX bundle was exported for newton pair off; this run uses newton on");
+  // default accumulation from the contract
+  if (half_edges)
+    h.accum = LK_ACCUM_HALF;
+  else if (c->comm && !c->newton_pair)
+    h.accum = LK_ACCUM_ONESIDED;
+  else
+    h.accum = LK_ACCUM_PLAIN;
+
+  hipError_t e = hipGetDevice(&h.device);
+  if (e != hipSuccess) return hip_fail(h, e, "hipGetDevice");
+  const size_t A = static_cast<size_t>(c->max_atoms);
+  const size_t E = static_cast<size_t>(c->max_edges);
+  const size_t S = h.scalar_bytes();
+  const size_t tiles = A / lk::kWave + 2;
+  if ((e = hipMalloc(&h.d_atoms, A * 4 * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(atoms)");
+  if ((e = dalloc(&h.d_species, A)) != hipSuccess) return hip_fail(h, e, "hipMalloc(species)");
+  if ((e = dalloc(&h.d_senders, E)) != hipSuccess) return hip_fail(h, e, "hipMalloc(senders)");
+  if ((e = dalloc(&h.d_receivers, E)) != hipSuccess) return hip_fail(h, e, "hipMalloc(receivers)");
+  if ((e = dalloc(&h.d_mask, E)) != hipSuccess) return hip_fail(h, e, "hipMalloc(edge_mask)");
+  if ((e = dalloc(&h.d_row_count, A)) != hipSuccess) return hip_fail(h, e, "hipMalloc(row_count)");
+  if ((e = dalloc(&h.d_row_atom, A)) != hipSuccess) return hip_fail(h, e, "hipMalloc(row_atom)");
+  if ((e = dalloc(&h.d_tile_count, 2 * tiles)) != hipSuccess) return hip_fail(h, e, "hipMalloc(tiles)");
+  if ((e = dalloc(&h.d_tile_off, tiles)) != hipSuccess) return hip_fail(h, e, "hipMalloc(tile_off)");
+  if ((e = hipMalloc(&h.d_fp, A * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(fp)");
+  if ((e = hipMalloc(&h.d_rho, A * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(rho)");
+  if ((e = dalloc(&h.d_partials, 8 * tiles)) != hipSuccess) return hip_fail(h, e, "hipMalloc(partials)");
+  if ((e = dalloc(&h.d_result, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(result)");
+  if ((e = hipHostMalloc(reinterpret_cast<void **>(&h.h_result), sizeof(lk::StepResult))) != hipSuccess)
+    return hip_fail(h, e, "hipHostMalloc(result)");
+  std::memset(h.h_result, 0, sizeof(lk::StepResult));
+  // Padding contract (cpp:368-383): unpacked slots index max_atoms with the mask off.
+  const long fill_blocks = static_cast<long>((E + 255) / 256);
+  hipLaunchKernelGGL(k_fill_int, dim3(fill_blocks), dim3(256), 0, 0, h.d_senders, static_cast<long>(E), c->max_atoms);
+  hipLaunchKernelGGL(k_fill_int, dim3(fill_blocks), dim3(256), 0, 0, h.d_receivers, static_cast<long>(E), c->max_atoms);
+  (void)hipMemset(h.d_mask, 0, E);
+  (void)hipMemset(h.d_atoms, 0, A * 4 * S);
+  (void)hipMemset(h.d_species, 0, A * sizeof(int));
+  (void)hipMemset(h.d_fp, 0, A * S);
+  (void)hipMemset(h.d_rho, 0, A * S);
+  (void)hipMemset(h.d_partials, 0, 8 * tiles * sizeof(double));
+  (void)hipMemset(h.d_result, 0, sizeof(lk::StepResult));
+  if (int rc = ensure_bits(h, 128)) return rc;
+  e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(h, e, "initialising buffers");
+  return LK_OK;
+}
+
+void lk_destroy(lk_handle *w)
+{
+  if (!w) return;
+  free_all(w->h);
+  delete w;
+}
+
+const char *lk_last_error(const lk_handle *w) { return w ? w->h.error.c_str() : "null handle"; }
+
+int lk_set_eam(lk_handle *w, const lk_eam_tables *t)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (!t || !t->embedding || !t->density || !t->pair || t->n_el < 1 || t->nrho < 2 || t->nr < 2 ||
+      !(t->drho > 0) || !(t->dr > 0))
+    return fail(h, LK_ERR_ARGUMENT, "invalid EAM tables");
+  if (h.model != 0) return fail(h, LK_ERR_STATE, "a model is already loaded on this handle");
+  const int n_el = t->n_el, npair = n_el * (n_el + 1) / 2, n_rtab = n_el + npair;
+  const size_t S = h.scalar_bytes();
+  // node-major r-tables: [node][table][4], density tables first, then the pair tables
+  std::vector<double> r(static_cast<size_t>(t->nr) * n_rtab * 4);
+  for (int node = 0; node < t->nr; ++node) {
+    for (int z = 0; z < n_el; ++z)
+      for (int c = 0; c < 4; ++c)
+        r[(static_cast<size_t>(node) * n_rtab + z) * 4 + c] = t->density[(static_cast<size_t>(z) * t->nr + node) * 4 + c];
+    for (int p = 0; p < npair; ++p)
+      for (int c = 0; c < 4; ++c)
+        r[(static_cast<size_t>(node) * n_rtab + n_el + p) * 4 + c] = t->pair[(static_cast<size_t>(p) * t->nr + node) * 4 + c];
+  }
+  const size_t nemb = static_cast<size_t>(n_el) * t->nrho * 4;
+  hipError_t e;
+  if ((e = hipMalloc(&h.d_rtab, r.size() * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(rtab)");
+  if ((e = hipMalloc(&h.d_etab, nemb * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(etab)");
+  // jnp.asarray(tables, dtype): coefficients narrowed to the contract precision (eam.py:277-279)
+  if (S == 8) {
+    e = hipMemcpy(h.d_rtab, r.data(), r.size() * 8, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(h.d_etab, t->embedding, nemb * 8, hipMemcpyHostToDevice);
+  } else {
+    std::vector<float> rf(r.begin(), r.end());
+    std::vector<float> ef(t->embedding, t->embedding + nemb);
+    e = hipMemcpy(h.d_rtab, rf.data(), rf.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(h.d_etab, ef.data(), ef.size() * 4, hipMemcpyHostToDevice);
+  }
+  if (e != hipSuccess) return hip_fail(h, e, "hipMemcpy(tables)");
+  h.n_el = n_el;
+  h.nrho = t->nrho;
+  h.nr = t->nr;
+  h.n_rtab = n_rtab;
+  h.drho = t->drho;
+  h.dr = t->dr;
+  h.eam_cutoff = t->cutoff;
+  h.model = 1;
+  return LK_OK;
+}
+
+int lk_set_lj(lk_handle *w, const lk_lj_params *p)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (!p || !(p->cutoff >= 0) || !(p->sigma > 0)) return fail(h, LK_ERR_ARGUMENT, "invalid LJ parameters");
+  if (h.model != 0) return fail(h, LK_ERR_STATE, "a model is already loaded on this handle");
+  h.lj = *p;
+  h.model = 2;
+  return LK_OK;
+}
+
+int lk_set_accumulation(lk_handle *w, int accum)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  const bool half_edges = h.contract.pairing != LK_PAIRING_FULL;
+  switch (accum) {
+    case LK_ACCUM_ONESIDED:
+      if (half_edges || h.contract.half_list || h.contract.n_hops != 1)
+        return fail(h, LK_ERR_ARGUMENT,
+                    "one-sided accumulation needs full pairing over a full list with n_hops = 1");
+      break;
+    case LK_ACCUM_HALF:
+      if (!half_edges) return fail(h, LK_ERR_ARGUMENT, "half accumulation needs a half-edge bundle");
+      break;
+    case LK_ACCUM_PLAIN:
+      if (half_edges) return fail(h, LK_ERR_ARGUMENT, "plain accumulation needs full pairing");
+      break;
+    default:
+      return fail(h, LK_ERR_ARGUMENT, "unknown accumulation scheme");
+  }
+  h.accum = accum;
+  return LK_OK;
+}
+
+int lk_set_ghost_map(lk_handle *w, int nlocal, int nghost, const int *ghost_owner)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (nlocal < 0 || nghost < 0 || (nghost > 0 && !ghost_owner))
+    return fail(h, LK_ERR_ARGUMENT, "invalid ghost map");
+  if (nlocal + nghost > h.contract.max_atoms)
+    return fail(h, LK_ERR_CAPACITY, "ghost map exceeds the atom capacity");
+  for (int g = 0; g < nghost; ++g)
+    if (ghost_owner[g] < 0 || ghost_owner[g] >= nlocal)
+      return fail(h, LK_ERR_ARGUMENT, "ghost owner outside the owned rows");
+  hipError_t e;
+  if (nghost > h.ghost_cap) {
+    if (h.d_ghost_owner) (void)hipFree(h.d_ghost_owner);
+    h.d_ghost_owner = nullptr;
+    if ((e = dalloc(&h.d_ghost_owner, nghost)) != hipSuccess) return hip_fail(h, e, "hipMalloc(ghost map)");
+    h.ghost_cap = nghost;
+  }
+  if (nghost > 0 &&
+      (e = hipMemcpy(h.d_ghost_owner, ghost_owner, sizeof(int) * nghost, hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(h, e, "hipMemcpy(ghost map)");
+  h.ghost_n = nghost;
+  h.ghost_nlocal = nlocal;
+  return LK_OK;
+}
+
+int lk_pack_atoms(lk_handle *w, void *stream, const double *x, const int *type, int nall)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (nall < 0 || (nall > 0 && (!x || !type))) return fail(h, LK_ERR_ARGUMENT, "invalid atom arrays");
+  hipError_t e = lk::launch_pack_atoms(h, as_stream(stream), x, type, nall);
+  if (e != hipSuccess) return hip_fail(h, e, "pack_atoms");
+  return LK_OK;
+}
+
+int lk_pack_edges(lk_handle *w, void *stream, const double *x, const int *ilist,
+                  const int *numneigh, const int *neighbors, long nb_stride, int inum, int gnum,
+                  int maxneighs, int nlocal)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  const lk_contract &c = h.contract;
+  if (inum < 0 || gnum < 0 || nlocal < 0) return fail(h, LK_ERR_ARGUMENT, "invalid list sizes");
+  const bool multi_hop = c.n_hops > 1;
+  long rows = static_cast<long>(inum) + (multi_hop ? gnum : 0);
+  if (rows > c.max_atoms) rows = c.max_atoms;  // the collective capacity check errors this step
+  const int max_neighbors_per_atom = maxneighs > 1 ? maxneighs : 1;
+  if (rows * max_neighbors_per_atom > static_cast<long>(INT_MAX))
+    return fail(h, LK_ERR_CAPACITY,
+                "LAMMPS-JAX neighbor pack index overflows int; reduce the bundle max_atoms or the "
+                "neigh_modify one setting");
+  if (rows > 0 && (!x || !ilist || !numneigh || !neighbors))
+    return fail(h, LK_ERR_ARGUMENT, "invalid neighbor list arrays");
+  if (rows > 0 && nb_stride < 1) return fail(h, LK_ERR_ARGUMENT, "invalid neighbor stride");
+  if (int rc = ensure_bits(h, max_neighbors_per_atom)) return rc;
+  const bool half_edges = c.pairing != LK_PAIRING_FULL;
+  const bool full_list = !c.half_list;
+  // cpp/pair_jax_kokkos.cpp:850-867
+  const int duplicate = c.newton_pair && c.pair_sum && !c.edge_force && !multi_hop && !c.comm;
+  const int half_filter = half_edges && full_list;
+  const int unique = half_edges && c.comm && full_list;
+  hipError_t e = lk::launch_pack_edges(h, as_stream(stream), x, ilist, numneigh, neighbors,
+                                       nb_stride, static_cast<int>(rows), max_neighbors_per_atom,
+                                       nlocal, duplicate, half_filter, unique);
+  if (e != hipSuccess) return hip_fail(h, e, "pack_edges");
+  return LK_OK;
+}
+
+int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, double scale, double *f)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (h.model == 0) return fail(h, LK_ERR_STATE, "LAMMPS-JAX runtime is not initialized");
+  if (nlocal < 0 || nghost < 0 || !f) return fail(h, LK_ERR_ARGUMENT, "invalid compute arguments");
+  if (static_cast<long>(nlocal) + nghost > h.contract.max_atoms)
+    return fail(h, LK_ERR_CAPACITY, "LAMMPS-JAX atom capacity exceeded");
+  if (h.contract.pair_sum) return fail(h, LK_ERR_UNSUPPORTED, "pair-sum bundles carry no EAM/LJ model");
+  hipStream_t s = as_stream(stream);
+  hipError_t e = hipSuccess;
+  if (h.accum == LK_ACCUM_ONESIDED) {
+    if (h.model == 1) {
+      if (nghost > 0 && (h.ghost_n != nghost || h.ghost_nlocal != nlocal))
+        return fail(h, LK_ERR_STATE,
+                    "one-sided EAM needs the ghost map of this step (lk_set_ghost_map) for the F' "
+                    "forward exchange");
+      e = lk::launch_eam_onesided(h, s, nlocal, nghost, scale, f, flags);
+    } else {
+      e = lk::launch_lj_onesided(h, s, nlocal, nghost, scale, f, flags);
+    }
+  } else {
+    return fail(h, LK_ERR_UNSUPPORTED, "this accumulation scheme is not implemented yet");
+  }
+  if (e != hipSuccess) return hip_fail(h, e, "compute");
+  return LK_OK;
+}
+
+int lk_step_result(lk_handle *w, void *stream, lk_step_info *out)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  hipStream_t s = as_stream(stream);
+  hipError_t e = hipMemcpyAsync(h.h_result, h.d_result, sizeof(lk::StepResult), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(h, e, "step result");
+  for (const auto &p : h.pending) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, h.event_pool[p.a], h.event_pool[p.b]) == hipSuccess) {
+      auto &acc = h.stage_ms[p.name];
+      acc.first += ms;
+      acc.second += 1;
+    }
+  }
+  h.pending.clear();
+  const lk::StepResult &r = *h.h_result;
+  // cpp/pair_jax_kokkos.cpp:1080: the next pack resets the slots this step used
+  h.cached_edge_count = r.edge_count;
+  if (out) {
+    out->energy = r.energy;
+    for (int k = 0; k < 6; ++k) out->virial[k] = r.virial[k];
+    out->edge_count = r.edge_count;
+    out->edge_overflow = r.edge_overflow;
+  }
+  return LK_OK;
+}
+
+int lk_timing_enable(lk_handle *w, int on)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (on && h.event_pool.empty()) {
+    h.event_pool.resize(64);
+    for (auto &ev : h.event_pool) {
+      hipError_t e = hipEventCreate(&ev);
+      if (e != hipSuccess) return hip_fail(h, e, "hipEventCreate");
+    }
+  }
+  h.timing = on != 0;
+  h.pending.clear();
+  h.stage_ms.clear();
+  return LK_OK;
+}
+
+int lk_timing_read(lk_handle *w, int index, char *name, int name_len, double *total_ms,
+                   long *count)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (index < 0 || index >= static_cast<int>(h.stage_ms.size())) return LK_ERR_ARGUMENT;
+  auto it = h.stage_ms.begin();
+  std::advance(it, index);
+  if (name && name_len > 0) {
+    std::strncpy(name, it->first.c_str(), name_len - 1);
+    name[name_len - 1] = 0;
+  }
+  if (total_ms) *total_ms = it->second.first;
+  if (count) *count = it->second.second;
+  return LK_OK;
+}
+
+int lk_edge_buffers(lk_handle *w, int **senders, int **receivers, unsigned char **mask)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  if (senders) *senders = w->h.d_senders;
+  if (receivers) *receivers = w->h.d_receivers;
+  if (mask) *mask = w->h.d_mask;
+  return LK_OK;
+}
+
+int lk_staging_buffers(lk_handle *w, void **atoms, int **species)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  if (atoms) *atoms = w->h.d_atoms;
+  if (species) *species = w->h.d_species;
+  return LK_OK;
+}
+
+int lk_model_buffers(lk_handle *w, void **rho, void **fp)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  if (rho) *rho = w->h.d_rho;
+  if (fp) *fp = w->h.d_fp;
+  return LK_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,124 @@
+// Internal state of one handle (one pair_style jax/kk instance on one GPU) and the launchers the
+// C ABI dispatches to. Nothing here crosses the library boundary.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/lk_hip.h"
+
+namespace lk {
+
+// Device-side results of one step, drained to pinned host memory once per compute.
+struct StepResult {
+  double energy;       // scale * model energy
+  double virial[6];    // xx yy zz xy xz yz, already scaled
+  int edge_count;      // demand count of the last pack (may exceed max_edges)
+  int edge_overflow;   // 1 when the last pack exceeded max_edges
+  int ghost_sender;    // 1 when a packed edge starts on a ghost row
+  int pad;
+};
+
+struct Handle {
+  lk_contract contract{};
+  int accum = LK_ACCUM_PLAIN;
+  std::string error;
+  int device = 0;
+
+  // model
+  int model = 0;  // 0 none, 1 eam, 2 lj
+  // EAM tables at contract precision: r-tables node-major [nr][n_rtab][4], embedding [n_el][nrho][4]
+  void *d_rtab = nullptr;
+  void *d_etab = nullptr;
+  int n_el = 0, nrho = 0, nr = 0, n_rtab = 0;
+  double drho = 0, dr = 0, eam_cutoff = 0;
+  lk_lj_params lj{};
+
+  // staging (cpp/pair_jax_kokkos.cpp:355-398): atom records and 0-based species
+  void *d_atoms = nullptr;  // Atom4<S>[max_atoms]
+  int *d_species = nullptr;
+  // packed edges: the bundle ABI arrays plus the row-tile layout metadata
+  int *d_senders = nullptr;
+  int *d_receivers = nullptr;
+  unsigned char *d_mask = nullptr;
+  int *d_row_count = nullptr;   // [max_atoms] edges per list row
+  int *d_row_atom = nullptr;    // [max_atoms] atom of each list row (-1 past max_atoms)
+  int *d_tile_count = nullptr;  // [tiles + 1]
+  int *d_tile_off = nullptr;    // [tiles + 1]
+  uint32_t *d_bits = nullptr;   // validity bits, word w of row ii at [w * max_atoms + ii]
+  int bits_words = 0;
+  int packed_rows = 0;          // list rows of the last pack
+  long cached_edge_count = 0;   // host copy of the previous demand count (cpp:1080)
+  int pack_serial = 0;
+
+  // per-atom model state
+  void *d_fp = nullptr;      // F'(rho) [max_atoms]
+  void *d_rho = nullptr;     // rho [max_atoms]
+  // block partials: energy and virial, reduced in a fixed order
+  double *d_partials = nullptr;
+  int partial_slots = 0;
+  StepResult *d_result = nullptr;
+  StepResult *h_result = nullptr;  // pinned
+
+  // single-rank comm description (ghost -> owner), uploaded by lk_set_ghost_map
+  int *d_ghost_owner = nullptr;
+  int ghost_cap = 0;
+  int ghost_n = 0;
+  int ghost_nlocal = 0;
+
+  // stage timing (lk_timing_enable): event pairs recorded around each launch, read back at
+  // lk_step_result; names follow the reference's Kokkos labels (LAMMPSJAX::pack_neighbors, ...)
+  bool timing = false;
+  std::vector<hipEvent_t> event_pool;
+  struct Pending {
+    const char *name;
+    int a, b;
+  };
+  std::vector<Pending> pending;
+  std::map<std::string, std::pair<double, long>> stage_ms;
+
+  size_t scalar_bytes() const { return contract.precision == LK_FLOAT64 ? 8 : 4; }
+};
+
+// Records a start event on construction and a stop event on destruction when timing is on.
+class StageTimer {
+ public:
+  StageTimer(Handle &h, hipStream_t s, const char *name) : h_(h), s_(s), name_(name)
+  {
+    if (!h_.timing) return;
+    const int n = static_cast<int>(h_.pending.size()) * 2;
+    if (n + 2 > static_cast<int>(h_.event_pool.size())) return;
+    a_ = n;
+    (void)hipEventRecord(h_.event_pool[a_], s_);
+  }
+  ~StageTimer()
+  {
+    if (a_ < 0) return;
+    (void)hipEventRecord(h_.event_pool[a_ + 1], s_);
+    h_.pending.push_back({name_, a_, a_ + 1});
+  }
+
+ private:
+  Handle &h_;
+  hipStream_t s_;
+  const char *name_;
+  int a_ = -1;
+};
+
+// launchers (stream-ordered, no host synchronisation)
+hipError_t launch_pack_atoms(Handle &h, hipStream_t s, const double *x, const int *type, int nall);
+hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const int *ilist,
+                             const int *numneigh, const int *neighbors, long stride, int num_rows,
+                             int maxneighs, int nlocal, int duplicate, int half_edges,
+                             int unique_boundary);
+hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
+                               double *f, int flags);
+hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
+                              double *f, int flags);
+hipError_t launch_finalize(Handle &h, hipStream_t s, int nblocks, double scale, int flags);
+
+}  // namespace lk

@@ -1,0 +1,154 @@
+// LJ 12-6 energy and gradient on gfx950 (reference arithmetic: examples/export_model.py:16-50).
+// One sweep over the row tiles of the pack (see lk_pack.hip): one lane per list row, each row's
+// energy and force accumulated in registers.
+
+#include "lk_device.h"
+#include "lk_internal.h"
+
+namespace lk {
+
+template <typename S>
+struct LjArgs {
+  const Atom4<S> *atoms;
+  const int *row_count;
+  const int *row_atom;
+  const int *tile_off;
+  const int *receivers;
+  int num_rows;
+  int max_edges;
+  S cutsq;
+  S sigsq;
+  S four_eps;
+  S edge_scale;
+  double *partials;
+  int nlocal;
+  double scale;
+  double *f;
+};
+
+// One-sided full list: the row atom takes the whole pair force 2 * de/d(r^2) * (x_j - x_i) and
+// edge_energy_scale * e per edge; the pair virial takes half of -2 de/d(r^2) d (x) d per edge.
+template <typename S, bool VIRIAL>
+__global__ __launch_bounds__(256) void k_lj_rows(LjArgs<S> a)
+{
+  const int lane = threadIdx.x & (kWave - 1);
+  const int tile = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  if (tile * kWave >= a.num_rows) return;
+  const int ii = tile * kWave + lane;
+  const bool row = ii < a.num_rows;
+  const int i = row ? a.row_atom[ii] : -1;
+  const int cnt = i >= 0 ? a.row_count[ii] : 0;
+  Atom4<S> ai = {S(0), S(0), S(0), S(0)};
+  if (i >= 0) ai = a.atoms[i];
+  const long base = a.tile_off[tile];
+  const S tiny = static_cast<S>(1.0e-12);
+  S en = S(0), fx = S(0), fy = S(0), fz = S(0);
+  double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
+  long cursor = 0;
+  for (int k = 0;; ++k) {
+    const bool active = k < cnt;
+    const uint64_t M = wave_ballot(active);
+    if (M == 0) break;
+    const long e = base + cursor + lanes_below(M);
+    cursor += __popcll(M);
+    if (!active || e >= a.max_edges) continue;
+    const int j = a.receivers[e];
+    const Atom4<S> aj = a.atoms[j];
+    S dx, dy, dz, r2;
+    {
+#pragma clang fp contract(off)
+      dx = aj.x - ai.x;
+      dy = aj.y - ai.y;
+      dz = aj.z - ai.z;
+      r2 = dx * dx + dy * dy + dz * dz;
+    }
+    if (!(r2 > tiny && r2 < a.cutsq)) continue;  // export_model.py:22
+    const S inv_r2 = a.sigsq / r2;
+    const S inv_r6 = inv_r2 * inv_r2 * inv_r2;
+    en += a.edge_scale * (a.four_eps * (inv_r6 * inv_r6 - inv_r6));
+    // de/d(r^2) = -4 eps (6 u^6 - 3 u^3) / r^2 with u^3 = inv_r6
+    const S dedr2 = -a.four_eps * (S(6) * inv_r6 * inv_r6 - S(3) * inv_r6) / r2;
+    const S coef = S(2) * dedr2;
+    fx += coef * dx;
+    fy += coef * dy;
+    fz += coef * dz;
+    if (VIRIAL) {
+      const double c = -0.5 * static_cast<double>(coef);
+      const double ddx = dx, ddy = dy, ddz = dz;
+      w0 += c * ddx * ddx;
+      w1 += c * ddy * ddy;
+      w2 += c * ddz * ddz;
+      w3 += c * ddx * ddy;
+      w4 += c * ddx * ddz;
+      w5 += c * ddy * ddz;
+    }
+  }
+  double e_own = 0.0;
+  if (i >= 0 && i < a.nlocal) {
+    e_own = static_cast<double>(en);
+    double *fi = a.f + 3L * i;
+    fi[0] += a.scale * static_cast<double>(fx);
+    fi[1] += a.scale * static_cast<double>(fy);
+    fi[2] += a.scale * static_cast<double>(fz);
+  }
+  const double esum = wave_sum(e_own);
+  if (VIRIAL) {
+    w0 = wave_sum(w0);
+    w1 = wave_sum(w1);
+    w2 = wave_sum(w2);
+    w3 = wave_sum(w3);
+    w4 = wave_sum(w4);
+    w5 = wave_sum(w5);
+  }
+  if (lane == 0) {
+    double *p = a.partials + 8L * tile;
+    p[0] = esum;
+    p[1] = w0;
+    p[2] = w1;
+    p[3] = w2;
+    p[4] = w3;
+    p[5] = w4;
+    p[6] = w5;
+  }
+}
+
+template <typename S>
+static hipError_t lj_onesided(Handle &h, hipStream_t s, int nlocal, double scale, double *f,
+                              int flags)
+{
+  LjArgs<S> a;
+  a.atoms = static_cast<const Atom4<S> *>(h.d_atoms);
+  a.row_count = h.d_row_count;
+  a.row_atom = h.d_row_atom;
+  a.tile_off = h.d_tile_off;
+  a.receivers = h.d_receivers;
+  a.num_rows = h.packed_rows;
+  a.max_edges = h.contract.max_edges;
+  a.cutsq = static_cast<S>(h.lj.cutoff * h.lj.cutoff);
+  a.sigsq = static_cast<S>(h.lj.sigma * h.lj.sigma);
+  a.four_eps = static_cast<S>(4.0 * h.lj.epsilon);
+  a.edge_scale = static_cast<S>(h.lj.edge_energy_scale);
+  a.partials = h.d_partials;
+  a.nlocal = nlocal;
+  a.scale = scale;
+  a.f = f;
+  const int ntiles = (h.packed_rows + kWave - 1) / kWave;
+  const int blocks = (ntiles + 3) / 4;
+  if (ntiles > 0) {
+    StageTimer timer(h, s, "lj_rows");
+    if (flags & LK_VIRIAL)
+      hipLaunchKernelGGL((k_lj_rows<S, true>), dim3(blocks), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((k_lj_rows<S, false>), dim3(blocks), dim3(256), 0, s, a);
+  }
+  return launch_finalize(h, s, ntiles, scale, flags);
+}
+
+hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int /*nghost*/, double scale,
+                              double *f, int flags)
+{
+  if (h.contract.precision == LK_FLOAT64) return lj_onesided<double>(h, s, nlocal, scale, f, flags);
+  return lj_onesided<float>(h, s, nlocal, scale, f, flags);
+}
+
+}  // namespace lk

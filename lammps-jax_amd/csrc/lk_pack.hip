@@ -1,0 +1,332 @@
+// Neighbour-list packing on gfx950: cutoff filter + stream compaction of the LAMMPS Kokkos list
+// into the bundle's sender/receiver/mask arrays (reference: cpp/pair_jax_kokkos.cpp:54-118,
+// 157-173, 811-874), and the atom staging copy (cpp:35-52, 794-809).
+//
+// Layout of the packed edges ("row tiles"). The list is LayoutLeft (atom-fastest), so a wave
+// reads it coalesced only with one lane per row. A wave therefore owns a tile of 64 consecutive
+// list rows. Within a tile the edges are ordered by their ordinal k among the row's kept
+// entries, then by row: at step k every row with more than k kept entries writes one edge, and
+// the wave's writes land contiguously (ballot + mbcnt compaction). Tiles follow each other in
+// row order, so the packed range [0, count) has no holes. The order is deterministic; the
+// reference's atomic counter gives an arbitrary order, and the two agree after canonical sort.
+//
+// Three launches: count (filter, per-row counts, validity bits), a scan of the tile totals, and
+// the compacted write; then the tail reset of slots the previous step used.
+
+#include "lk_device.h"
+#include "lk_internal.h"
+
+namespace lk {
+
+// PackAtomsFunctor (cpp/pair_jax_kokkos.cpp:35-52): positions narrowed to the contract precision,
+// species = type - 1. The record keeps the species beside the position for one-gather lookups.
+template <typename S>
+__global__ __launch_bounds__(256) void k_pack_atoms(const double *__restrict__ x,
+                                                     const int *__restrict__ type, int span,
+                                                     Atom4<S> *__restrict__ atoms,
+                                                     int *__restrict__ species)
+{
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= span) return;
+  const int sp = type[i] - 1;
+  Atom4<S> a;
+  a.x = static_cast<S>(x[3L * i + 0]);
+  a.y = static_cast<S>(x[3L * i + 1]);
+  a.z = static_cast<S>(x[3L * i + 2]);
+  a.w = static_cast<S>(sp);
+  atoms[i] = a;
+  species[i] = sp;
+}
+
+struct PackArgs {
+  const double *x;
+  const int *ilist;
+  const int *numneigh;
+  const int *neighbors;
+  long stride;
+  int num_rows;
+  int maxneighs;
+  int max_atoms;
+  int max_edges;
+  int nlocal;
+  double cutsq;
+  int duplicate;        // duplicate_reverse_edges (cpp:850-852)
+  int half_edges;       // half_edges && full_list (cpp:863)
+  int unique_boundary;  // half_edges && comm && full_list (cpp:864-865)
+  int words;            // validity words per row
+  int pitch;            // row pitch of the bits array (max_atoms)
+  uint32_t *bits;
+  int *row_count;
+  int *row_atom;
+  int *tile_count;
+  int *tile_flags;
+};
+
+// The filter chain of PackNeighborFunctor::operator() (cpp:84-101) for list entry (i, jj).
+// r^2 is formed without FMA contraction, in double, from the engine's x, so the keep/drop
+// decision at r^2 == rc^2 matches the reference bit for bit.
+__device__ __forceinline__ bool keep_entry(const PackArgs &a, int i, double xi0, double xi1,
+                                           double xi2, int j)
+{
+#pragma clang fp contract(off)
+  if (j >= a.max_atoms) return false;
+  const double xj0 = a.x[3L * j + 0];
+  const double xj1 = a.x[3L * j + 1];
+  const double xj2 = a.x[3L * j + 2];
+  const double dx = xi0 - xj0;
+  const double dy = xi1 - xj1;
+  const double dz = xi2 - xj2;
+  const double rsq = dx * dx + dy * dy + dz * dz;
+  if (rsq > a.cutsq) return false;
+  if (a.half_edges && j < i) return false;
+  if (a.unique_boundary && j >= a.nlocal) {
+    if (xj2 < xi2) return false;
+    if (xj2 == xi2) {
+      if (xj1 < xi1) return false;
+      if (xj1 == xi1 && xj0 < xi0) return false;
+    }
+  }
+  return true;
+}
+
+// Pass 1: one lane per list row; walks the row's list slots in order, keeps the validity bits
+// (LayoutLeft words, coalesced) and the row's kept count; lane 0 stores the tile total.
+__global__ __launch_bounds__(256) void k_pack_count(PackArgs a)
+{
+  const int lane = threadIdx.x & (kWave - 1);
+  const int tile = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int ii = tile * kWave + lane;
+  const bool row = ii < a.num_rows;
+  int i = -1;
+  int nn = 0;
+  if (row) {
+    i = a.ilist[ii];
+    if (i < a.max_atoms) {
+      nn = min(a.numneigh[i], a.maxneighs);
+    } else {
+      i = -1;  // cpp:84: rows past max_atoms pack nothing
+    }
+  }
+  double xi0 = 0.0, xi1 = 0.0, xi2 = 0.0;
+  if (i >= 0) {
+    xi0 = a.x[3L * i + 0];
+    xi1 = a.x[3L * i + 1];
+    xi2 = a.x[3L * i + 2];
+  }
+  const int nn_max = wave_max_int(nn);
+  int cnt = 0;
+  uint32_t word = 0;
+  for (int jj = 0; jj < nn_max; ++jj) {
+    bool keep = false;
+    if (jj < nn) {
+      const int j = a.neighbors[static_cast<long>(jj) * a.stride + i] & kNeighMask;
+      keep = keep_entry(a, i, xi0, xi1, xi2, j);
+    }
+    if (keep) {
+      word |= 1u << (jj & 31);
+      ++cnt;
+    }
+    if ((jj & 31) == 31) {
+      if (row) a.bits[static_cast<long>(jj >> 5) * a.pitch + ii] = word;
+      word = 0;
+    }
+  }
+  if ((nn_max & 31) != 0 && row) a.bits[static_cast<long>(nn_max >> 5) * a.pitch + ii] = word;
+  if (row) {
+    a.row_count[ii] = cnt;
+    a.row_atom[ii] = i;
+  }
+  const int edges = cnt * (a.duplicate ? 2 : 1);
+  const int total = wave_sum(edges);
+  const bool ghost_row = i >= a.nlocal && cnt > 0;
+  const uint64_t gmask = wave_ballot(ghost_row);
+  if (lane == 0 && tile * kWave < a.num_rows) {
+    a.tile_count[tile] = total;
+    a.tile_flags[tile] = gmask != 0 ? 1 : 0;
+  }
+}
+
+// Pass 2: exclusive scan of the tile totals in one block, in a fixed order. Writes the tile
+// offsets, the demand count and overflow flag (cpp:103-108 semantics: overflow when the count
+// exceeds max_edges), and whether any kept edge starts on a ghost row.
+__global__ __launch_bounds__(1024) void k_tile_scan(const int *__restrict__ tile_count,
+                                                     const int *__restrict__ tile_flags,
+                                                     int ntiles, int max_edges,
+                                                     int *__restrict__ tile_off,
+                                                     StepResult *__restrict__ result)
+{
+  __shared__ long part[1024];
+  __shared__ int flag_any;
+  const int t = threadIdx.x;
+  if (t == 0) flag_any = 0;
+  const int per = (ntiles + blockDim.x - 1) / blockDim.x;
+  const int lo = min(t * per, ntiles);
+  const int hi = min(lo + per, ntiles);
+  long sum = 0;
+  int flags = 0;
+  for (int k = lo; k < hi; ++k) {
+    sum += tile_count[k];
+    flags |= tile_flags[k];
+  }
+  part[t] = sum;
+  __syncthreads();
+  if (flags) atomicOr(&flag_any, 1);
+  // Hillis-Steele inclusive scan over the per-thread sums
+  for (int off = 1; off < static_cast<int>(blockDim.x); off <<= 1) {
+    const long v = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  long run = part[t] - sum;  // exclusive prefix of this thread's range
+  for (int k = lo; k < hi; ++k) {
+    tile_off[k] = static_cast<int>(run);
+    run += tile_count[k];
+  }
+  if (t == static_cast<int>(blockDim.x) - 1) {
+    const long total = part[t];
+    tile_off[ntiles] = static_cast<int>(total);
+    result->edge_count = static_cast<int>(total);
+    result->edge_overflow = total > max_edges ? 1 : 0;
+  }
+  __syncthreads();
+  if (t == 0) result->ghost_sender = flag_any;
+}
+
+// Pass 3: compacted write. All lanes of the wave advance the kept-entry ordinal k together; the
+// rows with more than k kept entries form the ballot M and write M's popcount consecutive edges.
+__global__ __launch_bounds__(256) void k_pack_write(PackArgs a, const int *__restrict__ tile_off,
+                                                    int *__restrict__ senders,
+                                                    int *__restrict__ receivers,
+                                                    unsigned char *__restrict__ mask)
+{
+  const int lane = threadIdx.x & (kWave - 1);
+  const int tile = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const int ii = tile * kWave + lane;
+  if (tile * kWave >= a.num_rows) return;  // whole wave past the rows
+  const bool row = ii < a.num_rows;
+  const int cnt = row ? a.row_count[ii] : 0;
+  const int i = row ? a.row_atom[ii] : -1;
+  const int mult = a.duplicate ? 2 : 1;
+  const long base = tile_off[tile];
+  int w = 0;
+  uint32_t word = cnt > 0 ? a.bits[ii] : 0u;
+  long cursor = 0;
+  for (int k = 0;; ++k) {
+    const bool active = k < cnt;
+    const uint64_t M = wave_ballot(active);
+    if (M == 0) break;
+    if (active) {
+      while (word == 0) {
+        ++w;
+        word = a.bits[static_cast<long>(w) * a.pitch + ii];
+      }
+      const int b = __builtin_ctz(word);
+      word &= word - 1u;
+      const int jj = w * 32 + b;
+      const int j = a.neighbors[static_cast<long>(jj) * a.stride + i] & kNeighMask;
+      const long e = base + (cursor + lanes_below(M)) * mult;
+      if (e + mult <= a.max_edges) {
+        senders[e] = i;
+        receivers[e] = j;
+        mask[e] = 1;
+        if (mult == 2) {
+          senders[e + 1] = j;
+          receivers[e + 1] = i;
+          mask[e + 1] = 1;
+        }
+      }
+    }
+    cursor += __popcll(M);
+  }
+}
+
+// ResetEdgeTailFunctor (cpp:157-173): slots past the new count that held last step's edges
+// return to the padding (max_atoms, max_atoms, false).
+__global__ __launch_bounds__(256) void k_tail_reset(const StepResult *__restrict__ result,
+                                                    long span, int max_atoms,
+                                                    int *__restrict__ senders,
+                                                    int *__restrict__ receivers,
+                                                    unsigned char *__restrict__ mask)
+{
+  const long e = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= span) return;
+  if (e < result->edge_count) return;
+  senders[e] = max_atoms;
+  receivers[e] = max_atoms;
+  mask[e] = 0;
+}
+
+hipError_t launch_pack_atoms(Handle &h, hipStream_t s, const double *x, const int *type, int nall)
+{
+  const int span = nall < h.contract.max_atoms ? nall : h.contract.max_atoms;
+  if (span <= 0) return hipSuccess;
+  const int blocks = (span + 255) / 256;
+  StageTimer timer(h, s, "pack_atoms");
+  if (h.contract.precision == LK_FLOAT64)
+    hipLaunchKernelGGL(k_pack_atoms<double>, dim3(blocks), dim3(256), 0, s, x, type, span,
+                       static_cast<Atom4<double> *>(h.d_atoms), h.d_species);
+  else
+    hipLaunchKernelGGL(k_pack_atoms<float>, dim3(blocks), dim3(256), 0, s, x, type, span,
+                       static_cast<Atom4<float> *>(h.d_atoms), h.d_species);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const int *ilist,
+                             const int *numneigh, const int *neighbors, long stride, int num_rows,
+                             int maxneighs, int nlocal, int duplicate, int half_edges,
+                             int unique_boundary)
+{
+  PackArgs a;
+  a.x = x;
+  a.ilist = ilist;
+  a.numneigh = numneigh;
+  a.neighbors = neighbors;
+  a.stride = stride;
+  a.num_rows = num_rows;
+  a.maxneighs = maxneighs;
+  a.max_atoms = h.contract.max_atoms;
+  a.max_edges = h.contract.max_edges;
+  a.nlocal = nlocal;
+  a.cutsq = h.contract.cutoff * h.contract.cutoff;
+  a.duplicate = duplicate;
+  a.half_edges = half_edges;
+  a.unique_boundary = unique_boundary;
+  a.words = h.bits_words;
+  a.pitch = h.contract.max_atoms;
+  a.bits = h.d_bits;
+  a.row_count = h.d_row_count;
+  a.row_atom = h.d_row_atom;
+  a.tile_count = h.d_tile_count;
+  a.tile_flags = h.d_tile_count + (h.contract.max_atoms / kWave + 2);
+  const int ntiles = (num_rows + kWave - 1) / kWave;
+  h.packed_rows = num_rows;
+  if (ntiles > 0) {
+    const int blocks = (ntiles + 3) / 4;
+    StageTimer timer(h, s, "pack_count");
+    hipLaunchKernelGGL(k_pack_count, dim3(blocks), dim3(256), 0, s, a);
+  }
+  {
+    StageTimer timer(h, s, "tile_scan");
+    hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(1024), 0, s, h.d_tile_count, a.tile_flags,
+                       ntiles, h.contract.max_edges, h.d_tile_off, h.d_result);
+  }
+  if (ntiles > 0) {
+    const int blocks = (ntiles + 3) / 4;
+    StageTimer timer(h, s, "pack_write");
+    hipLaunchKernelGGL(k_pack_write, dim3(blocks), dim3(256), 0, s, a, h.d_tile_off, h.d_senders,
+                       h.d_receivers, h.d_mask);
+  }
+  const long span = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
+                                                                 : h.contract.max_edges;
+  if (span > 0) {
+    const long blocks = (span + 255) / 256;
+    StageTimer timer(h, s, "tail_reset");
+    hipLaunchKernelGGL(k_tail_reset, dim3(blocks), dim3(256), 0, s, h.d_result, span,
+                       h.contract.max_atoms, h.d_senders, h.d_receivers, h.d_mask);
+  }
+  ++h.pack_serial;
+  return hipGetLastError();
+}
+
+}  // namespace lk

@@ -1,0 +1,133 @@
+"""Single-rank LAMMPS stand-in (liblkharness.so): periodic ghosts and Kokkos-layout lists.
+
+It plays the engine's part of PairJaxKokkos::compute (cpp/pair_jax_kokkos.cpp:1005-1024):
+owned atoms first, then ghost images within the communication cutoff; ilist, numneigh and the
+LayoutLeft neighbour matrix. It is the caller of the hot path, not part of it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().with_name("liblkharness.so")
+
+LIST_FULL = 0
+LIST_HALF = 1
+LIST_FULL_GHOST = 2
+
+_lib = None
+
+
+def _load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is not built; run `python lammps-jax_amd/build.py`")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    vp, ip, dp, lp = ctypes.c_void_p, ctypes.c_int, ctypes.c_double, ctypes.c_long
+    lib.lkh_create.argtypes = [ip, vp, vp, vp, dp, ctypes.c_char_p, ip]
+    lib.lkh_create.restype = vp
+    lib.lkh_destroy.argtypes = [vp]
+    for name in ("lkh_nlocal", "lkh_nghost", "lkh_inum", "lkh_gnum", "lkh_maxneighs"):
+        getattr(lib, name).argtypes = [vp]
+        getattr(lib, name).restype = ip
+    for name in ("lkh_stride", "lkh_list_entries"):
+        getattr(lib, name).argtypes = [vp]
+        getattr(lib, name).restype = lp
+    for name in ("lkh_x",):
+        getattr(lib, name).argtypes = [vp]
+        getattr(lib, name).restype = ctypes.POINTER(ctypes.c_double)
+    for name in ("lkh_type", "lkh_ghost_owner", "lkh_ghost_shift", "lkh_ghost_offsets",
+                 "lkh_ghost_list", "lkh_ilist", "lkh_numneigh", "lkh_neighbors"):
+        getattr(lib, name).argtypes = [vp]
+        getattr(lib, name).restype = ctypes.POINTER(ctypes.c_int)
+    lib.lkh_update_ghosts.argtypes = [vp, vp]
+    lib.lkh_update_ghosts.restype = None
+    lib.lkh_build_list.argtypes = [vp, dp, ip, ip]
+    lib.lkh_build_list.restype = ip
+    lib.lkh_error.argtypes = [vp]
+    lib.lkh_error.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def _copy(ptr, n, dtype) -> np.ndarray:
+    if n == 0:
+        return np.zeros(0, dtype=dtype)
+    return np.ctypeslib.as_array(ptr, shape=(n,)).astype(dtype, copy=True)
+
+
+class System:
+    """Owned atoms in a periodic box [0, box) plus their ghost images."""
+
+    def __init__(self, x: np.ndarray, types: np.ndarray, box, cutghost: float):
+        lib = _load()
+        x = np.ascontiguousarray(x, dtype=np.float64)
+        types = np.ascontiguousarray(types, dtype=np.int32)
+        box = np.ascontiguousarray(box, dtype=np.float64)
+        if x.ndim != 2 or x.shape[1] != 3 or len(types) != len(x):
+            raise ValueError("x must be [n, 3] with one type per atom")
+        err = ctypes.create_string_buffer(256)
+        self._h = lib.lkh_create(len(x), x.ctypes.data, types.ctypes.data, box.ctypes.data,
+                                 float(cutghost), err, 256)
+        if not self._h:
+            raise ValueError(err.value.decode())
+        self.box = box.copy()
+        self.cutghost = float(cutghost)
+        self.nlocal = lib.lkh_nlocal(self._h)
+        self.nghost = lib.lkh_nghost(self._h)
+        self._refresh_atoms()
+        self.list = None
+
+    def _refresh_atoms(self) -> None:
+        lib = _load()
+        nall = self.nlocal + self.nghost
+        self.x = _copy(lib.lkh_x(self._h), 3 * nall, np.float64).reshape(nall, 3)
+        self.type = _copy(lib.lkh_type(self._h), nall, np.int32)
+        self.ghost_owner = _copy(lib.lkh_ghost_owner(self._h), self.nghost, np.int32)
+        self.ghost_shift = _copy(lib.lkh_ghost_shift(self._h), 3 * self.nghost, np.int32).reshape(-1, 3)
+
+    @property
+    def nall(self) -> int:
+        return self.nlocal + self.nghost
+
+    def update_ghosts(self, x_owned: np.ndarray) -> None:
+        """Forward comm of positions: ghosts follow their owners with the image shift."""
+        lib = _load()
+        x_owned = np.ascontiguousarray(x_owned, dtype=np.float64)
+        lib.lkh_update_ghosts(self._h, x_owned.ctypes.data)
+        nall = self.nall
+        self.x = _copy(lib.lkh_x(self._h), 3 * nall, np.float64).reshape(nall, 3)
+
+    def build_list(self, cutneigh: float, kind: int = LIST_FULL, stride_align: int = 64) -> dict:
+        """Binned neighbour list; returns ilist, numneigh, LayoutLeft neighbors and sizes."""
+        lib = _load()
+        if lib.lkh_build_list(self._h, float(cutneigh), int(kind), int(stride_align)) != 0:
+            raise ValueError(lib.lkh_error(self._h).decode())
+        inum, gnum = lib.lkh_inum(self._h), lib.lkh_gnum(self._h)
+        maxneighs = lib.lkh_maxneighs(self._h)
+        stride = lib.lkh_stride(self._h)
+        rows = inum + gnum
+        self.list = dict(
+            ilist=_copy(lib.lkh_ilist(self._h), rows, np.int32),
+            numneigh=_copy(lib.lkh_numneigh(self._h), self.nall, np.int32),
+            neighbors=_copy(lib.lkh_neighbors(self._h), stride * maxneighs, np.int32),
+            inum=inum, gnum=gnum, maxneighs=maxneighs, stride=int(stride),
+            entries=int(lib.lkh_list_entries(self._h)), cutneigh=float(cutneigh), kind=int(kind),
+        )
+        return self.list
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            _load().lkh_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
