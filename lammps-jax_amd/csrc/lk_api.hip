@@ -50,7 +50,7 @@ __global__ void k_fill_int(int *p, long n, int v)
 
 void free_all(Handle &h)
 {
-  void *ptrs[] = {h.d_rtab,      h.d_etab,      h.d_atoms,       h.d_species,   h.d_senders,
+  void *ptrs[] = {h.d_ltab,      h.d_rtab,      h.d_etab,      h.d_atoms,       h.d_species,   h.d_senders,
                   h.d_receivers, h.d_mask,      h.d_row_count,   h.d_row_atom,  h.d_tile_count,
                   h.d_tile_off,  h.d_bits,      h.d_fp,          h.d_rho,       h.d_partials,
                   h.d_result,    h.d_ghost_owner};
@@ -146,6 +146,8 @@ int lk_create(const lk_contract *c, lk_handle **out)
 
   hipError_t e = hipGetDevice(&h.device);
   if (e != hipSuccess) return hip_fail(h, e, "hipGetDevice");
+  e = hipDeviceGetAttribute(&h.num_cus, hipDeviceAttributeMultiprocessorCount, h.device);
+  if (e != hipSuccess) return hip_fail(h, e, "hipDeviceGetAttribute");
   const size_t A = static_cast<size_t>(c->max_atoms);
   const size_t E = static_cast<size_t>(c->max_edges);
   const size_t S = h.scalar_bytes();
@@ -227,6 +229,23 @@ int lk_set_eam(lk_handle *w, const lk_eam_tables *t)
     if (e == hipSuccess) e = hipMemcpy(h.d_etab, ef.data(), ef.size() * 4, hipMemcpyHostToDevice);
   }
   if (e != hipSuccess) return hip_fail(h, e, "hipMemcpy(tables)");
+  // LDS source entries, 16 bytes per (node, table): float64 keeps (f, d) = (c0, c1) of the node
+  // (the kernels rebuild c2, c3 from nodes m and m+1 exactly as the host did); float32 keeps the
+  // four narrowed coefficients.
+  const size_t nent = static_cast<size_t>(t->nr) * n_rtab;
+  if ((e = hipMalloc(&h.d_ltab, nent * 16)) != hipSuccess) return hip_fail(h, e, "hipMalloc(ltab)");
+  if (S == 8) {
+    std::vector<double> l(nent * 2);
+    for (size_t q = 0; q < nent; ++q) {
+      l[2 * q + 0] = r[4 * q + 0];
+      l[2 * q + 1] = r[4 * q + 1];
+    }
+    e = hipMemcpy(h.d_ltab, l.data(), nent * 16, hipMemcpyHostToDevice);
+  } else {
+    std::vector<float> l(r.begin(), r.end());
+    e = hipMemcpy(h.d_ltab, l.data(), nent * 16, hipMemcpyHostToDevice);
+  }
+  if (e != hipSuccess) return hip_fail(h, e, "hipMemcpy(ltab)");
   h.n_el = n_el;
   h.nrho = t->nrho;
   h.nr = t->nr;

@@ -68,6 +68,41 @@ __device__ __forceinline__ Locator<S> locate(S x, S delta, int n)
   return L;
 }
 
+// Interval and fraction with a multiply by 1/delta (per-edge lookups; the division's result can
+// differ in the last bit, which moves t by one ulp at most).
+template <typename S>
+__device__ __forceinline__ Locator<S> locate_mul(S x, S inv_delta, int n)
+{
+  Locator<S> L;
+  const S idx = x * inv_delta;
+  S fl = floor(idx);
+  fl = fl >= S(0) ? fl : S(0);
+  fl = fl <= S(n - 2) ? fl : S(n - 2);
+  L.node = static_cast<int>(fl);
+  L.t_raw = idx - static_cast<S>(L.node);
+  L.t = L.t_raw < S(1) ? L.t_raw : S(1);
+  return L;
+}
+
+// 1/sqrt(x), x > 0: the hardware estimate refined by Newton-Raphson steps
+// y <- y + y (1 - x y^2) / 2 (two in float64, one in float32), about one ulp.
+__device__ __forceinline__ double rsqrt_nr(double x)
+{
+  double y = __builtin_amdgcn_rsq(x);
+  double e = fma(-(x * y), y, 1.0);
+  y = fma(0.5 * y, e, y);
+  e = fma(-(x * y), y, 1.0);
+  y = fma(0.5 * y, e, y);
+  return y;
+}
+
+__device__ __forceinline__ float rsqrt_nr(float x)
+{
+  float y = __builtin_amdgcn_rsqf(x);
+  const float e = fmaf(-(x * y), y, 1.0f);
+  return fmaf(0.5f * y, e, y);
+}
+
 template <typename S>
 __device__ __forceinline__ S cubic_value(const S *c, S t)
 {

@@ -1,19 +1,50 @@
 // EAM/alloy energy and gradient on gfx950 (reference arithmetic: python/lammps_jax/eam.py:115-333,
 // the one-sided full-list scheme of python/lammps_jax/eam_pallas.py:181-249).
 //
-// Both sweeps walk the row tiles written by the pack (lk_pack.hip): one lane per list row, the
-// wave advancing the kept-entry ordinal k together, so the receivers of step k are read as one
-// contiguous run. A row's sums stay in its lane's registers: no float atomics, no cross-lane
-// reductions per edge, and a fixed summation order (bitwise reproducible runs).
+// Both sweeps walk the row tiles written by the pack (lk_pack.hip, lk_tile.h): one lane per list
+// row, the waves of a tile advancing the kept-entry ordinal k together, so the receivers of one
+// step are read as one contiguous run. A row's sums stay in registers and meet across waves in
+// LDS in a fixed order: no float atomics, bitwise reproducible runs.
 //
-// r-tables are node-major: rtab[node][table][4] with the n_el density tables first and the
-// pair (r*phi) tables after them, so every lookup of one edge (same r, same node) touches one
-// 32*n_rtab-byte record.
+// Spline tables live in LDS. Each (node, table) entry is 16 bytes: in float64 the node's value
+// and slope (f, d) = (c0, c1), from which c2 and c3 are rebuilt with nodes m and m+1 exactly as
+// PairEAM::interpolate computes them on the host (eam.py:130-134, no contraction), so the
+// coefficients are bit-identical to the host table; in float32 the four narrowed coefficients.
+// The LDS window holds the top nodes of the r-grid (short distances below it read the float64
+// rows from global memory). Blocks are persistent: they fill LDS once and then take groups of
+// tiles, XCD by XCD.
+//
+// Density sweep: rho over the row's edges (one table per edge), then F(rho) and F'(rho).
+// Force sweep:   F'_i rho'_j + F'_j rho'_i + phi', the pair energy phi/2 and the pair virial.
+
+#include <type_traits>
 
 #include "lk_device.h"
 #include "lk_internal.h"
+#include "lk_tile.h"
 
 namespace lk {
+
+template <typename S>
+using LdsEntry = std::conditional_t<sizeof(S) == 8, double2, float4>;
+
+template <typename S>
+struct Coef {
+  S c0, c1, c2, c3;
+};
+
+// Rebuilds one interval's coefficients from the (f, d) entries of nodes m and m+1.
+__device__ __forceinline__ Coef<double> coef_from(double2 e0, double2 e1)
+{
+#pragma clang fp contract(off)
+  const double step = e1.x - e0.x;
+  Coef<double> c;
+  c.c0 = e0.x;
+  c.c1 = e0.y;
+  c.c2 = 3.0 * step - 2.0 * e0.y - e1.y;
+  c.c3 = e0.y + e1.y - 2.0 * step;
+  return c;
+}
 
 template <typename S>
 struct EamArgs {
@@ -24,7 +55,8 @@ struct EamArgs {
   const int *receivers;
   int num_rows;
   int max_edges;
-  const S *rtab;
+  const S *rtab;                 // global rows [nr][n_rtab][4]
+  const LdsEntry<S> *ltab;       // LDS source [nr][n_rtab]
   int n_rtab;
   int n_el;
   int nr;
@@ -37,7 +69,7 @@ struct EamArgs {
   S inv_drho;
   S *fp;
   S *rho;
-  double *partials;  // [tiles][8]: 0 energy, 1..6 virial
+  double *partials;  // [tiles][8]: 0 embedding energy, 1..6 virial, 7 pair energy
   int nlocal;
   double scale;
   double *f;
@@ -46,6 +78,61 @@ struct EamArgs {
 // Species index into the tables. XLA clamps out-of-range gathers, so types past the table's
 // elements read its last element (the reference warns at pair_coeff, cpp:602-606).
 __device__ __forceinline__ int clamp_species(int z, int n_el) { return z < 0 ? 0 : (z >= n_el ? n_el - 1 : z); }
+
+// LDS table window: tables [0, T) of the nodes [lo, nr).
+template <typename S>
+struct Window {
+  const LdsEntry<S> *lds;
+  int T;   // tables per node held in LDS
+  int lo;  // first node in LDS
+};
+
+// Copies the window into LDS (all threads of the block) and returns it.
+template <typename S>
+__device__ __forceinline__ Window<S> fill_window(LdsEntry<S> *lds, int cap_entries,
+                                                 const EamArgs<S> &a, int T)
+{
+  Window<S> w;
+  w.lds = lds;
+  w.T = T;
+  const int cap_nodes = cap_entries / T;
+  w.lo = a.nr > cap_nodes ? a.nr - cap_nodes : 0;
+  const int n = (a.nr - w.lo) * T;
+  for (int q = threadIdx.x; q < n; q += blockDim.x) {
+    const int node = w.lo + q / T;
+    lds[q] = a.ltab[static_cast<long>(node) * a.n_rtab + (q % T)];
+  }
+  __syncthreads();
+  return w;
+}
+
+template <typename S>
+__device__ __forceinline__ Coef<S> rcoef(const Window<S> &w, const EamArgs<S> &a, int m, int tab)
+{
+  if (m >= w.lo) {
+    const int q = (m - w.lo) * w.T + tab;
+    if constexpr (sizeof(S) == 8) {
+      return coef_from(w.lds[q], w.lds[q + w.T]);
+    } else {
+      const float4 e = w.lds[q];
+      return Coef<S>{e.x, e.y, e.z, e.w};
+    }
+  }
+  const S *c = a.rtab + (static_cast<long>(m) * a.n_rtab + tab) * 4;
+  return Coef<S>{c[0], c[1], c[2], c[3]};
+}
+
+template <typename S>
+__device__ __forceinline__ S cvalue(const Coef<S> &c, S t)
+{
+  return c.c0 + t * (c.c1 + t * (c.c2 + t * c.c3));
+}
+
+template <typename S>
+__device__ __forceinline__ S cslope_t(const Coef<S> &c, S t)
+{
+  return c.c1 + t * (S(2) * c.c2 + t * (S(3) * c.c3));
+}
 
 // Embedding value and slope at rho, extrapolating linearly past the table (eam.py:155-164).
 template <typename S>
@@ -58,58 +145,103 @@ __device__ __forceinline__ void embed(const EamArgs<S> &a, int z, S rho, S &F, S
   Fp = (L.t_raw > S(1) ? end_slope : cubic_slope_t(c, L.t)) * a.inv_drho;
 }
 
-// Sweep 1 (one-sided): rho_i and the halved pair energy over the row's own edges, then the
-// embedding F(rho_i) and F'(rho_i). Owned rows add their energy to the tile partial.
-template <typename S>
-__global__ __launch_bounds__(256) void k_eam_density_rows(EamArgs<S> a)
+// Persistent walk over tile groups (TPB consecutive tiles per group), XCD by XCD. The loop count
+// is the same for every thread of a block (barriers inside stay matched); tiles past the rows
+// come out empty.
+struct GroupWalk {
+  int g, g_end, step;
+};
+
+__device__ __forceinline__ GroupWalk group_walk(int ngroups)
 {
+  const int nbx = gridDim.x / kXcds;              // blocks per XCD
+  const int xcd = blockIdx.x % kXcds;
+  const int local = blockIdx.x / kXcds;
+  const int per = (ngroups + kXcds - 1) / kXcds;  // groups per XCD
+  GroupWalk w;
+  w.g = xcd * per + local;
+  w.g_end = min((xcd + 1) * per, ngroups);
+  w.step = nbx;
+  return w;
+}
+
+inline int persistent_grid(int ngroups, int blocks_per_cu, int num_cus)
+{
+  int want = ngroups;
+  const int cap = blocks_per_cu * (num_cus > 0 ? num_cus : 256);
+  if (want > cap) want = cap;
+  return ((want + kXcds - 1) / kXcds) * kXcds;
+}
+
+constexpr int kDensW = 4, kDensTPB = 4, kDensLds = 4096;     // 64 KB table window
+constexpr int kForceW = 4, kForceTPB = 4, kForceLds = 7680;  // 120 KB table window
+
+// Density sweep (one-sided): rho_i over the row's own edges, then F(rho_i), F'(rho_i). Owned rows
+// add F(rho_i) to the tile's energy partial.
+template <typename S, int W, int TPB>
+__global__ __launch_bounds__(W * TPB * 64) void k_eam_density_rows(EamArgs<S> a, int ngroups)
+{
+  __shared__ LdsEntry<S> lds[kDensLds];
+  __shared__ S part[TPB][W][kWave];
+  const Window<S> win = fill_window<S>(lds, kDensLds, a, a.n_el);
+  const int sub = threadIdx.x / (W * kWave);
+  const int wave = (threadIdx.x / kWave) % W;
   const int lane = threadIdx.x & (kWave - 1);
-  const int tile = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
-  if (tile * kWave >= a.num_rows) return;
-  const int ii = tile * kWave + lane;
-  const bool row = ii < a.num_rows;
-  const int i = row ? a.row_atom[ii] : -1;
-  const int cnt = i >= 0 ? a.row_count[ii] : 0;
-  Atom4<S> ai = {S(0), S(0), S(0), S(0)};
-  if (i >= 0) ai = a.atoms[i];
-  const int zi = clamp_species(static_cast<int>(ai.w), a.n_el);
-  const long base = a.tile_off[tile];
-  S rho = S(0), epair = S(0);
-  long cursor = 0;
-  for (int k = 0;; ++k) {
-    const bool active = k < cnt;
-    const uint64_t M = wave_ballot(active);
-    if (M == 0) break;
-    const long e = base + cursor + lanes_below(M);
-    cursor += __popcll(M);
-    if (!active || e >= a.max_edges) continue;
-    const int j = a.receivers[e];
-    const Atom4<S> aj = a.atoms[j];
-    S r2;
-    {
+  for (GroupWalk gw = group_walk(ngroups); gw.g < gw.g_end; gw.g += gw.step) {
+    const int tile = gw.g * TPB + sub;
+    const int ii = tile * kWave + lane;
+    const bool row = ii < a.num_rows;
+    const int i = row ? a.row_atom[ii] : -1;
+    const int cnt = i >= 0 ? a.row_count[ii] : 0;
+    Atom4<S> ai = {S(0), S(0), S(0), S(0)};
+    if (i >= 0) ai = a.atoms[i];
+    const long base = tile * kWave < a.num_rows ? a.tile_off[tile] : 0;
+    S rho = S(0);
+    struct Rec {
+      Atom4<S> at;
+      bool valid;
+    };
+    for_tile_edges_pipelined<W, Rec>(
+        cnt, base, wave, a.max_edges, a.receivers,
+        [&](int j) {
+          Rec r;
+          r.valid = j >= 0;
+          if (r.valid) r.at = a.atoms[j];
+          return r;
+        },
+        [&](const Rec &r) {
+          if (!r.valid) return;
+          S r2;
+          {
 #pragma clang fp contract(off)
-      const S dx = aj.x - ai.x, dy = aj.y - ai.y, dz = aj.z - ai.z;
-      r2 = dx * dx + dy * dy + dz * dz;
+            const S dx = r.at.x - ai.x, dy = r.at.y - ai.y, dz = r.at.z - ai.z;
+            r2 = dx * dx + dy * dy + dz * dz;
+          }
+          if (!(r2 < a.cutsq)) return;  // valid = mask & r_sq < cutoff_sq (eam.py:288)
+          const S rr = r2 * rsqrt_nr(r2);
+          const Locator<S> L = locate_mul(rr, a.inv_dr, a.nr);
+          const int zj = clamp_species(static_cast<int>(r.at.w), a.n_el);
+          rho += cvalue(rcoef(win, a, L.node, zj), L.t);
+        });
+    part[sub][wave][lane] = rho;
+    __syncthreads();
+    if (wave == 0) {
+      rho = part[sub][0][lane];
+#pragma unroll
+      for (int w = 1; w < W; ++w) rho += part[sub][w][lane];
+      double e_own = 0.0;
+      if (i >= 0) {
+        S F, Fp;
+        embed(a, clamp_species(static_cast<int>(ai.w), a.n_el), rho, F, Fp);
+        a.fp[i] = Fp;
+        if (a.rho) a.rho[i] = rho;
+        if (i < a.nlocal) e_own = static_cast<double>(F);
+      }
+      const double esum = wave_sum(e_own);
+      if (lane == 0 && tile * kWave < a.num_rows) a.partials[8L * tile + 0] = esum;
     }
-    if (!(r2 < a.cutsq)) continue;  // valid = mask & r_sq < cutoff_sq (eam.py:288)
-    const S r = sqrt(r2);
-    const Locator<S> L = locate(r, a.dr, a.nr);
-    const S *rec = a.rtab + static_cast<long>(L.node) * a.n_rtab * 4;
-    const int zj = clamp_species(static_cast<int>(aj.w), a.n_el);
-    rho += cubic_value(rec + 4 * zj, L.t);
-    const S z2 = cubic_value(rec + 4 * (a.n_el + pair_row(zi, zj)), L.t);
-    epair += S(0.5) * z2 / r;
+    __syncthreads();
   }
-  double e_own = 0.0;
-  if (i >= 0) {
-    S F, Fp;
-    embed(a, zi, rho, F, Fp);
-    a.fp[i] = Fp;
-    if (a.rho) a.rho[i] = rho;
-    if (i < a.nlocal) e_own = static_cast<double>(epair + F);
-  }
-  const double esum = wave_sum(e_own);
-  if (lane == 0) a.partials[8L * tile + 0] = esum;
 }
 
 // Forward comm stand-in: ghost rows read their owner's F' (LAMMPS forward_comm on one rank).
@@ -123,104 +255,148 @@ __global__ __launch_bounds__(256) void k_forward_rows(S *__restrict__ v,
   v[nlocal + g] = v[owner[g]];
 }
 
-// Sweep 2 (one-sided): the row atom's whole force, psip/r * (x_j - x_i) per edge with
-// psip = F'_i rho'_j(r) + F'_j rho'_i(r) + phi'(r) (eam.py:385-398), added into the engine's f.
-// The pair virial takes half of -psip/r * d (x) d per directed edge of the full list.
-template <typename S, bool VIRIAL>
-__global__ __launch_bounds__(256) void k_eam_force_rows(EamArgs<S> a)
+// Force sweep (one-sided): the row atom's whole force, psip/r * (x_j - x_i) per edge with
+// psip = F'_i rho'_j(r) + F'_j rho'_i(r) + phi'(r) (eam.py:385-398), added into the engine's f;
+// half the pair energy phi(r)/2 per directed edge (eam.py:300-307); the pair virial takes half of
+// -psip/r * d (x) d per directed edge of the full list.
+template <typename S, int W, int TPB, bool VIRIAL>
+__global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, int ngroups)
 {
+  __shared__ LdsEntry<S> lds[kForceLds];
+  __shared__ S part[4][TPB][W][kWave];
+  __shared__ double vir[TPB][6][W];
+  const Window<S> win = fill_window<S>(lds, kForceLds, a, a.n_rtab);
+  const int sub = threadIdx.x / (W * kWave);
+  const int wave = (threadIdx.x / kWave) % W;
   const int lane = threadIdx.x & (kWave - 1);
-  const int tile = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
-  if (tile * kWave >= a.num_rows) return;
-  const int ii = tile * kWave + lane;
-  const bool row = ii < a.num_rows;
-  const int i = row ? a.row_atom[ii] : -1;
-  const int cnt = i >= 0 ? a.row_count[ii] : 0;
-  Atom4<S> ai = {S(0), S(0), S(0), S(0)};
-  S fpi = S(0);
-  if (i >= 0) {
-    ai = a.atoms[i];
-    fpi = a.fp[i];
-  }
-  const int zi = clamp_species(static_cast<int>(ai.w), a.n_el);
-  const long base = a.tile_off[tile];
-  S fx = S(0), fy = S(0), fz = S(0);
-  double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
-  long cursor = 0;
-  for (int k = 0;; ++k) {
-    const bool active = k < cnt;
-    const uint64_t M = wave_ballot(active);
-    if (M == 0) break;
-    const long e = base + cursor + lanes_below(M);
-    cursor += __popcll(M);
-    if (!active || e >= a.max_edges) continue;
-    const int j = a.receivers[e];
-    const Atom4<S> aj = a.atoms[j];
-    const S fpj = a.fp[j];
-    S dx, dy, dz, r2;
-    {
+  for (GroupWalk gw = group_walk(ngroups); gw.g < gw.g_end; gw.g += gw.step) {
+    const int tile = gw.g * TPB + sub;
+    const int ii = tile * kWave + lane;
+    const bool row = ii < a.num_rows;
+    const int i = row ? a.row_atom[ii] : -1;
+    const int cnt = i >= 0 ? a.row_count[ii] : 0;
+    Atom4<S> ai = {S(0), S(0), S(0), S(0)};
+    S fpi = S(0);
+    if (i >= 0) {
+      ai = a.atoms[i];
+      fpi = a.fp[i];
+    }
+    const int zi = clamp_species(static_cast<int>(ai.w), a.n_el);
+    const long base = tile * kWave < a.num_rows ? a.tile_off[tile] : 0;
+    S fx = S(0), fy = S(0), fz = S(0), ep = S(0);
+    double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
+    struct Rec {
+      Atom4<S> at;
+      S fp;
+      bool valid;
+    };
+    for_tile_edges_pipelined<W, Rec>(
+        cnt, base, wave, a.max_edges, a.receivers,
+        [&](int j) {
+          Rec r;
+          r.valid = j >= 0;
+          if (r.valid) {
+            r.at = a.atoms[j];
+            r.fp = a.fp[j];
+          }
+          return r;
+        },
+        [&](const Rec &r) {
+          if (!r.valid) return;
+          S dx, dy, dz, r2;
+          {
 #pragma clang fp contract(off)
-      dx = aj.x - ai.x;
-      dy = aj.y - ai.y;
-      dz = aj.z - ai.z;
-      r2 = dx * dx + dy * dy + dz * dz;
-    }
-    if (!(r2 < a.cutsq)) continue;
-    const S r = sqrt(r2);
-    const Locator<S> L = locate(r, a.dr, a.nr);
-    const S *rec = a.rtab + static_cast<long>(L.node) * a.n_rtab * 4;
-    const int zj = clamp_species(static_cast<int>(aj.w), a.n_el);
-    const S *cj = rec + 4 * zj;
-    const S *ci = rec + 4 * zi;
-    const S *cp = rec + 4 * (a.n_el + pair_row(zi, zj));
-    // Past the table the non-extrapolated lookups saturate: autodiff slope 0 (eam.py:150).
-    const bool inside = !(L.t_raw > S(1));
-    const S rhojp = inside ? cubic_slope_t(cj, L.t) * a.inv_dr : S(0);
-    const S rhoip = inside ? cubic_slope_t(ci, L.t) * a.inv_dr : S(0);
-    const S z2 = cubic_value(cp, L.t);
-    const S z2p = inside ? cubic_slope_t(cp, L.t) * a.inv_dr : S(0);
-    const S rinv = S(1) / r;
-    const S phi = z2 * rinv;
-    const S phip = (z2p - phi) * rinv;
-    const S psip = fpi * rhojp + fpj * rhoip + phip;
-    const S coef = psip * rinv;
-    fx += coef * dx;
-    fy += coef * dy;
-    fz += coef * dz;
+            dx = r.at.x - ai.x;
+            dy = r.at.y - ai.y;
+            dz = r.at.z - ai.z;
+            r2 = dx * dx + dy * dy + dz * dz;
+          }
+          if (!(r2 < a.cutsq)) return;
+          const S rinv = rsqrt_nr(r2);
+          const S rr = r2 * rinv;
+          const Locator<S> L = locate_mul(rr, a.inv_dr, a.nr);
+          const int zj = clamp_species(static_cast<int>(r.at.w), a.n_el);
+          const Coef<S> cj = rcoef(win, a, L.node, zj);
+          const Coef<S> ci = rcoef(win, a, L.node, zi);
+          const Coef<S> cp = rcoef(win, a, L.node, a.n_el + pair_row(zi, zj));
+          // Past the table the non-extrapolated lookups saturate: autodiff slope 0 (eam.py:150).
+          const bool inside = !(L.t_raw > S(1));
+          const S rhojp = inside ? cslope_t(cj, L.t) * a.inv_dr : S(0);
+          const S rhoip = inside ? cslope_t(ci, L.t) * a.inv_dr : S(0);
+          const S z2 = cvalue(cp, L.t);
+          const S z2p = inside ? cslope_t(cp, L.t) * a.inv_dr : S(0);
+          const S phi = z2 * rinv;
+          const S phip = (z2p - phi) * rinv;
+          const S psip = fpi * rhojp + r.fp * rhoip + phip;
+          const S coef = psip * rinv;
+          ep += S(0.5) * phi;
+          fx += coef * dx;
+          fy += coef * dy;
+          fz += coef * dz;
+          if (VIRIAL) {
+            const double c = -0.5 * static_cast<double>(coef);
+            const double ddx = dx, ddy = dy, ddz = dz;
+            w0 += c * ddx * ddx;
+            w1 += c * ddy * ddy;
+            w2 += c * ddz * ddz;
+            w3 += c * ddx * ddy;
+            w4 += c * ddx * ddz;
+            w5 += c * ddy * ddz;
+          }
+        });
+    part[0][sub][wave][lane] = fx;
+    part[1][sub][wave][lane] = fy;
+    part[2][sub][wave][lane] = fz;
+    part[3][sub][wave][lane] = ep;
     if (VIRIAL) {
-      const double c = -0.5 * static_cast<double>(coef);
-      const double ddx = dx, ddy = dy, ddz = dz;
-      w0 += c * ddx * ddx;
-      w1 += c * ddy * ddy;
-      w2 += c * ddz * ddz;
-      w3 += c * ddx * ddy;
-      w4 += c * ddx * ddz;
-      w5 += c * ddy * ddz;
+      w0 = wave_sum(w0);
+      w1 = wave_sum(w1);
+      w2 = wave_sum(w2);
+      w3 = wave_sum(w3);
+      w4 = wave_sum(w4);
+      w5 = wave_sum(w5);
+      if (lane == 0) {
+        vir[sub][0][wave] = w0;
+        vir[sub][1][wave] = w1;
+        vir[sub][2][wave] = w2;
+        vir[sub][3][wave] = w3;
+        vir[sub][4][wave] = w4;
+        vir[sub][5][wave] = w5;
+      }
     }
-  }
-  if (i >= 0 && i < a.nlocal) {
-    // AddForcesFunctor (cpp:175-192) fused: f(i) += scale * F(i); only owned rows carry force.
-    double *fi = a.f + 3L * i;
-    fi[0] += a.scale * static_cast<double>(fx);
-    fi[1] += a.scale * static_cast<double>(fy);
-    fi[2] += a.scale * static_cast<double>(fz);
-  }
-  if (VIRIAL) {
-    w0 = wave_sum(w0);
-    w1 = wave_sum(w1);
-    w2 = wave_sum(w2);
-    w3 = wave_sum(w3);
-    w4 = wave_sum(w4);
-    w5 = wave_sum(w5);
-    if (lane == 0) {
-      double *p = a.partials + 8L * tile;
-      p[1] = w0;
-      p[2] = w1;
-      p[3] = w2;
-      p[4] = w3;
-      p[5] = w4;
-      p[6] = w5;
+    __syncthreads();
+    if (wave == 0) {
+      fx = part[0][sub][0][lane];
+      fy = part[1][sub][0][lane];
+      fz = part[2][sub][0][lane];
+      ep = part[3][sub][0][lane];
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        fx += part[0][sub][w][lane];
+        fy += part[1][sub][w][lane];
+        fz += part[2][sub][w][lane];
+        ep += part[3][sub][w][lane];
+      }
+      double e_own = 0.0;
+      if (i >= 0 && i < a.nlocal) {
+        // AddForcesFunctor (cpp:175-192) fused: f(i) += scale * F(i); owned rows only.
+        double *fi = a.f + 3L * i;
+        fi[0] += a.scale * static_cast<double>(fx);
+        fi[1] += a.scale * static_cast<double>(fy);
+        fi[2] += a.scale * static_cast<double>(fz);
+        e_own = static_cast<double>(ep);
+      }
+      const double esum = wave_sum(e_own);
+      if (tile * kWave < a.num_rows) {
+        if (lane == 0) a.partials[8L * tile + 7] = esum;
+        if (VIRIAL && lane < 6) {
+          double v = vir[sub][lane][0];
+          for (int w = 1; w < W; ++w) v += vir[sub][lane][w];
+          a.partials[8L * tile + 1 + lane] = v;
+        }
+      }
     }
+    __syncthreads();
   }
 }
 
@@ -232,8 +408,10 @@ __global__ __launch_bounds__(256) void k_finalize(const double *__restrict__ par
   __shared__ double red[7][256];
   const int t = threadIdx.x;
   double acc[7] = {0, 0, 0, 0, 0, 0, 0};
-  for (int k = t; k < ntiles; k += blockDim.x)
-    for (int c = 0; c < 7; ++c) acc[c] += partials[8L * k + c];
+  for (int k = t; k < ntiles; k += blockDim.x) {
+    acc[0] += partials[8L * k + 0] + partials[8L * k + 7];
+    for (int c = 1; c < 7; ++c) acc[c] += partials[8L * k + c];
+  }
   for (int c = 0; c < 7; ++c) red[c][t] = acc[c];
   __syncthreads();
   for (int off = blockDim.x / 2; off >= 1; off >>= 1) {
@@ -259,6 +437,7 @@ static EamArgs<S> eam_args(Handle &h, int nlocal, double scale, double *f)
   a.num_rows = h.packed_rows;
   a.max_edges = h.contract.max_edges;
   a.rtab = static_cast<const S *>(h.d_rtab);
+  a.ltab = static_cast<const LdsEntry<S> *>(h.d_ltab);
   a.n_rtab = h.n_rtab;
   a.n_el = h.n_el;
   a.nr = h.nr;
@@ -284,10 +463,12 @@ static hipError_t eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
 {
   EamArgs<S> a = eam_args<S>(h, nlocal, scale, f);
   const int ntiles = (h.packed_rows + kWave - 1) / kWave;
-  const int blocks = (ntiles + 3) / 4;
   if (ntiles > 0) {
+    const int ngroups = (ntiles + kDensTPB - 1) / kDensTPB;
+    const int grid = persistent_grid(ngroups, 2, h.num_cus);
     StageTimer timer(h, s, "eam_density");
-    hipLaunchKernelGGL(k_eam_density_rows<S>, dim3(blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((k_eam_density_rows<S, kDensW, kDensTPB>), dim3(grid),
+                       dim3(kDensW * kDensTPB * kWave), 0, s, a, ngroups);
   }
   if (nghost > 0) {
     StageTimer timer(h, s, "forward_fp");
@@ -295,11 +476,15 @@ static hipError_t eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
                        static_cast<S *>(h.d_fp), h.d_ghost_owner, nlocal, nghost);
   }
   if (ntiles > 0) {
+    const int ngroups = (ntiles + kForceTPB - 1) / kForceTPB;
+    const int grid = persistent_grid(ngroups, 1, h.num_cus);
     StageTimer timer(h, s, "eam_force");
     if (flags & LK_VIRIAL)
-      hipLaunchKernelGGL((k_eam_force_rows<S, true>), dim3(blocks), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((k_eam_force_rows<S, kForceW, kForceTPB, true>), dim3(grid),
+                         dim3(kForceW * kForceTPB * kWave), 0, s, a, ngroups);
     else
-      hipLaunchKernelGGL((k_eam_force_rows<S, false>), dim3(blocks), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((k_eam_force_rows<S, kForceW, kForceTPB, false>), dim3(grid),
+                         dim3(kForceW * kForceTPB * kWave), 0, s, a, ngroups);
   }
   return launch_finalize(h, s, ntiles, scale, flags);
 }

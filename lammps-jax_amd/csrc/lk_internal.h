@@ -34,6 +34,8 @@ struct Handle {
   // EAM tables at contract precision: r-tables node-major [nr][n_rtab][4], embedding [n_el][nrho][4]
   void *d_rtab = nullptr;
   void *d_etab = nullptr;
+  void *d_ltab = nullptr;  // LDS source: [nr][n_rtab] 16-byte entries, see lk_eam.hip
+  int num_cus = 0;
   int n_el = 0, nrho = 0, nr = 0, n_rtab = 0;
   double drho = 0, dr = 0, eam_cutoff = 0;
   lk_lj_params lj{};

@@ -4,6 +4,7 @@
 
 #include "lk_device.h"
 #include "lk_internal.h"
+#include "lk_tile.h"
 
 namespace lk {
 
@@ -28,12 +29,15 @@ struct LjArgs {
 
 // One-sided full list: the row atom takes the whole pair force 2 * de/d(r^2) * (x_j - x_i) and
 // edge_energy_scale * e per edge; the pair virial takes half of -2 de/d(r^2) d (x) d per edge.
-template <typename S, bool VIRIAL>
-__global__ __launch_bounds__(256) void k_lj_rows(LjArgs<S> a)
+template <typename S, int W, bool VIRIAL>
+__global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
 {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int tile = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  __shared__ S part[4][W][kWave];
+  __shared__ double vir[6][W];
+  const int tile = tile_of_block();
   if (tile * kWave >= a.num_rows) return;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
   const int ii = tile * kWave + lane;
   const bool row = ii < a.num_rows;
   const int i = row ? a.row_atom[ii] : -1;
@@ -44,14 +48,7 @@ __global__ __launch_bounds__(256) void k_lj_rows(LjArgs<S> a)
   const S tiny = static_cast<S>(1.0e-12);
   S en = S(0), fx = S(0), fy = S(0), fz = S(0);
   double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
-  long cursor = 0;
-  for (int k = 0;; ++k) {
-    const bool active = k < cnt;
-    const uint64_t M = wave_ballot(active);
-    if (M == 0) break;
-    const long e = base + cursor + lanes_below(M);
-    cursor += __popcll(M);
-    if (!active || e >= a.max_edges) continue;
+  for_tile_edges<W>(cnt, base, wave, a.max_edges, [&](long e) {
     const int j = a.receivers[e];
     const Atom4<S> aj = a.atoms[j];
     S dx, dy, dz, r2;
@@ -62,7 +59,7 @@ __global__ __launch_bounds__(256) void k_lj_rows(LjArgs<S> a)
       dz = aj.z - ai.z;
       r2 = dx * dx + dy * dy + dz * dz;
     }
-    if (!(r2 > tiny && r2 < a.cutsq)) continue;  // export_model.py:22
+    if (!(r2 > tiny && r2 < a.cutsq)) return;  // export_model.py:22
     const S inv_r2 = a.sigsq / r2;
     const S inv_r6 = inv_r2 * inv_r2 * inv_r2;
     en += a.edge_scale * (a.four_eps * (inv_r6 * inv_r6 - inv_r6));
@@ -82,6 +79,39 @@ __global__ __launch_bounds__(256) void k_lj_rows(LjArgs<S> a)
       w4 += c * ddx * ddz;
       w5 += c * ddy * ddz;
     }
+  });
+  part[0][wave][lane] = en;
+  part[1][wave][lane] = fx;
+  part[2][wave][lane] = fy;
+  part[3][wave][lane] = fz;
+  if (VIRIAL) {
+    w0 = wave_sum(w0);
+    w1 = wave_sum(w1);
+    w2 = wave_sum(w2);
+    w3 = wave_sum(w3);
+    w4 = wave_sum(w4);
+    w5 = wave_sum(w5);
+    if (lane == 0) {
+      vir[0][wave] = w0;
+      vir[1][wave] = w1;
+      vir[2][wave] = w2;
+      vir[3][wave] = w3;
+      vir[4][wave] = w4;
+      vir[5][wave] = w5;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  en = part[0][0][lane];
+  fx = part[1][0][lane];
+  fy = part[2][0][lane];
+  fz = part[3][0][lane];
+#pragma unroll
+  for (int w = 1; w < W; ++w) {
+    en += part[0][w][lane];
+    fx += part[1][w][lane];
+    fy += part[2][w][lane];
+    fz += part[3][w][lane];
   }
   double e_own = 0.0;
   if (i >= 0 && i < a.nlocal) {
@@ -92,23 +122,14 @@ __global__ __launch_bounds__(256) void k_lj_rows(LjArgs<S> a)
     fi[2] += a.scale * static_cast<double>(fz);
   }
   const double esum = wave_sum(e_own);
-  if (VIRIAL) {
-    w0 = wave_sum(w0);
-    w1 = wave_sum(w1);
-    w2 = wave_sum(w2);
-    w3 = wave_sum(w3);
-    w4 = wave_sum(w4);
-    w5 = wave_sum(w5);
-  }
   if (lane == 0) {
-    double *p = a.partials + 8L * tile;
-    p[0] = esum;
-    p[1] = w0;
-    p[2] = w1;
-    p[3] = w2;
-    p[4] = w3;
-    p[5] = w4;
-    p[6] = w5;
+    a.partials[8L * tile] = esum;
+    a.partials[8L * tile + 7] = 0.0;
+  }
+  if (VIRIAL && lane < 6) {
+    double v = vir[lane][0];
+    for (int w = 1; w < W; ++w) v += vir[lane][w];
+    a.partials[8L * tile + 1 + lane] = v;
   }
 }
 
@@ -132,14 +153,15 @@ static hipError_t lj_onesided(Handle &h, hipStream_t s, int nlocal, double scale
   a.nlocal = nlocal;
   a.scale = scale;
   a.f = f;
+  constexpr int W = 8;
   const int ntiles = (h.packed_rows + kWave - 1) / kWave;
-  const int blocks = (ntiles + 3) / 4;
+  const int grid = tile_grid(ntiles);
   if (ntiles > 0) {
     StageTimer timer(h, s, "lj_rows");
     if (flags & LK_VIRIAL)
-      hipLaunchKernelGGL((k_lj_rows<S, true>), dim3(blocks), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((k_lj_rows<S, W, true>), dim3(grid), dim3(W * kWave), 0, s, a);
     else
-      hipLaunchKernelGGL((k_lj_rows<S, false>), dim3(blocks), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((k_lj_rows<S, W, false>), dim3(grid), dim3(W * kWave), 0, s, a);
   }
   return launch_finalize(h, s, ntiles, scale, flags);
 }

@@ -15,6 +15,7 @@
 
 #include "lk_device.h"
 #include "lk_internal.h"
+#include "lk_tile.h"
 
 namespace lk {
 
@@ -89,12 +90,17 @@ __device__ __forceinline__ bool keep_entry(const PackArgs &a, int i, double xi0,
   return true;
 }
 
-// Pass 1: one lane per list row; walks the row's list slots in order, keeps the validity bits
-// (LayoutLeft words, coalesced) and the row's kept count; lane 0 stores the tile total.
-__global__ __launch_bounds__(256) void k_pack_count(PackArgs a)
+// Pass 1: one lane per list row, W waves per 64-row tile. Wave w takes the 32-slot words
+// w, w + W, ... of every row: it reads those list slots (coalesced across the rows), applies the
+// filter and stores the validity word (LayoutLeft words). The per-wave kept counts meet in LDS.
+template <int W>
+__global__ __launch_bounds__(W * 64) void k_pack_count(PackArgs a)
 {
+  __shared__ int part[W][kWave];
+  const int tile = tile_of_block();
+  if (tile * kWave >= a.num_rows) return;
+  const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int tile = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const int ii = tile * kWave + lane;
   const bool row = ii < a.num_rows;
   int i = -1;
@@ -114,24 +120,32 @@ __global__ __launch_bounds__(256) void k_pack_count(PackArgs a)
     xi2 = a.x[3L * i + 2];
   }
   const int nn_max = wave_max_int(nn);
+  const int nwords = (nn_max + 31) >> 5;
   int cnt = 0;
-  uint32_t word = 0;
-  for (int jj = 0; jj < nn_max; ++jj) {
-    bool keep = false;
-    if (jj < nn) {
-      const int j = a.neighbors[static_cast<long>(jj) * a.stride + i] & kNeighMask;
-      keep = keep_entry(a, i, xi0, xi1, xi2, j);
+  for (int w = wave; w < nwords; w += W) {
+    uint32_t word = 0;
+    const int jj0 = w * 32;
+    const int jj1 = min(jj0 + 32, nn_max);
+#pragma unroll 4
+    for (int jj = jj0; jj < jj1; ++jj) {
+      bool keep = false;
+      if (jj < nn) {
+        const int j = a.neighbors[static_cast<long>(jj) * a.stride + i] & kNeighMask;
+        keep = keep_entry(a, i, xi0, xi1, xi2, j);
+      }
+      if (keep) {
+        word |= 1u << (jj & 31);
+        ++cnt;
+      }
     }
-    if (keep) {
-      word |= 1u << (jj & 31);
-      ++cnt;
-    }
-    if ((jj & 31) == 31) {
-      if (row) a.bits[static_cast<long>(jj >> 5) * a.pitch + ii] = word;
-      word = 0;
-    }
+    if (row) a.bits[static_cast<long>(w) * a.pitch + ii] = word;
   }
-  if ((nn_max & 31) != 0 && row) a.bits[static_cast<long>(nn_max >> 5) * a.pitch + ii] = word;
+  part[wave][lane] = cnt;
+  __syncthreads();
+  if (wave != 0) return;
+  cnt = part[0][lane];
+#pragma unroll
+  for (int w = 1; w < W; ++w) cnt += part[w][lane];
   if (row) {
     a.row_count[ii] = cnt;
     a.row_atom[ii] = i;
@@ -140,7 +154,7 @@ __global__ __launch_bounds__(256) void k_pack_count(PackArgs a)
   const int total = wave_sum(edges);
   const bool ghost_row = i >= a.nlocal && cnt > 0;
   const uint64_t gmask = wave_ballot(ghost_row);
-  if (lane == 0 && tile * kWave < a.num_rows) {
+  if (lane == 0) {
     a.tile_count[tile] = total;
     a.tile_flags[tile] = gmask != 0 ? 1 : 0;
   }
@@ -193,17 +207,20 @@ __global__ __launch_bounds__(1024) void k_tile_scan(const int *__restrict__ tile
   if (t == 0) result->ghost_sender = flag_any;
 }
 
-// Pass 3: compacted write. All lanes of the wave advance the kept-entry ordinal k together; the
-// rows with more than k kept entries form the ballot M and write M's popcount consecutive edges.
-__global__ __launch_bounds__(256) void k_pack_write(PackArgs a, const int *__restrict__ tile_off,
-                                                    int *__restrict__ senders,
-                                                    int *__restrict__ receivers,
-                                                    unsigned char *__restrict__ mask)
+// Pass 3: compacted write, W waves per tile. Every wave walks the ordinals k in step (each lane
+// popping its row's validity bits in order); wave k % W writes ordinal k: the rows with more than
+// k kept entries form the ballot M and write M's popcount consecutive edges.
+template <int W>
+__global__ __launch_bounds__(W * 64) void k_pack_write(PackArgs a, const int *__restrict__ tile_off,
+                                                       int *__restrict__ senders,
+                                                       int *__restrict__ receivers,
+                                                       unsigned char *__restrict__ mask)
 {
+  const int tile = tile_of_block();
+  if (tile * kWave >= a.num_rows) return;
+  const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int tile = (blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const int ii = tile * kWave + lane;
-  if (tile * kWave >= a.num_rows) return;  // whole wave past the rows
   const bool row = ii < a.num_rows;
   const int cnt = row ? a.row_count[ii] : 0;
   const int i = row ? a.row_atom[ii] : -1;
@@ -223,17 +240,19 @@ __global__ __launch_bounds__(256) void k_pack_write(PackArgs a, const int *__res
       }
       const int b = __builtin_ctz(word);
       word &= word - 1u;
-      const int jj = w * 32 + b;
-      const int j = a.neighbors[static_cast<long>(jj) * a.stride + i] & kNeighMask;
-      const long e = base + (cursor + lanes_below(M)) * mult;
-      if (e + mult <= a.max_edges) {
-        senders[e] = i;
-        receivers[e] = j;
-        mask[e] = 1;
-        if (mult == 2) {
-          senders[e + 1] = j;
-          receivers[e + 1] = i;
-          mask[e + 1] = 1;
+      if ((k % W) == wave) {
+        const int jj = w * 32 + b;
+        const int j = a.neighbors[static_cast<long>(jj) * a.stride + i] & kNeighMask;
+        const long e = base + (cursor + lanes_below(M)) * mult;
+        if (e + mult <= a.max_edges) {
+          senders[e] = i;
+          receivers[e] = j;
+          mask[e] = 1;
+          if (mult == 2) {
+            senders[e + 1] = j;
+            receivers[e + 1] = i;
+            mask[e + 1] = 1;
+          }
         }
       }
     }
@@ -301,10 +320,11 @@ hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const in
   a.tile_flags = h.d_tile_count + (h.contract.max_atoms / kWave + 2);
   const int ntiles = (num_rows + kWave - 1) / kWave;
   h.packed_rows = num_rows;
+  constexpr int W = 4;
+  const int grid = tile_grid(ntiles);
   if (ntiles > 0) {
-    const int blocks = (ntiles + 3) / 4;
     StageTimer timer(h, s, "pack_count");
-    hipLaunchKernelGGL(k_pack_count, dim3(blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_pack_count<W>, dim3(grid), dim3(W * kWave), 0, s, a);
   }
   {
     StageTimer timer(h, s, "tile_scan");
@@ -312,10 +332,9 @@ hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const in
                        ntiles, h.contract.max_edges, h.d_tile_off, h.d_result);
   }
   if (ntiles > 0) {
-    const int blocks = (ntiles + 3) / 4;
     StageTimer timer(h, s, "pack_write");
-    hipLaunchKernelGGL(k_pack_write, dim3(blocks), dim3(256), 0, s, a, h.d_tile_off, h.d_senders,
-                       h.d_receivers, h.d_mask);
+    hipLaunchKernelGGL(k_pack_write<W>, dim3(grid), dim3(W * kWave), 0, s, a, h.d_tile_off,
+                       h.d_senders, h.d_receivers, h.d_mask);
   }
   const long span = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
                                                                  : h.contract.max_edges;
