@@ -161,6 +161,18 @@ int lk_pack_edges(lk_handle *h, void *stream, const double *x, const int *ilist,
 int lk_compute(lk_handle *h, void *stream, int nlocal, int nghost, int flags, double scale,
                double *f);
 
+/*
+ * One MD step's device work: lk_pack_atoms + lk_pack_edges + lk_compute with the same results.
+ * The one-sided scheme runs fused in three launches (the model reads the neighbour list where the
+ * pack reads it and never reads the packed arrays back); other schemes run the three in order.
+ * Replaces the pack/execute/add sequence of PairJaxKokkos::compute (cpp/pair_jax_kokkos.cpp:
+ * 1023-1100).
+ */
+int lk_pack_compute(lk_handle *h, void *stream, const double *x, const int *type, int nall,
+                    const int *ilist, const int *numneigh, const int *neighbors, long nb_stride,
+                    int inum, int gnum, int maxneighs, int nlocal, int nghost, int flags,
+                    double scale, double *f);
+
 /* Synchronises the stream and returns energy, virial and the pack counts of the last step. */
 int lk_step_result(lk_handle *h, void *stream, lk_step_info *out);
 

@@ -53,7 +53,7 @@ void free_all(Handle &h)
   void *ptrs[] = {h.d_ltab,      h.d_rtab,      h.d_etab,      h.d_atoms,       h.d_species,   h.d_senders,
                   h.d_receivers, h.d_mask,      h.d_row_count,   h.d_row_atom,  h.d_tile_count,
                   h.d_tile_off,  h.d_bits,      h.d_fp,          h.d_rho,       h.d_partials,
-                  h.d_result,    h.d_ghost_owner};
+                  h.d_result,    h.d_ghost_owner, h.d_ghost_off, h.d_ghost_list, h.d_done};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -165,6 +165,7 @@ int lk_create(const lk_contract *c, lk_handle **out)
   if ((e = hipMalloc(&h.d_rho, A * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(rho)");
   if ((e = dalloc(&h.d_partials, 8 * tiles)) != hipSuccess) return hip_fail(h, e, "hipMalloc(partials)");
   if ((e = dalloc(&h.d_result, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(result)");
+  if ((e = dalloc(&h.d_done, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(done)");
   if ((e = hipHostMalloc(reinterpret_cast<void **>(&h.h_result), sizeof(lk::StepResult))) != hipSuccess)
     return hip_fail(h, e, "hipHostMalloc(result)");
   std::memset(h.h_result, 0, sizeof(lk::StepResult));
@@ -179,6 +180,7 @@ int lk_create(const lk_contract *c, lk_handle **out)
   (void)hipMemset(h.d_rho, 0, A * S);
   (void)hipMemset(h.d_partials, 0, 8 * tiles * sizeof(double));
   (void)hipMemset(h.d_result, 0, sizeof(lk::StepResult));
+  (void)hipMemset(h.d_done, 0, sizeof(int));
   if (int rc = ensure_bits(h, 128)) return rc;
   e = hipDeviceSynchronize();
   if (e != hipSuccess) return hip_fail(h, e, "initialising buffers");
@@ -304,15 +306,40 @@ int lk_set_ghost_map(lk_handle *w, int nlocal, int nghost, const int *ghost_owne
     if (ghost_owner[g] < 0 || ghost_owner[g] >= nlocal)
       return fail(h, LK_ERR_ARGUMENT, "ghost owner outside the owned rows");
   hipError_t e;
-  if (nghost > h.ghost_cap) {
+  if (nghost > h.ghost_cap || !h.d_ghost_owner || !h.d_ghost_list) {
+    // the owner map and its inverse list share one capacity
     if (h.d_ghost_owner) (void)hipFree(h.d_ghost_owner);
+    if (h.d_ghost_list) (void)hipFree(h.d_ghost_list);
     h.d_ghost_owner = nullptr;
+    h.d_ghost_list = nullptr;
+    h.ghost_cap = 0;
     if ((e = dalloc(&h.d_ghost_owner, nghost)) != hipSuccess) return hip_fail(h, e, "hipMalloc(ghost map)");
+    if ((e = dalloc(&h.d_ghost_list, nghost)) != hipSuccess) return hip_fail(h, e, "hipMalloc(ghost list)");
     h.ghost_cap = nghost;
   }
   if (nghost > 0 &&
       (e = hipMemcpy(h.d_ghost_owner, ghost_owner, sizeof(int) * nghost, hipMemcpyHostToDevice)) != hipSuccess)
     return hip_fail(h, e, "hipMemcpy(ghost map)");
+  // inverse map: the ghost images of each owned row, in increasing ghost order
+  std::vector<int> off(static_cast<size_t>(nlocal) + 1, 0), lst(static_cast<size_t>(nghost));
+  for (int g = 0; g < nghost; ++g) off[ghost_owner[g] + 1]++;
+  for (int i = 0; i < nlocal; ++i) off[i + 1] += off[i];
+  {
+    std::vector<int> cur(off.begin(), off.end() - 1);
+    for (int g = 0; g < nghost; ++g) lst[cur[ghost_owner[g]]++] = nlocal + g;
+  }
+  if (nlocal + 1 > h.ghost_off_cap) {
+    if (h.d_ghost_off) (void)hipFree(h.d_ghost_off);
+    h.d_ghost_off = nullptr;
+    if ((e = dalloc(&h.d_ghost_off, static_cast<size_t>(nlocal) + 1)) != hipSuccess)
+      return hip_fail(h, e, "hipMalloc(ghost offsets)");
+    h.ghost_off_cap = nlocal + 1;
+  }
+  if ((e = hipMemcpy(h.d_ghost_off, off.data(), sizeof(int) * off.size(), hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(h, e, "hipMemcpy(ghost offsets)");
+  if (nghost > 0 &&
+      (e = hipMemcpy(h.d_ghost_list, lst.data(), sizeof(int) * nghost, hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(h, e, "hipMemcpy(ghost list)");
   h.ghost_n = nghost;
   h.ghost_nlocal = nlocal;
   return LK_OK;
@@ -386,6 +413,48 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
     return fail(h, LK_ERR_UNSUPPORTED, "this accumulation scheme is not implemented yet");
   }
   if (e != hipSuccess) return hip_fail(h, e, "compute");
+  return LK_OK;
+}
+
+int lk_pack_compute(lk_handle *w, void *stream, const double *x, const int *type, int nall,
+                    const int *ilist, const int *numneigh, const int *neighbors, long nb_stride,
+                    int inum, int gnum, int maxneighs, int nlocal, int nghost, int flags,
+                    double scale, double *f)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (h.model == 0) return fail(h, LK_ERR_STATE, "LAMMPS-JAX runtime is not initialized");
+  if (h.accum != LK_ACCUM_ONESIDED || h.contract.pair_sum) {
+    // schemes without a fused form run the three entry points in order
+    int rc = lk_pack_atoms(w, stream, x, type, nall);
+    if (rc == LK_OK) rc = lk_pack_edges(w, stream, x, ilist, numneigh, neighbors, nb_stride, inum,
+                                        gnum, maxneighs, nlocal);
+    if (rc == LK_OK) rc = lk_compute(w, stream, nlocal, nghost, flags, scale, f);
+    return rc;
+  }
+  const lk_contract &c = h.contract;
+  if (nall < 0 || nlocal < 0 || nghost < 0 || inum < 0 || gnum < 0 || !f)
+    return fail(h, LK_ERR_ARGUMENT, "invalid step arguments");
+  if (static_cast<long>(nlocal) + nghost > c.max_atoms)
+    return fail(h, LK_ERR_CAPACITY, "LAMMPS-JAX atom capacity exceeded");
+  long rows = static_cast<long>(inum) + (c.n_hops > 1 ? gnum : 0);
+  if (rows > c.max_atoms) rows = c.max_atoms;
+  const int max_neighbors_per_atom = maxneighs > 1 ? maxneighs : 1;
+  if (rows * max_neighbors_per_atom > static_cast<long>(INT_MAX))
+    return fail(h, LK_ERR_CAPACITY,
+                "LAMMPS-JAX neighbor pack index overflows int; reduce the bundle max_atoms or the "
+                "neigh_modify one setting");
+  if ((rows > 0 || nall > 0) && (!x || !type || !ilist || !numneigh || !neighbors))
+    return fail(h, LK_ERR_ARGUMENT, "invalid atom or neighbor list arrays");
+  if (h.model == 1 && nghost > 0 && (h.ghost_n != nghost || h.ghost_nlocal != nlocal))
+    return fail(h, LK_ERR_STATE,
+                "one-sided EAM needs the ghost map of this step (lk_set_ghost_map) for the F' "
+                "forward exchange");
+  if (int rc = ensure_bits(h, max_neighbors_per_atom)) return rc;
+  hipError_t e = lk::launch_step_onesided(h, as_stream(stream), x, type, nall, ilist, numneigh,
+                                          neighbors, nb_stride, static_cast<int>(rows),
+                                          max_neighbors_per_atom, nlocal, nghost, flags, scale, f);
+  if (e != hipSuccess) return hip_fail(h, e, "fused step");
   return LK_OK;
 }
 

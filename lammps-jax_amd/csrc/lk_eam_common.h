@@ -1,0 +1,196 @@
+// Pieces shared by the EAM kernels (lk_eam.hip, lk_step.hip): argument block, LDS-staged
+// spline tables, embedding lookup and the persistent XCD-grouped tile walk.
+#pragma once
+
+#include <type_traits>
+
+#include "lk_device.h"
+#include "lk_internal.h"
+#include "lk_tile.h"
+
+namespace lk {
+
+template <typename S>
+using LdsEntry = std::conditional_t<sizeof(S) == 8, double2, float4>;
+
+template <typename S>
+struct Coef {
+  S c0, c1, c2, c3;
+};
+
+// Rebuilds one interval's coefficients from the (f, d) entries of nodes m and m+1.
+__device__ __forceinline__ Coef<double> coef_from(double2 e0, double2 e1)
+{
+#pragma clang fp contract(off)
+  const double step = e1.x - e0.x;
+  Coef<double> c;
+  c.c0 = e0.x;
+  c.c1 = e0.y;
+  c.c2 = 3.0 * step - 2.0 * e0.y - e1.y;
+  c.c3 = e0.y + e1.y - 2.0 * step;
+  return c;
+}
+
+template <typename S>
+struct EamArgs {
+  const Atom4<S> *atoms;
+  const int *row_count;
+  const int *row_atom;
+  const int *tile_off;
+  const int *receivers;
+  int num_rows;
+  int max_edges;
+  const S *rtab;                 // global rows [nr][n_rtab][4]
+  const LdsEntry<S> *ltab;       // LDS source [nr][n_rtab]
+  int n_rtab;
+  int n_el;
+  int nr;
+  S dr;
+  S inv_dr;
+  S cutsq;
+  const S *etab;
+  int nrho;
+  S drho;
+  S inv_drho;
+  S *fp;
+  S *rho;
+  double *partials;  // [tiles][8]: 0 embedding energy, 1..6 virial, 7 pair energy
+  int nlocal;
+  double scale;
+  double *f;
+};
+
+// Species index into the tables. XLA clamps out-of-range gathers, so types past the table's
+// elements read its last element (the reference warns at pair_coeff, cpp:602-606).
+__device__ __forceinline__ int clamp_species(int z, int n_el) { return z < 0 ? 0 : (z >= n_el ? n_el - 1 : z); }
+
+// LDS table window: tables [0, T) of the nodes [lo, nr).
+template <typename S>
+struct Window {
+  const LdsEntry<S> *lds;
+  int T;   // tables per node held in LDS
+  int lo;  // first node in LDS
+};
+
+// Copies the window into LDS (all threads of the block) and returns it.
+template <typename S>
+__device__ __forceinline__ Window<S> fill_window(LdsEntry<S> *lds, int cap_entries,
+                                                 const EamArgs<S> &a, int T)
+{
+  Window<S> w;
+  w.lds = lds;
+  w.T = T;
+  const int cap_nodes = cap_entries / T;
+  w.lo = a.nr > cap_nodes ? a.nr - cap_nodes : 0;
+  const int n = (a.nr - w.lo) * T;
+  for (int q = threadIdx.x; q < n; q += blockDim.x) {
+    const int node = w.lo + q / T;
+    lds[q] = a.ltab[static_cast<long>(node) * a.n_rtab + (q % T)];
+  }
+  __syncthreads();
+  return w;
+}
+
+template <typename S>
+__device__ __forceinline__ Coef<S> rcoef(const Window<S> &w, const EamArgs<S> &a, int m, int tab)
+{
+  if (m >= w.lo) {
+    const int q = (m - w.lo) * w.T + tab;
+    if constexpr (sizeof(S) == 8) {
+      return coef_from(w.lds[q], w.lds[q + w.T]);
+    } else {
+      const float4 e = w.lds[q];
+      return Coef<S>{e.x, e.y, e.z, e.w};
+    }
+  }
+  const S *c = a.rtab + (static_cast<long>(m) * a.n_rtab + tab) * 4;
+  return Coef<S>{c[0], c[1], c[2], c[3]};
+}
+
+template <typename S>
+__device__ __forceinline__ S cvalue(const Coef<S> &c, S t)
+{
+  return c.c0 + t * (c.c1 + t * (c.c2 + t * c.c3));
+}
+
+template <typename S>
+__device__ __forceinline__ S cslope_t(const Coef<S> &c, S t)
+{
+  return c.c1 + t * (S(2) * c.c2 + t * (S(3) * c.c3));
+}
+
+// Embedding value and slope at rho, extrapolating linearly past the table (eam.py:155-164).
+template <typename S>
+__device__ __forceinline__ void embed(const EamArgs<S> &a, int z, S rho, S &F, S &Fp)
+{
+  const Locator<S> L = locate(rho, a.drho, a.nrho);
+  const S *c = a.etab + (static_cast<long>(z) * a.nrho + L.node) * 4;
+  const S end_slope = c[1] + S(2) * c[2] + S(3) * c[3];
+  F = cubic_value(c, L.t) + (L.t_raw - L.t) * end_slope;
+  Fp = (L.t_raw > S(1) ? end_slope : cubic_slope_t(c, L.t)) * a.inv_drho;
+}
+
+// Persistent walk over tile groups (TPB consecutive tiles per group), XCD by XCD. The loop count
+// is the same for every thread of a block (barriers inside stay matched); tiles past the rows
+// come out empty.
+struct GroupWalk {
+  int g, g_end, step;
+};
+
+__device__ __forceinline__ GroupWalk group_walk(int ngroups)
+{
+  const int nbx = gridDim.x / kXcds;              // blocks per XCD
+  const int xcd = blockIdx.x % kXcds;
+  const int local = blockIdx.x / kXcds;
+  const int per = (ngroups + kXcds - 1) / kXcds;  // groups per XCD
+  GroupWalk w;
+  w.g = xcd * per + local;
+  w.g_end = min((xcd + 1) * per, ngroups);
+  w.step = nbx;
+  return w;
+}
+
+inline int persistent_grid(int ngroups, int blocks_per_cu, int num_cus)
+{
+  int want = ngroups;
+  const int cap = blocks_per_cu * (num_cus > 0 ? num_cus : 256);
+  if (want > cap) want = cap;
+  return ((want + kXcds - 1) / kXcds) * kXcds;
+}
+
+constexpr int kDensLdsFused = 4096;   // 64 KB table window (fused count pass)
+constexpr int kForceLdsFused = 7680;  // 120 KB table window (fused write pass)
+
+template <typename S>
+inline EamArgs<S> eam_args(Handle &h, int nlocal, double scale, double *f)
+{
+  EamArgs<S> a;
+  a.atoms = static_cast<const Atom4<S> *>(h.d_atoms);
+  a.row_count = h.d_row_count;
+  a.row_atom = h.d_row_atom;
+  a.tile_off = h.d_tile_off;
+  a.receivers = h.d_receivers;
+  a.num_rows = h.packed_rows;
+  a.max_edges = h.contract.max_edges;
+  a.rtab = static_cast<const S *>(h.d_rtab);
+  a.ltab = static_cast<const LdsEntry<S> *>(h.d_ltab);
+  a.n_rtab = h.n_rtab;
+  a.n_el = h.n_el;
+  a.nr = h.nr;
+  a.dr = static_cast<S>(h.dr);
+  a.inv_dr = S(1) / static_cast<S>(h.dr);
+  a.cutsq = static_cast<S>(h.eam_cutoff * h.eam_cutoff);
+  a.etab = static_cast<const S *>(h.d_etab);
+  a.nrho = h.nrho;
+  a.drho = static_cast<S>(h.drho);
+  a.inv_drho = S(1) / static_cast<S>(h.drho);
+  a.fp = static_cast<S *>(h.d_fp);
+  a.rho = static_cast<S *>(h.d_rho);
+  a.partials = h.d_partials;
+  a.nlocal = nlocal;
+  a.scale = scale;
+  a.f = f;
+  return a;
+}
+
+}  // namespace lk

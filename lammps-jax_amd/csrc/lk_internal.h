@@ -68,6 +68,10 @@ struct Handle {
 
   // single-rank comm description (ghost -> owner), uploaded by lk_set_ghost_map
   int *d_ghost_owner = nullptr;
+  int *d_ghost_off = nullptr;   // owner -> ghost images, CSR over the owned rows [nlocal + 1]
+  int *d_ghost_list = nullptr;  // [nghost] ghost rows, increasing within each owner
+  int ghost_off_cap = 0;
+  int *d_done = nullptr;        // block counter of the fused step's last-block reduction
   int ghost_cap = 0;
   int ghost_n = 0;
   int ghost_nlocal = 0;
@@ -122,5 +126,10 @@ hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
 hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
                               double *f, int flags);
 hipError_t launch_finalize(Handle &h, hipStream_t s, int nblocks, double scale, int flags);
+hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles);
+hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,
+                                int nall, const int *ilist, const int *numneigh,
+                                const int *neighbors, long stride, int num_rows, int maxneighs,
+                                int nlocal, int nghost, int flags, double scale, double *f);
 
 }  // namespace lk

@@ -126,7 +126,6 @@ __global__ __launch_bounds__(W * 64) void k_pack_count(PackArgs a)
     uint32_t word = 0;
     const int jj0 = w * 32;
     const int jj1 = min(jj0 + 32, nn_max);
-#pragma unroll 4
     for (int jj = jj0; jj < jj1; ++jj) {
       bool keep = false;
       if (jj < nn) {
@@ -274,6 +273,13 @@ __global__ __launch_bounds__(256) void k_tail_reset(const StepResult *__restrict
   senders[e] = max_atoms;
   receivers[e] = max_atoms;
   mask[e] = 0;
+}
+
+hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles)
+{
+  hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(1024), 0, s, h.d_tile_count, tile_flags, ntiles,
+                     h.contract.max_edges, h.d_tile_off, h.d_result);
+  return hipGetLastError();
 }
 
 hipError_t launch_pack_atoms(Handle &h, hipStream_t s, const double *x, const int *type, int nall)

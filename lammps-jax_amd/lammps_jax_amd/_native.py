@@ -30,7 +30,7 @@ LK_VIRIAL = 2
 EXPORTED = (
     "lk_create", "lk_destroy", "lk_last_error", "lk_set_eam", "lk_set_lj",
     "lk_set_accumulation", "lk_set_ghost_map", "lk_pack_atoms", "lk_pack_edges", "lk_compute",
-    "lk_step_result", "lk_timing_enable", "lk_timing_read", "lk_edge_buffers",
+    "lk_pack_compute", "lk_step_result", "lk_timing_enable", "lk_timing_read", "lk_edge_buffers",
     "lk_staging_buffers", "lk_model_buffers",
 )
 
@@ -120,6 +120,9 @@ def load() -> ctypes.CDLL:
     lib.lk_pack_edges.restype = ip
     lib.lk_compute.argtypes = [vp, vp, ip, ip, ip, dp, vp]
     lib.lk_compute.restype = ip
+    lib.lk_pack_compute.argtypes = [vp, vp, vp, vp, ip, vp, vp, vp, ctypes.c_long, ip, ip, ip,
+                                    ip, ip, ip, dp, vp]
+    lib.lk_pack_compute.restype = ip
     lib.lk_step_result.argtypes = [vp, vp, pp(LkStepInfo)]
     lib.lk_step_result.restype = ip
     lib.lk_timing_enable.argtypes = [vp, ip]

@@ -124,6 +124,13 @@ class Handle:
                                           int(stride), int(inum), int(gnum), int(maxneighs),
                                           int(nlocal)))
 
+    def pack_compute(self, stream, x, types, nall, ilist, numneigh, neighbors, stride, inum, gnum,
+                     maxneighs, nlocal, nghost, flags, scale, f):
+        self.check(self.lib.lk_pack_compute(self.ptr, stream, x, types, int(nall), ilist, numneigh,
+                                            neighbors, int(stride), int(inum), int(gnum),
+                                            int(maxneighs), int(nlocal), int(nghost), int(flags),
+                                            float(scale), f))
+
     def compute(self, stream, nlocal, nghost, flags, scale, f):
         self.check(self.lib.lk_compute(self.ptr, stream, int(nlocal), int(nghost), int(flags),
                                        float(scale), f))
@@ -211,7 +218,7 @@ class PairJax:
 
     def __init__(self, system, model, *, precision=8, accumulation="onesided", n_hops=1,
                  max_atoms=None, edges_per_atom=128, max_edges=None, scale=1.0, device="cuda:0",
-                 newton_pair=True, comm=None, pairing="full", pair_sum=False):
+                 newton_pair=True, comm=None, pairing="full", pair_sum=False, fused=True):
         torch = _torch()
         self.torch = torch
         self.device = torch.device(device)
@@ -226,6 +233,7 @@ class PairJax:
         self.max_edges = int(max_edges if max_edges is not None else self.max_atoms * edges_per_atom)
         self.scale = float(scale)
         self.n_hops = n_hops
+        self.fused = fused
         half_list = lst["kind"] == 1
         if comm is None:
             comm = accumulation in ("onesided", "half")
@@ -260,8 +268,11 @@ class PairJax:
     def stream(self) -> int:
         return self.torch.cuda.current_stream(self.device).cuda_stream
 
-    def enqueue(self, eflag=True, vflag=True, zero_forces=True) -> None:
-        """Stream-ordered work of one compute() call, without the host readback."""
+    def enqueue(self, eflag=True, vflag=True, zero_forces=True, fused=None) -> None:
+        """Stream-ordered work of one compute() call, without the host readback.
+
+        fused: one lk_pack_compute call (default) or the three entry points in order."""
+        fused = self.fused if fused is None else fused
         s, lst = self.system, self.system.list
         st = self.stream()
         nlocal, nghost, nall = s.nlocal, s.nghost, s.nall
@@ -271,11 +282,18 @@ class PairJax:
             raise N.LammpsJaxError(
                 N.LK_ERR_CAPACITY,
                 f"LAMMPS-JAX atom capacity exceeded: global max {nall} atoms, capacity {self.max_atoms}")
+        flags = (N.LK_ENERGY if eflag else 0) | (N.LK_VIRIAL if vflag else 0)
+        if fused:
+            self.h.pack_compute(st, self.x.data_ptr(), self.type.data_ptr(), nall,
+                                self.ilist.data_ptr(), self.numneigh.data_ptr(),
+                                self.neighbors.data_ptr(), lst["stride"], lst["inum"], lst["gnum"],
+                                lst["maxneighs"], nlocal, nghost, flags, self.scale,
+                                self.f.data_ptr())
+            return
         self.h.pack_atoms(st, self.x.data_ptr(), self.type.data_ptr(), nall)
         self.h.pack_edges(st, self.x.data_ptr(), self.ilist.data_ptr(), self.numneigh.data_ptr(),
                           self.neighbors.data_ptr(), lst["stride"], lst["inum"], lst["gnum"],
                           lst["maxneighs"], nlocal)
-        flags = (N.LK_ENERGY if eflag else 0) | (N.LK_VIRIAL if vflag else 0)
         self.h.compute(st, nlocal, nghost, flags, self.scale, self.f.data_ptr())
 
     def pack(self, x=None) -> StepInfo:
@@ -289,8 +307,8 @@ class PairJax:
                           lst["maxneighs"], s.nlocal)
         return self.h.step_result(st)
 
-    def compute(self, eflag=True, vflag=True, check_capacity=True) -> StepInfo:
-        self.enqueue(eflag, vflag)
+    def compute(self, eflag=True, vflag=True, check_capacity=True, fused=None) -> StepInfo:
+        self.enqueue(eflag, vflag, fused=fused)
         info = self.h.step_result(self.stream())
         if check_capacity and info.edge_overflow:
             raise N.LammpsJaxError(

@@ -19,12 +19,13 @@ pytestmark = pytest.mark.gpu
 TOL = {8: 1e-10, 4: 1e-5}
 
 
-def _case(name, cells, precision, seed=1, scale=1.0):
+def _case(name, cells, precision, seed=1, scale=1.0, fused=True, max_edges=None):
     wl = systems.make_workload(name, cells=cells, seed=seed)
     sysm = wl.system()
     lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
     model = ("eam", wl.tables) if wl.model == "eam" else ("lj", wl.lj)
-    pj = PairJax(sysm, model, precision=precision, accumulation="onesided", scale=scale)
+    pj = PairJax(sysm, model, precision=precision, accumulation="onesided", scale=scale,
+                 fused=fused, max_edges=max_edges)
     return wl, sysm, lst, pj
 
 
@@ -41,12 +42,13 @@ def _oracle(wl, sysm, pj, precision, mode):
     return O.lj_compute(wl.lj, pos, **kw)
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("precision", [8, 4])
 @pytest.mark.parametrize("name", ["eam_alloy_131k", "lj_fcc_1k"])
-def test_onesided_matches_oracle(gpu, name, precision):
+def test_onesided_matches_oracle(gpu, name, precision, fused):
     cells = (4, 4, 4) if name.startswith("eam") else (5, 5, 5)
-    wl, sysm, lst, pj = _case(name, cells, precision, seed=2)
-    print(f"model case {name} precision={precision} nall={sysm.nall}", flush=True)
+    wl, sysm, lst, pj = _case(name, cells, precision, seed=2, fused=fused)
+    print(f"model case {name} precision={precision} fused={fused} nall={sysm.nall}", flush=True)
     info = pj.compute()
     f = pj.forces()
     ref = _oracle(wl, sysm, pj, precision, O.ONESIDED)
@@ -108,3 +110,44 @@ def test_edge_capacity_error_message(gpu):
     pj = PairJax(sysm, ("eam", wl.tables), precision=8, accumulation="onesided", max_edges=1000)
     with pytest.raises(LammpsJaxError, match="LAMMPS-JAX edge capacity exceeded: global max"):
         pj.compute()
+
+
+@pytest.mark.parametrize("name", ["eam_alloy_131k", "lj_fcc_1k"])
+def test_fused_step_writes_the_same_packed_arrays(gpu, name):
+    """lk_pack_compute stores the packed edges at exactly the positions lk_pack_edges does."""
+    cells = (5, 5, 5)
+    wl, sysm, lst, fused = _case(name, cells, 8, seed=6, fused=True)
+    _, _, _, split = _case(name, cells, 8, seed=6, fused=False)
+    a = fused.compute()
+    b = split.compute()
+    assert a.edge_count == b.edge_count and a.edge_overflow == b.edge_overflow == 0
+    for u, v in zip(fused.edges(), split.edges()):
+        np.testing.assert_array_equal(u, v)
+    fa, fb = fused.forces(), split.forces()
+    assert rel_err(fa, fb) < 1e-12
+    assert a.energy == pytest.approx(b.energy, rel=1e-12)
+    np.testing.assert_allclose(a.virial, b.virial, rtol=1e-11, atol=1e-12 * np.abs(b.virial).max())
+
+
+def test_fused_step_tail_reset_and_overflow(gpu):
+    import torch
+
+    from lammps_jax_amd._native import LammpsJaxError
+
+    wl, sysm, lst, pj = _case("eam_alloy_131k", (4, 4, 4), 8, seed=7)
+    first = pj.compute()
+    # expanded positions: fewer kept pairs; the slots of the first step past the new count reset
+    pj.x = torch.from_numpy(sysm.x * 1.04).to(pj.device)
+    second = pj.compute()
+    assert second.edge_count < first.edge_count
+    s, r, m = pj.edges()
+    c = second.edge_count
+    assert np.all(m[:c] == 1) and not m[c:].any()
+    assert np.all(s[c:] == pj.max_atoms) and np.all(r[c:] == pj.max_atoms)
+    # edge capacity smaller than the demand: the count reports demand and the step errors
+    wl, sysm, lst, small = _case("eam_alloy_131k", (4, 4, 4), 8, seed=7, max_edges=3000)
+    with pytest.raises(LammpsJaxError, match="edge capacity exceeded"):
+        small.compute()
+    info = small.compute(check_capacity=False)
+    assert info.edge_overflow == 1 and info.edge_count == first.edge_count
+    assert int(small.edges()[2].sum()) == 3000
