@@ -50,6 +50,11 @@ def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: 
         return 8 * R + 4 * E + rec * A + 48 * N
     if stage == "forward_fp":
         return (A - N) * (4 + 2 * S)
+    if stage == "step_count":
+        # list + row data, x and type of every atom once, atom records and species out,
+        # validity bits, row counts, F' (owned + ghost images) and rho out
+        return (8 * R + 4 * entries + 28 * A + (rec + 4) * A + 4 * R * words + 8 * R
+                + S * A + S * N)
     return 0.0
 
 
@@ -138,6 +143,13 @@ def main() -> int:
     stages = pj.h.timing()
     pj.h.timing_enable(False)
     print(f"[bench] timed {args.steps} steps in {elapsed:.4f}s", file=sys.stderr, flush=True)
+    # forces-only steps (eflag = vflag = 0), as most MD steps run between thermo outputs
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        pj.compute(eflag=False, vflag=False)
+    torch.cuda.synchronize(dev)
+    forces_only_ms = 1e3 * (time.perf_counter() - t0) / args.steps
 
     N, A, E = sysm.nlocal, nall, info.edge_count
     R = lst["inum"] + (lst["gnum"] if wl.n_hops > 1 else 0)
@@ -192,6 +204,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "stages_us": {k: round(v, 2) for k, v in sorted(stage_us.items())},
         "device_us_per_step": round(device_us, 2),
+        "forces_only": {"ms_per_step": forces_only_ms,
+                        "atom_steps_per_s": N / (forces_only_ms * 1e-3)},
         "step_roofline": {
             "survey_bytes_per_step": sb["total"],
             "device_us": round(device_us, 2),

@@ -118,6 +118,7 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
   __shared__ LdsEntry<S> lds[kForceLds];
   __shared__ S part[4][TPB][W][kWave];
   __shared__ double vir[TPB][6][W];
+  __shared__ double tpart[TPB][7];  // per tile: pair energy, virial 1..6
   const Window<S> win = fill_window<S>(lds, kForceLds, a, a.n_rtab);
   const int sub = threadIdx.x / (W * kWave);
   const int wave = (threadIdx.x / kWave) % W;
@@ -240,42 +241,25 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
         e_own = static_cast<double>(ep);
       }
       const double esum = wave_sum(e_own);
-      if (tile * kWave < a.num_rows) {
-        if (lane == 0) a.partials[8L * tile + 7] = esum;
-        if (VIRIAL && lane < 6) {
-          double v = vir[sub][lane][0];
-          for (int w = 1; w < W; ++w) v += vir[sub][lane][w];
-          a.partials[8L * tile + 1 + lane] = v;
-        }
+      if (lane == 0) tpart[sub][0] = esum;
+      if (VIRIAL && lane < 6) {
+        double v = vir[sub][lane][0];
+        for (int w = 1; w < W; ++w) v += vir[sub][lane][w];
+        tpart[sub][1 + lane] = v;
       }
     }
     __syncthreads();
+    // The block's first wave stores the partials of the group's tiles (the only wave that
+    // writes partials, see finalize_last_block); tpart is next written after the next barrier.
+    if (threadIdx.x < TPB * 7) {
+      const int q = threadIdx.x / 7, c = threadIdx.x % 7;
+      const int t = gw.g * TPB + q;
+      if (t * kWave < a.num_rows && (c == 0 || VIRIAL))
+        a.partials[8L * t + (c == 0 ? 7 : c)] = tpart[q][c];
+    }
   }
-}
-
-// Fixed-order reduction of the tile partials into the step result (energy and virial scaled).
-__global__ __launch_bounds__(256) void k_finalize(const double *__restrict__ partials, int ntiles,
-                                                  double scale, int flags,
-                                                  StepResult *__restrict__ result)
-{
-  __shared__ double red[7][256];
-  const int t = threadIdx.x;
-  double acc[7] = {0, 0, 0, 0, 0, 0, 0};
-  for (int k = t; k < ntiles; k += blockDim.x) {
-    acc[0] += partials[8L * k + 0] + partials[8L * k + 7];
-    for (int c = 1; c < 7; ++c) acc[c] += partials[8L * k + c];
-  }
-  for (int c = 0; c < 7; ++c) red[c][t] = acc[c];
-  __syncthreads();
-  for (int off = blockDim.x / 2; off >= 1; off >>= 1) {
-    if (t < off)
-      for (int c = 0; c < 7; ++c) red[c][t] += red[c][t + off];
-    __syncthreads();
-  }
-  if (t == 0) {
-    result->energy = (flags & LK_ENERGY) ? scale * red[0][0] : 0.0;
-    for (int c = 0; c < 6; ++c) result->virial[c] = (flags & LK_VIRIAL) ? scale * red[c + 1][0] : 0.0;
-  }
+  finalize_last_block(a.partials, a.ntiles, a.scale, a.flags, a.result, a.done,
+                      reinterpret_cast<double *>(lds));
 }
 
 template <typename S>
@@ -283,6 +267,7 @@ static hipError_t eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
                                double *f, int flags)
 {
   EamArgs<S> a = eam_args<S>(h, nlocal, scale, f);
+  a.flags = flags;
   const int ntiles = (h.packed_rows + kWave - 1) / kWave;
   if (ntiles > 0) {
     const int ngroups = (ntiles + kDensTPB - 1) / kDensTPB;
@@ -296,18 +281,35 @@ static hipError_t eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
     hipLaunchKernelGGL(k_forward_rows<S>, dim3((nghost + 255) / 256), dim3(256), 0, s,
                        static_cast<S *>(h.d_fp), h.d_ghost_owner, nlocal, nghost);
   }
-  if (ntiles > 0) {
-    const int ngroups = (ntiles + kForceTPB - 1) / kForceTPB;
-    const int grid = persistent_grid(ngroups, 1, h.num_cus);
-    StageTimer timer(h, s, "eam_force");
-    if (flags & LK_VIRIAL)
-      hipLaunchKernelGGL((k_eam_force_rows<S, kForceW, kForceTPB, true>), dim3(grid),
-                         dim3(kForceW * kForceTPB * kWave), 0, s, a, ngroups);
-    else
-      hipLaunchKernelGGL((k_eam_force_rows<S, kForceW, kForceTPB, false>), dim3(grid),
-                         dim3(kForceW * kForceTPB * kWave), 0, s, a, ngroups);
-  }
-  return launch_finalize(h, s, ntiles, scale, flags);
+  return launch_eam_force(h, s, a, flags);
+}
+
+template <typename S>
+hipError_t launch_eam_force_t(Handle &h, hipStream_t s, EamArgs<S> a, int flags)
+{
+  // One launch even with no rows: its last block writes the step result.
+  const int ntiles = a.ntiles;
+  const int ngroups = ntiles > 0 ? (ntiles + kForceTPB - 1) / kForceTPB : 1;
+  const int grid = persistent_grid(ngroups, 1, h.num_cus);
+  a.flags = flags;
+  StageTimer timer(h, s, "eam_force");
+  if (flags & LK_VIRIAL)
+    hipLaunchKernelGGL((k_eam_force_rows<S, kForceW, kForceTPB, true>), dim3(grid),
+                       dim3(kForceW * kForceTPB * kWave), 0, s, a, ngroups);
+  else
+    hipLaunchKernelGGL((k_eam_force_rows<S, kForceW, kForceTPB, false>), dim3(grid),
+                       dim3(kForceW * kForceTPB * kWave), 0, s, a, ngroups);
+  return hipGetLastError();
+}
+
+hipError_t launch_eam_force(Handle &h, hipStream_t s, EamArgs<double> a, int flags)
+{
+  return launch_eam_force_t<double>(h, s, a, flags);
+}
+
+hipError_t launch_eam_force(Handle &h, hipStream_t s, EamArgs<float> a, int flags)
+{
+  return launch_eam_force_t<float>(h, s, a, flags);
 }
 
 hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
@@ -315,15 +317,6 @@ hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
 {
   if (h.contract.precision == LK_FLOAT64) return eam_onesided<double>(h, s, nlocal, nghost, scale, f, flags);
   return eam_onesided<float>(h, s, nlocal, nghost, scale, f, flags);
-}
-
-hipError_t launch_finalize(Handle &h, hipStream_t s, int ntiles, double scale, int flags)
-{
-  // Slots a sweep did not write this step (virial without LK_VIRIAL) are read but discarded.
-  StageTimer timer(h, s, "finalize");
-  hipLaunchKernelGGL(k_finalize, dim3(1), dim3(256), 0, s, h.d_partials, ntiles, scale, flags,
-                     h.d_result);
-  return hipGetLastError();
 }
 
 }  // namespace lk

@@ -58,6 +58,10 @@ struct EamArgs {
   int nlocal;
   double scale;
   double *f;
+  StepResult *result;
+  int *done;
+  int ntiles;
+  int flags;
 };
 
 // Species index into the tables. XLA clamps out-of-range gathers, so types past the table's
@@ -158,8 +162,50 @@ inline int persistent_grid(int ngroups, int blocks_per_cu, int num_cus)
   return ((want + kXcds - 1) / kXcds) * kXcds;
 }
 
-constexpr int kDensLdsFused = 4096;   // 64 KB table window (fused count pass)
-constexpr int kForceLdsFused = 7680;  // 120 KB table window (fused write pass)
+// The last block of a launch to finish reduces the tile partials (slot 0 + slot 7 energy, slots
+// 1..6 virial) in a fixed order into the step result, so no separate finalize launch is needed.
+// Every thread of the block calls it after its last write of partials; `scratch` holds
+// 7 * blockDim.x doubles of LDS that is no longer in use. Returns in every block.
+//
+// Only the first wave of a block may have written partials: it alone issues the device-scope
+// release (an L2 write-back, costly when every wave of every block issues one). No acquire on
+// that side either: it would invalidate the XCD's L2 under the blocks still running there; only
+// the last block needs it.
+__device__ __forceinline__ void finalize_last_block(const double *partials, int ntiles,
+                                                    double scale, int flags,
+                                                    StepResult *result, int *done,
+                                                    double *scratch)
+{
+  __shared__ int last_block;
+  if (threadIdx.x < kWave) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0) last_block = atomicAdd(done, 1) == static_cast<int>(gridDim.x) - 1;
+  __syncthreads();
+  if (!last_block) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const int t = threadIdx.x, nt = blockDim.x;
+  double acc[7] = {0, 0, 0, 0, 0, 0, 0};
+  for (int k = t; k < ntiles; k += nt) {
+    const double *q = partials + 8L * k;
+    acc[0] += q[0] + q[7];
+    for (int c = 1; c < 7; ++c) acc[c] += q[c];
+  }
+  for (int c = 0; c < 7; ++c) scratch[c * nt + t] = acc[c];
+  __syncthreads();
+  for (int off = nt / 2; off >= 1; off >>= 1) {
+    if (t < off)
+      for (int c = 0; c < 7; ++c) scratch[c * nt + t] += scratch[c * nt + t + off];
+    __syncthreads();
+  }
+  if (t == 0) {
+    result->energy = (flags & LK_ENERGY) ? scale * scratch[0] : 0.0;
+    for (int c = 0; c < 6; ++c)
+      result->virial[c] = (flags & LK_VIRIAL) ? scale * scratch[(c + 1) * nt] : 0.0;
+    *done = 0;  // ready for the next launch
+  }
+}
+
+constexpr int kDensLdsFused = 4096;  // 64 KB table window (fused count pass)
 
 template <typename S>
 inline EamArgs<S> eam_args(Handle &h, int nlocal, double scale, double *f)
@@ -190,7 +236,15 @@ inline EamArgs<S> eam_args(Handle &h, int nlocal, double scale, double *f)
   a.nlocal = nlocal;
   a.scale = scale;
   a.f = f;
+  a.result = h.d_result;
+  a.done = h.d_done;
+  a.ntiles = (h.packed_rows + kWave - 1) / kWave;
+  a.flags = 0;
   return a;
 }
+
+// The force sweep over the packed edges (lk_eam.hip); its last block writes the step result.
+hipError_t launch_eam_force(Handle &h, hipStream_t s, EamArgs<double> a, int flags);
+hipError_t launch_eam_force(Handle &h, hipStream_t s, EamArgs<float> a, int flags);
 
 }  // namespace lk

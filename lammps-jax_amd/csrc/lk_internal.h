@@ -125,8 +125,8 @@ hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
                                double *f, int flags);
 hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
                               double *f, int flags);
-hipError_t launch_finalize(Handle &h, hipStream_t s, int nblocks, double scale, int flags);
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles);
+
 hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,
                                 int nall, const int *ilist, const int *numneigh,
                                 const int *neighbors, long stride, int num_rows, int maxneighs,

@@ -5,6 +5,7 @@
 #include "lk_device.h"
 #include "lk_internal.h"
 #include "lk_tile.h"
+#include "lk_eam_common.h"
 
 namespace lk {
 
@@ -25,6 +26,10 @@ struct LjArgs {
   int nlocal;
   double scale;
   double *f;
+  StepResult *result;
+  int *done;
+  int ntiles;
+  int flags;
 };
 
 // One-sided full list: the row atom takes the whole pair force 2 * de/d(r^2) * (x_j - x_i) and
@@ -34,17 +39,19 @@ __global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
 {
   __shared__ S part[4][W][kWave];
   __shared__ double vir[6][W];
+  __shared__ double scratch[7 * W * kWave];
+  // No early exit: every block counts itself in for the last-block reduction.
   const int tile = tile_of_block();
-  if (tile * kWave >= a.num_rows) return;
+  const bool has_rows = tile * kWave < a.num_rows;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   const int ii = tile * kWave + lane;
-  const bool row = ii < a.num_rows;
+  const bool row = has_rows && ii < a.num_rows;
   const int i = row ? a.row_atom[ii] : -1;
   const int cnt = i >= 0 ? a.row_count[ii] : 0;
   Atom4<S> ai = {S(0), S(0), S(0), S(0)};
   if (i >= 0) ai = a.atoms[i];
-  const long base = a.tile_off[tile];
+  const long base = has_rows ? a.tile_off[tile] : 0;
   const S tiny = static_cast<S>(1.0e-12);
   S en = S(0), fx = S(0), fy = S(0), fz = S(0);
   double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
@@ -101,7 +108,7 @@ __global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
     }
   }
   __syncthreads();
-  if (wave != 0) return;
+  if (wave == 0) {
   en = part[0][0][lane];
   fx = part[1][0][lane];
   fy = part[2][0][lane];
@@ -122,15 +129,17 @@ __global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
     fi[2] += a.scale * static_cast<double>(fz);
   }
   const double esum = wave_sum(e_own);
-  if (lane == 0) {
+  if (has_rows && lane == 0) {
     a.partials[8L * tile] = esum;
     a.partials[8L * tile + 7] = 0.0;
   }
-  if (VIRIAL && lane < 6) {
+  if (has_rows && VIRIAL && lane < 6) {
     double v = vir[lane][0];
     for (int w = 1; w < W; ++w) v += vir[lane][w];
     a.partials[8L * tile + 1 + lane] = v;
   }
+  }
+  finalize_last_block(a.partials, a.ntiles, a.scale, a.flags, a.result, a.done, scratch);
 }
 
 template <typename S>
@@ -153,17 +162,20 @@ static hipError_t lj_onesided(Handle &h, hipStream_t s, int nlocal, double scale
   a.nlocal = nlocal;
   a.scale = scale;
   a.f = f;
+  a.result = h.d_result;
+  a.done = h.d_done;
   constexpr int W = 8;
   const int ntiles = (h.packed_rows + kWave - 1) / kWave;
-  const int grid = tile_grid(ntiles);
-  if (ntiles > 0) {
-    StageTimer timer(h, s, "lj_rows");
-    if (flags & LK_VIRIAL)
-      hipLaunchKernelGGL((k_lj_rows<S, W, true>), dim3(grid), dim3(W * kWave), 0, s, a);
-    else
-      hipLaunchKernelGGL((k_lj_rows<S, W, false>), dim3(grid), dim3(W * kWave), 0, s, a);
-  }
-  return launch_finalize(h, s, ntiles, scale, flags);
+  a.ntiles = ntiles;
+  a.flags = flags;
+  // One launch even with no rows: its last block writes the step result.
+  const int grid = tile_grid(ntiles > 0 ? ntiles : 1);
+  StageTimer timer(h, s, "lj_rows");
+  if (flags & LK_VIRIAL)
+    hipLaunchKernelGGL((k_lj_rows<S, W, true>), dim3(grid), dim3(W * kWave), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_lj_rows<S, W, false>), dim3(grid), dim3(W * kWave), 0, s, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int /*nghost*/, double scale,

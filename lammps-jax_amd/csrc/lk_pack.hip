@@ -16,6 +16,7 @@
 #include "lk_device.h"
 #include "lk_internal.h"
 #include "lk_tile.h"
+#include "lk_pack.h"
 
 namespace lk {
 
@@ -37,57 +38,6 @@ __global__ __launch_bounds__(256) void k_pack_atoms(const double *__restrict__ x
   a.w = static_cast<S>(sp);
   atoms[i] = a;
   species[i] = sp;
-}
-
-struct PackArgs {
-  const double *x;
-  const int *ilist;
-  const int *numneigh;
-  const int *neighbors;
-  long stride;
-  int num_rows;
-  int maxneighs;
-  int max_atoms;
-  int max_edges;
-  int nlocal;
-  double cutsq;
-  int duplicate;        // duplicate_reverse_edges (cpp:850-852)
-  int half_edges;       // half_edges && full_list (cpp:863)
-  int unique_boundary;  // half_edges && comm && full_list (cpp:864-865)
-  int words;            // validity words per row
-  int pitch;            // row pitch of the bits array (max_atoms)
-  uint32_t *bits;
-  int *row_count;
-  int *row_atom;
-  int *tile_count;
-  int *tile_flags;
-};
-
-// The filter chain of PackNeighborFunctor::operator() (cpp:84-101) for list entry (i, jj).
-// r^2 is formed without FMA contraction, in double, from the engine's x, so the keep/drop
-// decision at r^2 == rc^2 matches the reference bit for bit.
-__device__ __forceinline__ bool keep_entry(const PackArgs &a, int i, double xi0, double xi1,
-                                           double xi2, int j)
-{
-#pragma clang fp contract(off)
-  if (j >= a.max_atoms) return false;
-  const double xj0 = a.x[3L * j + 0];
-  const double xj1 = a.x[3L * j + 1];
-  const double xj2 = a.x[3L * j + 2];
-  const double dx = xi0 - xj0;
-  const double dy = xi1 - xj1;
-  const double dz = xi2 - xj2;
-  const double rsq = dx * dx + dy * dy + dz * dz;
-  if (rsq > a.cutsq) return false;
-  if (a.half_edges && j < i) return false;
-  if (a.unique_boundary && j >= a.nlocal) {
-    if (xj2 < xi2) return false;
-    if (xj2 == xi2) {
-      if (xj1 < xi1) return false;
-      if (xj1 == xi1 && xj0 < xi0) return false;
-    }
-  }
-  return true;
 }
 
 // Pass 1: one lane per list row, W waves per 64-row tile. Wave w takes the 32-slot words
@@ -210,13 +160,12 @@ __global__ __launch_bounds__(1024) void k_tile_scan(const int *__restrict__ tile
 // popping its row's validity bits in order); wave k % W writes ordinal k: the rows with more than
 // k kept entries form the ballot M and write M's popcount consecutive edges.
 template <int W>
-__global__ __launch_bounds__(W * 64) void k_pack_write(PackArgs a, const int *__restrict__ tile_off,
-                                                       int *__restrict__ senders,
-                                                       int *__restrict__ receivers,
-                                                       unsigned char *__restrict__ mask)
+__device__ __forceinline__ void pack_write_tile(const PackArgs &a, int tile,
+                                                     const int *__restrict__ tile_off,
+                                                     int *__restrict__ senders,
+                                                     int *__restrict__ receivers,
+                                                     unsigned char *__restrict__ mask)
 {
-  const int tile = tile_of_block();
-  if (tile * kWave >= a.num_rows) return;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   const int ii = tile * kWave + lane;
@@ -259,20 +208,26 @@ __global__ __launch_bounds__(W * 64) void k_pack_write(PackArgs a, const int *__
   }
 }
 
-// ResetEdgeTailFunctor (cpp:157-173): slots past the new count that held last step's edges
-// return to the padding (max_atoms, max_atoms, false).
-__global__ __launch_bounds__(256) void k_tail_reset(const StepResult *__restrict__ result,
-                                                    long span, int max_atoms,
-                                                    int *__restrict__ senders,
-                                                    int *__restrict__ receivers,
-                                                    unsigned char *__restrict__ mask)
+
+template <int W>
+__global__ __launch_bounds__(W * 64) void k_pack_write(PackArgs a, const int *__restrict__ tile_off,
+                                                       int *__restrict__ senders,
+                                                       int *__restrict__ receivers,
+                                                       unsigned char *__restrict__ mask,
+                                                       const StepResult *__restrict__ result,
+                                                       long reset_end)
 {
-  const long e = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (e >= span) return;
-  if (e < result->edge_count) return;
-  senders[e] = max_atoms;
-  receivers[e] = max_atoms;
-  mask[e] = 0;
+  const int tile = tile_of_block();
+  if (tile * kWave < a.num_rows) pack_write_tile<W>(a, tile, tile_off, senders, receivers, mask);
+  // ResetEdgeTailFunctor (cpp:157-173): slots past the new count that held last step's edges
+  // return to the padding (max_atoms, max_atoms, false); a grid-stride pass over every block.
+  const long count = result->edge_count;
+  for (long e = count + static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < reset_end;
+       e += static_cast<long>(gridDim.x) * blockDim.x) {
+    senders[e] = a.max_atoms;
+    receivers[e] = a.max_atoms;
+    mask[e] = 0;
+  }
 }
 
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles)
@@ -297,10 +252,9 @@ hipError_t launch_pack_atoms(Handle &h, hipStream_t s, const double *x, const in
   return hipGetLastError();
 }
 
-hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const int *ilist,
-                             const int *numneigh, const int *neighbors, long stride, int num_rows,
-                             int maxneighs, int nlocal, int duplicate, int half_edges,
-                             int unique_boundary)
+PackArgs pack_args(Handle &h, const double *x, const int *ilist, const int *numneigh,
+                   const int *neighbors, long stride, int num_rows, int maxneighs, int nlocal,
+                   int duplicate, int half_edges, int unique_boundary)
 {
   PackArgs a;
   a.x = x;
@@ -324,6 +278,30 @@ hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const in
   a.row_atom = h.d_row_atom;
   a.tile_count = h.d_tile_count;
   a.tile_flags = h.d_tile_count + (h.contract.max_atoms / kWave + 2);
+  return a;
+}
+
+hipError_t launch_pack_write(Handle &h, hipStream_t s, const PackArgs &a)
+{
+  constexpr int W = 4;
+  const int ntiles = (a.num_rows + kWave - 1) / kWave;
+  const long reset_end = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
+                                                                     : h.contract.max_edges;
+  // at least one block so the tail reset runs when the list is empty
+  const int grid = tile_grid(ntiles > 0 ? ntiles : 1);
+  StageTimer timer(h, s, "pack_write");
+  hipLaunchKernelGGL(k_pack_write<W>, dim3(grid), dim3(W * kWave), 0, s, a, h.d_tile_off,
+                     h.d_senders, h.d_receivers, h.d_mask, h.d_result, reset_end);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const int *ilist,
+                             const int *numneigh, const int *neighbors, long stride, int num_rows,
+                             int maxneighs, int nlocal, int duplicate, int half_edges,
+                             int unique_boundary)
+{
+  const PackArgs a = pack_args(h, x, ilist, numneigh, neighbors, stride, num_rows, maxneighs,
+                               nlocal, duplicate, half_edges, unique_boundary);
   const int ntiles = (num_rows + kWave - 1) / kWave;
   h.packed_rows = num_rows;
   constexpr int W = 4;
@@ -337,21 +315,9 @@ hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const in
     hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(1024), 0, s, h.d_tile_count, a.tile_flags,
                        ntiles, h.contract.max_edges, h.d_tile_off, h.d_result);
   }
-  if (ntiles > 0) {
-    StageTimer timer(h, s, "pack_write");
-    hipLaunchKernelGGL(k_pack_write<W>, dim3(grid), dim3(W * kWave), 0, s, a, h.d_tile_off,
-                       h.d_senders, h.d_receivers, h.d_mask);
-  }
-  const long span = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
-                                                                 : h.contract.max_edges;
-  if (span > 0) {
-    const long blocks = (span + 255) / 256;
-    StageTimer timer(h, s, "tail_reset");
-    hipLaunchKernelGGL(k_tail_reset, dim3(blocks), dim3(256), 0, s, h.d_result, span,
-                       h.contract.max_atoms, h.d_senders, h.d_receivers, h.d_mask);
-  }
+  hipError_t e = launch_pack_write(h, s, a);
   ++h.pack_serial;
-  return hipGetLastError();
+  return e;
 }
 
 }  // namespace lk
