@@ -92,6 +92,36 @@ def cpu_baseline(wl, sysm, lst, max_atoms, max_edges, budget_s: float, max_steps
     }
 
 
+def calibrate_copy(mib: int) -> int:
+    """A plain copy of known size: FETCH_SIZE and WRITE_SIZE of its dispatches give the factor
+    that turns the counters into bytes (expected bytes / counted bytes)."""
+    import torch
+
+    n = mib * (1 << 20) // 8
+    src = torch.arange(n, dtype=torch.float64, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_each_way": n * 8, "dispatches": 10}))
+    return 0
+
+
+def pmc_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` from the committed PMC summary, or None.
+
+    The summary (profiles/pmc_<kernel>_<workload>.txt) holds a line
+    `traffic_bytes_per_launch = <bytes>`: FETCH_SIZE + WRITE_SIZE per dispatch from two
+    rocprofv3 --pmc runs, each scaled by the factor the same counter reads on a plain copy."""
+    path = REPO / "profiles" / f"pmc_{kernel}_{workload}.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch"):
+            return float(line.split("=", 1)[1])
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -100,11 +130,18 @@ def main() -> int:
     ap.add_argument("--workload", default="eam_alloy_131k")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
+    ap.add_argument("--split-steps", type=int, default=20,
+                    help="steps through the separate pack entry points, for packing us/step")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB ten times (scales the PMC "
+                         "byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one GPU per box); "
               "run with --gpus 1", file=sys.stderr)
         return 2
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
 
     import torch
 
@@ -150,6 +187,20 @@ def main() -> int:
         pj.compute(eflag=False, vflag=False)
     torch.cuda.synchronize(dev)
     forces_only_ms = 1e3 * (time.perf_counter() - t0) / args.steps
+    # packing alone: the separate entry points (lk_pack_atoms, lk_pack_edges) with their timers
+    pack_us = None
+    if args.split_steps > 0:
+        for _ in range(3):
+            pj.compute(fused=False)
+        torch.cuda.synchronize(dev)
+        pj.h.timing_enable(True)
+        for _ in range(args.split_steps):
+            pj.compute(fused=False)
+        torch.cuda.synchronize(dev)
+        split = pj.h.timing()
+        pj.h.timing_enable(False)
+        pack_stages = ("pack_atoms", "pack_count", "tile_scan", "pack_write")
+        pack_us = {k: 1e3 * split[k][0] / split[k][1] for k in pack_stages if k in split}
 
     N, A, E = sysm.nlocal, nall, info.edge_count
     R = lst["inum"] + (lst["gnum"] if wl.n_hops > 1 else 0)
@@ -199,13 +250,15 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": pmc_traffic(dom, wl.name),
         },
         "cpu_baseline": cpu,
         "stages_us": {k: round(v, 2) for k, v in sorted(stage_us.items())},
         "device_us_per_step": round(device_us, 2),
         "forces_only": {"ms_per_step": forces_only_ms,
                         "atom_steps_per_s": N / (forces_only_ms * 1e-3)},
+        "packing_us_per_step": round(sum(pack_us.values()), 2) if pack_us else None,
+        "packing_stages_us": {k: round(v, 2) for k, v in pack_us.items()} if pack_us else None,
         "step_roofline": {
             "survey_bytes_per_step": sb["total"],
             "device_us": round(device_us, 2),

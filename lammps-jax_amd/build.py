@@ -21,7 +21,8 @@ CSRC = ROOT / "csrc"
 PKG = ROOT / "lammps_jax_amd"
 BUILD = ROOT / "_build"
 
-HIP_SOURCES = ["lk_api.hip", "lk_pack.hip", "lk_eam.hip", "lk_lj.hip", "lk_step.hip"]
+HIP_SOURCES = ["lk_api.hip", "lk_pack.hip", "lk_eam.hip", "lk_lj.hip", "lk_step.hip",
+               "lk_twosided.hip"]
 
 OFFLOAD_ARCH = os.environ.get("LK_OFFLOAD_ARCH", "gfx950")
 HIPCC_FLAGS = [

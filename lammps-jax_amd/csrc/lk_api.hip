@@ -53,7 +53,9 @@ void free_all(Handle &h)
   void *ptrs[] = {h.d_ltab,      h.d_rtab,      h.d_etab,      h.d_atoms,       h.d_species,   h.d_senders,
                   h.d_receivers, h.d_mask,      h.d_row_count,   h.d_row_atom,  h.d_tile_count,
                   h.d_tile_off,  h.d_bits,      h.d_fp,          h.d_rho,       h.d_partials,
-                  h.d_result,    h.d_ghost_owner, h.d_ghost_off, h.d_ghost_list, h.d_done};
+                  h.d_result,    h.d_ghost_owner, h.d_ghost_off, h.d_ghost_list, h.d_done,
+                  h.d_deg,       h.d_inc_loc,   h.d_inc_part,    h.d_inc_tmp,   h.d_inc,
+                  h.d_rho_part,  h.d_epair};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -76,6 +78,30 @@ int ensure_bits(Handle &h, int maxneighs)
   e = dalloc(&h.d_bits, static_cast<size_t>(words) * h.contract.max_atoms);
   if (e != hipSuccess) return hip_fail(h, e, "hipMalloc(validity bits)");
   h.bits_words = words;
+  return LK_OK;
+}
+
+// Buffers of the two-sided schemes, sized from the contract once (first use).
+int ensure_incidence(Handle &h)
+{
+  if (h.d_inc) return LK_OK;
+  const long A = h.contract.max_atoms;
+  const long E2 = 2L * h.contract.max_edges;
+  if (E2 > static_cast<long>(INT_MAX))
+    return fail(h, LK_ERR_CAPACITY,
+                "LAMMPS-JAX edge capacity too large for two-sided accumulation (2 * max_edges "
+                "must fit in int)");
+  const long chunks = (A + 1 + 4095) / 4096;
+  hipError_t e;
+  if ((e = dalloc(&h.d_deg, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence counts)");
+  if ((e = dalloc(&h.d_inc_loc, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence offsets)");
+  if ((e = dalloc(&h.d_inc_part, chunks)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence chunks)");
+  if ((e = dalloc(&h.d_inc_tmp, E2)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence staging)");
+  if ((e = dalloc(&h.d_inc, E2)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence lists)");
+  if ((e = hipMalloc(&h.d_rho_part, A * h.scalar_bytes())) != hipSuccess) return hip_fail(h, e, "hipMalloc(rho partials)");
+  if ((e = hipMalloc(&h.d_epair, A * h.scalar_bytes())) != hipSuccess) return hip_fail(h, e, "hipMalloc(pair energy)");
+  if ((e = hipMemset(h.d_deg, 0, sizeof(int) * (A + 1))) != hipSuccess) return hip_fail(h, e, "hipMemset(incidence counts)");
+  if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(h, e, "initialising incidence buffers");
   return LK_OK;
 }
 
@@ -290,6 +316,8 @@ int lk_set_accumulation(lk_handle *w, int accum)
     default:
       return fail(h, LK_ERR_ARGUMENT, "unknown accumulation scheme");
   }
+  if (accum != LK_ACCUM_ONESIDED)
+    if (int rc = ensure_incidence(h)) return rc;
   h.accum = accum;
   return LK_OK;
 }
@@ -350,6 +378,7 @@ int lk_pack_atoms(lk_handle *w, void *stream, const double *x, const int *type, 
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
   if (nall < 0 || (nall > 0 && (!x || !type))) return fail(h, LK_ERR_ARGUMENT, "invalid atom arrays");
+  h.x_last = x;
   hipError_t e = lk::launch_pack_atoms(h, as_stream(stream), x, type, nall);
   if (e != hipSuccess) return hip_fail(h, e, "pack_atoms");
   return LK_OK;
@@ -375,6 +404,7 @@ int lk_pack_edges(lk_handle *w, void *stream, const double *x, const int *ilist,
     return fail(h, LK_ERR_ARGUMENT, "invalid neighbor list arrays");
   if (rows > 0 && nb_stride < 1) return fail(h, LK_ERR_ARGUMENT, "invalid neighbor stride");
   if (int rc = ensure_bits(h, max_neighbors_per_atom)) return rc;
+  h.x_last = x;
   const bool half_edges = c.pairing != LK_PAIRING_FULL;
   const bool full_list = !c.half_list;
   // cpp/pair_jax_kokkos.cpp:850-867
@@ -410,7 +440,17 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
       e = lk::launch_lj_onesided(h, s, nlocal, nghost, scale, f, flags);
     }
   } else {
-    return fail(h, LK_ERR_UNSUPPORTED, "this accumulation scheme is not implemented yet");
+    if (h.accum == LK_ACCUM_HALF && h.model != 1)
+      return fail(h, LK_ERR_UNSUPPORTED,
+                  "half accumulation is defined for EAM; LJ on half lists uses plain accumulation");
+    if (h.accum == LK_ACCUM_HALF && nghost > 0 && (h.ghost_n != nghost || h.ghost_nlocal != nlocal))
+      return fail(h, LK_ERR_STATE,
+                  "half accumulation needs the ghost map of this step (lk_set_ghost_map) for the "
+                  "density fold");
+    if ((flags & LK_VIRIAL) && h.contract.newton_pair && nlocal + nghost > 0 && !h.x_last)
+      return fail(h, LK_ERR_STATE, "the f.r virial needs the positions of a prior pack");
+    if (int rc = ensure_incidence(h)) return rc;
+    e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, h.x_last);
   }
   if (e != hipSuccess) return hip_fail(h, e, "compute");
   return LK_OK;

@@ -258,7 +258,7 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
         a.partials[8L * t + (c == 0 ? 7 : c)] = tpart[q][c];
     }
   }
-  finalize_last_block(a.partials, a.ntiles, a.scale, a.flags, a.result, a.done,
+  finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done,
                       reinterpret_cast<double *>(lds));
 }
 

@@ -165,14 +165,15 @@ inline int persistent_grid(int ngroups, int blocks_per_cu, int num_cus)
 // The last block of a launch to finish reduces the tile partials (slot 0 + slot 7 energy, slots
 // 1..6 virial) in a fixed order into the step result, so no separate finalize launch is needed.
 // Every thread of the block calls it after its last write of partials; `scratch` holds
-// 7 * blockDim.x doubles of LDS that is no longer in use. Returns in every block.
+// 7 * blockDim.x doubles of LDS that is no longer in use. Returns in every block. The energy is
+// scaled by `escale`, the virial by `vscale` (1 when the partials already hold scaled forces).
 //
 // Only the first wave of a block may have written partials: it alone issues the device-scope
 // release (an L2 write-back, costly when every wave of every block issues one). No acquire on
 // that side either: it would invalidate the XCD's L2 under the blocks still running there; only
 // the last block needs it.
 __device__ __forceinline__ void finalize_last_block(const double *partials, int ntiles,
-                                                    double scale, int flags,
+                                                    double escale, double vscale, int flags,
                                                     StepResult *result, int *done,
                                                     double *scratch)
 {
@@ -198,9 +199,9 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
     __syncthreads();
   }
   if (t == 0) {
-    result->energy = (flags & LK_ENERGY) ? scale * scratch[0] : 0.0;
+    result->energy = (flags & LK_ENERGY) ? escale * scratch[0] : 0.0;
     for (int c = 0; c < 6; ++c)
-      result->virial[c] = (flags & LK_VIRIAL) ? scale * scratch[(c + 1) * nt] : 0.0;
+      result->virial[c] = (flags & LK_VIRIAL) ? vscale * scratch[(c + 1) * nt] : 0.0;
     *done = 0;  // ready for the next launch
   }
 }

@@ -71,7 +71,7 @@ struct Handle {
   int *d_ghost_off = nullptr;   // owner -> ghost images, CSR over the owned rows [nlocal + 1]
   int *d_ghost_list = nullptr;  // [nghost] ghost rows, increasing within each owner
   int ghost_off_cap = 0;
-  int *d_done = nullptr;        // block counter of the fused step's last-block reduction
+  int *d_done = nullptr;        // block counter of the last-block result reduction
   int ghost_cap = 0;
   int ghost_n = 0;
   int ghost_nlocal = 0;
@@ -86,6 +86,16 @@ struct Handle {
   };
   std::vector<Pending> pending;
   std::map<std::string, std::pair<double, long>> stage_ms;
+
+  // incidence lists of the two-sided schemes (lk_twosided.hip), allocated on first use
+  int *d_deg = nullptr;         // [max_atoms + 1] incident-edge counts, zero between steps
+  int *d_inc_loc = nullptr;     // [max_atoms + 1] offsets within each scan chunk
+  int *d_inc_part = nullptr;    // [chunks] chunk offsets
+  uint32_t *d_inc_tmp = nullptr;  // [2 max_edges] (edge << 1 | side), unsorted
+  int *d_inc = nullptr;         // [2 max_edges] other atom | side << 31, ascending edge order
+  void *d_rho_part = nullptr;   // [max_atoms] per-row density before the ghost fold
+  void *d_epair = nullptr;      // [max_atoms] per-row pair energy
+  const double *x_last = nullptr;  // engine positions of the last pack (f.r virial)
 
   size_t scalar_bytes() const { return contract.precision == LK_FLOAT64 ? 8 : 4; }
 };
@@ -126,6 +136,9 @@ hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
 hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
                               double *f, int flags);
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles);
+
+hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
+                            double scale, double *f, const double *x);
 
 hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,
                                 int nall, const int *ilist, const int *numneigh,

@@ -139,7 +139,7 @@ __global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
     a.partials[8L * tile + 1 + lane] = v;
   }
   }
-  finalize_last_block(a.partials, a.ntiles, a.scale, a.flags, a.result, a.done, scratch);
+  finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done, scratch);
 }
 
 template <typename S>

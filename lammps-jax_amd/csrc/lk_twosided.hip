@@ -1,0 +1,665 @@
+// Two-sided accumulation schemes on the packed edges: LK_ACCUM_PLAIN and LK_ACCUM_HALF.
+//
+// PLAIN is the sparse-edge atom-force bundle (wrap_energy_fn, python/lammps_jax/export.py:153-209
+// over make_setfl_energy(half_edges=False), eam.py:265-333, or the LJ energy of
+// examples/export_model.py:16-50): density and pair energy sit on the sender; the energy sums
+// the owned rows, or every row when an edge starts on a ghost row (export.py:183-194), or the
+// owned rows only for n_hops > 1 / communicating bundles; forces are -dE/dx, so the sender takes
+// +g and the receiver -g and ghost rows carry force rows for the reverse comm.
+// HALF is the communicating half-edge bundle (eam.py:303-317): density to both ends, the sender
+// carries the whole pair energy, ghost density partials fold into their owners (reverse comm),
+// ghost F' is the owner's, and both ends take the pair force.
+// In both, the engine's f gains scale * F over nall rows with newton on (AddForcesFunctor,
+// cpp/pair_jax_kokkos.cpp:175-192, 959-987) and the virial is f.r over the nall rows of the
+// total f (VirialFDotRFunctor, cpp:227-245), reported only with newton on (cpp:733-736).
+//
+// Every per-atom sum is a segmented reduction over the atom's incident edges in ascending edge
+// order, so results are bitwise reproducible without float atomics:
+//   count    incident-edge count per atom (integer atomics; exact)
+//   scan     exclusive offsets (two-level: 4096-element chunks, then the chunk totals)
+//   fill     (edge << 1 | side) into each atom's segment (atomicSub: the counts return to zero,
+//            ready for the next step)
+//   sort     one wave per atom ranks its segment by edge id and stores the other atom of each
+//            edge with the side in the top bit (side 1: this atom is the receiver)
+//   sweeps   16 lanes per atom walk the sorted segment; a fixed butterfly sums the lanes.
+
+#include "lk_eam_common.h"
+
+namespace lk {
+
+constexpr int kScanThreads = 1024;
+constexpr int kScanItems = 4;
+constexpr int kScanChunk = kScanThreads * kScanItems;
+constexpr int kGroup = 16;                     // lanes per atom in the row sweeps
+constexpr int kRowBlock = 1024;                // threads per row-sweep block
+constexpr int kRowAtoms = kRowBlock / kGroup;  // 64 atoms per block = one partial tile
+constexpr int kIncLds = 7680;                  // 120 KB table window
+
+struct IncArgs {
+  const int *senders;
+  const int *receivers;
+  const unsigned char *mask;
+  const StepResult *result;
+  int max_edges;
+  int nrows;  // atoms that may appear on an edge (max_atoms)
+  int *deg;   // [nrows + 1], zero between steps
+  int *loc;   // [nrows + 1] offsets within each scan chunk
+  int *part;  // [chunks] exclusive chunk offsets
+  uint32_t *tmp;
+  int *inc;
+};
+
+__device__ __forceinline__ long live_edges(const StepResult *r, int max_edges)
+{
+  const long c = r->edge_count;
+  return c < max_edges ? c : max_edges;
+}
+
+__device__ __forceinline__ int inc_off(const int *loc, const int *part, int a)
+{
+  return loc[a] + part[a / kScanChunk];
+}
+
+__device__ __forceinline__ bool edge_ends(const IncArgs &a, long e, int &s, int &r)
+{
+  if (!a.mask[e]) return false;
+  s = a.senders[e];
+  r = a.receivers[e];
+  return s >= 0 && s < a.nrows && r >= 0 && r < a.nrows;
+}
+
+__global__ __launch_bounds__(256) void k_inc_count(IncArgs a)
+{
+  const long n = live_edges(a.result, a.max_edges);
+  for (long e = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < n;
+       e += static_cast<long>(gridDim.x) * blockDim.x) {
+    int s, r;
+    if (!edge_ends(a, e, s, r)) continue;
+    atomicAdd(&a.deg[s], 1);
+    atomicAdd(&a.deg[r], 1);
+  }
+}
+
+// Exclusive scan of in[0, n) within 4096-element chunks; chunk totals to part[].
+__global__ __launch_bounds__(kScanThreads) void k_scan_chunks(const int *__restrict__ in, int n,
+                                                              int *__restrict__ out,
+                                                              int *__restrict__ part)
+{
+  __shared__ int wsum[kScanThreads / kWave];
+  const int t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
+  const long base = static_cast<long>(blockIdx.x) * kScanChunk + static_cast<long>(t) * kScanItems;
+  int v[kScanItems];
+  int s = 0;
+#pragma unroll
+  for (int q = 0; q < kScanItems; ++q) {
+    v[q] = base + q < n ? in[base + q] : 0;
+    s += v[q];
+  }
+  int incl = s;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += y;
+  }
+  if (lane == kWave - 1) wsum[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    const int w = lane < kScanThreads / kWave ? wsum[lane] : 0;
+    int wi = w;
+#pragma unroll
+    for (int off = 1; off < kScanThreads / kWave; off <<= 1) {
+      const int y = __shfl_up(wi, off, kWave);
+      if (lane >= off) wi += y;
+    }
+    if (lane < kScanThreads / kWave) wsum[lane] = wi - w;
+  }
+  __syncthreads();
+  int run = wsum[wave] + incl - s;
+#pragma unroll
+  for (int q = 0; q < kScanItems; ++q) {
+    if (base + q < n) out[base + q] = run;
+    run += v[q];
+  }
+  if (t == kScanThreads - 1) part[blockIdx.x] = run;
+}
+
+// Exclusive scan of the chunk totals in place (one block).
+__global__ __launch_bounds__(kScanThreads) void k_scan_parts(int *__restrict__ part, int nparts)
+{
+  __shared__ int wsum[kScanThreads / kWave];
+  __shared__ int carry;
+  const int t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
+  if (t == 0) carry = 0;
+  __syncthreads();
+  for (int b0 = 0; b0 < nparts; b0 += kScanThreads) {
+    const int i = b0 + t;
+    const int v = i < nparts ? part[i] : 0;
+    int incl = v;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int y = __shfl_up(incl, off, kWave);
+      if (lane >= off) incl += y;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+      const int w = lane < kScanThreads / kWave ? wsum[lane] : 0;
+      int wi = w;
+#pragma unroll
+      for (int off = 1; off < kScanThreads / kWave; off <<= 1) {
+        const int y = __shfl_up(wi, off, kWave);
+        if (lane >= off) wi += y;
+      }
+      if (lane < kScanThreads / kWave) wsum[lane] = wi - w;
+    }
+    __syncthreads();
+    const int c = carry;
+    if (i < nparts) part[i] = c + wsum[wave] + incl - v;
+    __syncthreads();
+    if (t == kScanThreads - 1) carry = c + wsum[wave] + incl;
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(256) void k_inc_fill(IncArgs a)
+{
+  const long n = live_edges(a.result, a.max_edges);
+  for (long e = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < n;
+       e += static_cast<long>(gridDim.x) * blockDim.x) {
+    int s, r;
+    if (!edge_ends(a, e, s, r)) continue;
+    const uint32_t key = static_cast<uint32_t>(e) << 1;
+    const int ps = inc_off(a.loc, a.part, s) + atomicSub(&a.deg[s], 1) - 1;
+    a.tmp[ps] = key;
+    const int pr = inc_off(a.loc, a.part, r) + atomicSub(&a.deg[r], 1) - 1;
+    a.tmp[pr] = key | 1u;
+  }
+}
+
+// One wave per atom: the rank of each entry is the number of smaller keys in the segment
+// (keys are distinct), so the store order is ascending edge id whatever order fill left.
+__global__ __launch_bounds__(256) void k_inc_sort(IncArgs a, int nsort)
+{
+  const int atom = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (atom >= nsort) return;  // whole wave
+  const int b = inc_off(a.loc, a.part, atom);
+  const int L = inc_off(a.loc, a.part, atom + 1) - b;
+  for (int c0 = 0; c0 < L; c0 += kWave) {
+    const bool mine = c0 + lane < L;
+    const uint32_t v = mine ? a.tmp[b + c0 + lane] : 0xFFFFFFFFu;
+    int rank = 0;
+    for (int c1 = 0; c1 < L; c1 += kWave) {
+      const uint32_t w = c1 + lane < L ? a.tmp[b + c1 + lane] : 0xFFFFFFFFu;
+#pragma unroll 16
+      for (int m = 0; m < kWave; ++m) {
+        const uint32_t wm = static_cast<uint32_t>(__shfl(static_cast<int>(w), m, kWave));
+        rank += wm < v ? 1 : 0;
+      }
+    }
+    if (mine) {
+      const long e = v >> 1;
+      const uint32_t side = v & 1u;
+      const int other = side ? a.senders[e] : a.receivers[e];
+      a.inc[b + rank] = static_cast<int>(static_cast<uint32_t>(other) | (side << 31));
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ T group_sum(T v)
+{
+#pragma unroll
+  for (int m = kGroup / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Arguments of the two-sided sweeps besides the model block.
+struct TwoSided {
+  const int *loc;
+  const int *part;
+  const int *inc;
+  int nall;
+  int nlocal;
+  int nadd;             // rows that take the force add: nall with newton on, else nlocal
+  int owned_rows_only;  // export.py:190-192 (n_hops > 1 or a communicating bundle)
+  int fdotr;            // newton on: the f.r virial is reported
+  const double *x;      // engine positions for the virial
+  const int *ghost_off;
+  const int *ghost_list;
+  int nblk;             // 64-atom tiles over nall
+};
+
+// Rows whose energy counts (export.py:183-194).
+__device__ __forceinline__ int energy_rows(const TwoSided &t, const StepResult *r, bool half)
+{
+  if (half || t.owned_rows_only) return t.nlocal;
+  return r->ghost_sender ? t.nall : t.nlocal;
+}
+
+template <typename S>
+__device__ __forceinline__ S geometry(const Atom4<S> &xa, const Atom4<S> &xo, S &dx, S &dy, S &dz)
+{
+#pragma clang fp contract(off)
+  dx = xo.x - xa.x;
+  dy = xo.y - xa.y;
+  dz = xo.z - xa.z;
+  return dx * dx + dy * dy + dz * dz;
+}
+
+// Density and pair energy per row (eam.py:298-314).
+template <typename S, bool HALF>
+__global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, TwoSided t,
+                                                               S *__restrict__ rho_part,
+                                                               S *__restrict__ epair)
+{
+  __shared__ LdsEntry<S> lds[kIncLds];
+  const Window<S> win = fill_window<S>(lds, kIncLds, m, m.n_rtab);
+  const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
+  for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
+    const int a = blk * kRowAtoms + g;
+    S rho = S(0), ep = S(0);
+    if (a < t.nall) {
+      const Atom4<S> xa = m.atoms[a];
+      const int za = clamp_species(static_cast<int>(xa.w), m.n_el);
+      const int b = inc_off(t.loc, t.part, a);
+      const int L = inc_off(t.loc, t.part, a + 1) - b;
+      for (int k = gl; k < L; k += kGroup) {
+        const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
+        const bool in = (v >> 31) != 0;
+        if (!HALF && in) continue;  // plain: density and pair energy stay on the sender
+        const int o = static_cast<int>(v & 0x7FFFFFFFu);
+        const Atom4<S> xo = m.atoms[o];
+        S dx, dy, dz;
+        const S r2 = geometry(xa, xo, dx, dy, dz);
+        if (!(r2 < m.cutsq)) continue;
+        const S rinv = rsqrt_nr(r2);
+        const S rr = r2 * rinv;
+        const Locator<S> L2 = locate_mul(rr, m.inv_dr, m.nr);
+        const int zo = clamp_species(static_cast<int>(xo.w), m.n_el);
+        rho += cvalue(rcoef(win, m, L2.node, zo), L2.t);
+        if (!in) {
+          const S phi = cvalue(rcoef(win, m, L2.node, m.n_el + pair_row(za, zo)), L2.t) * rinv;
+          ep += HALF ? phi : S(0.5) * phi;  // half: the sender carries both halves
+        }
+      }
+    }
+    rho = group_sum(rho);
+    ep = group_sum(ep);
+    if (gl == 0 && a < t.nall) {
+      rho_part[a] = rho;
+      epair[a] = ep;
+    }
+  }
+}
+
+// Embedding: F and F' per row (eam.py:319-321); half folds ghost densities into their owners
+// first and hands the owner's F' to its ghost images. Energy partial of the tile into slot 0.
+template <typename S, bool HALF>
+__global__ __launch_bounds__(kWave) void k_eam_embed_inc(EamArgs<S> m, TwoSided t,
+                                                         const S *__restrict__ rho_part,
+                                                         const S *__restrict__ epair)
+{
+  const int tile = blockIdx.x;
+  const int a = tile * kWave + threadIdx.x;
+  const int erows = energy_rows(t, m.result, HALF);
+  double e_row = 0.0;
+  if (HALF) {
+    if (a < t.nlocal) {
+      S rho = rho_part[a];
+      if (t.ghost_off)
+        for (int q = t.ghost_off[a]; q < t.ghost_off[a + 1]; ++q) rho += rho_part[t.ghost_list[q]];
+      S F, Fp;
+      embed(m, clamp_species(static_cast<int>(m.atoms[a].w), m.n_el), rho, F, Fp);
+      m.fp[a] = Fp;
+      m.rho[a] = rho;
+      if (t.ghost_off)
+        for (int q = t.ghost_off[a]; q < t.ghost_off[a + 1]; ++q) {
+          m.fp[t.ghost_list[q]] = Fp;
+          m.rho[t.ghost_list[q]] = S(0);
+        }
+      e_row = static_cast<double>(epair[a] + F);
+    }
+  } else if (a < t.nall) {
+    const S rho = rho_part[a];
+    S F, Fp;
+    embed(m, clamp_species(static_cast<int>(m.atoms[a].w), m.n_el), rho, F, Fp);
+    m.fp[a] = Fp;
+    m.rho[a] = rho;
+    if (a < erows) e_row = static_cast<double>(epair[a] + F);
+  }
+  const double esum = wave_sum(e_row);
+  if (threadIdx.x == 0 && tile < t.nblk) m.partials[8L * tile] = esum;
+}
+
+// Per-row f.r virial of the total f after the add, summed over the 64 rows of the tile in a fixed
+// order by the first wave, which alone stores partials (finalize_last_block's contract).
+template <bool VIRIAL>
+__device__ __forceinline__ void add_row_force(double *f, const double *x, int a, int nadd,
+                                              int nall, int fdotr, double scale, double fx,
+                                              double fy, double fz, double (*vt)[kRowAtoms],
+                                              int g)
+{
+  double w[6] = {0, 0, 0, 0, 0, 0};
+  if (a < nall) {
+    double *fa = f + 3L * a;
+    double tx = fa[0], ty = fa[1], tz = fa[2];
+    if (a < nadd) {
+      tx += scale * fx;
+      ty += scale * fy;
+      tz += scale * fz;
+      fa[0] = tx;
+      fa[1] = ty;
+      fa[2] = tz;
+    }
+    if (VIRIAL && fdotr) {
+      const double *xa = x + 3L * a;
+      w[0] = tx * xa[0];
+      w[1] = ty * xa[1];
+      w[2] = tz * xa[2];
+      w[3] = ty * xa[0];
+      w[4] = tz * xa[0];
+      w[5] = tz * xa[1];
+    }
+  }
+  if (VIRIAL)
+    for (int c = 0; c < 6; ++c) vt[c][g] = w[c];
+}
+
+template <bool VIRIAL>
+__device__ __forceinline__ void store_tile_virial(double *partials, int blk,
+                                                  double (*vt)[kRowAtoms], double e_tile,
+                                                  bool write_energy)
+{
+  // called by the first wave only, after a barrier
+  const int lane = threadIdx.x;
+  if (VIRIAL) {
+    for (int c = 0; c < 6; ++c) {
+      const double v = wave_sum(vt[c][lane]);
+      if (lane == 0) partials[8L * blk + 1 + c] = v;
+    }
+  }
+  if (lane == 0) {
+    partials[8L * blk + 7] = 0.0;
+    if (write_energy) partials[8L * blk] = e_tile;
+  }
+}
+
+// Force sweep (eam.py:336-409 closed form; export.py:197-204 autodiff convention).
+template <typename S, bool HALF, bool VIRIAL>
+__global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSided t)
+{
+  __shared__ LdsEntry<S> lds[kIncLds];
+  __shared__ double vt[6][kRowAtoms];
+  const Window<S> win = fill_window<S>(lds, kIncLds, m, m.n_rtab);
+  const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
+  const int erows = energy_rows(t, m.result, HALF);
+  for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
+    const int a = blk * kRowAtoms + g;
+    S fx = S(0), fy = S(0), fz = S(0);
+    if (a < t.nall) {
+      const Atom4<S> xa = m.atoms[a];
+      const int za = clamp_species(static_cast<int>(xa.w), m.n_el);
+      const S fpa = m.fp[a];
+      const int b = inc_off(t.loc, t.part, a);
+      const int L = inc_off(t.loc, t.part, a + 1) - b;
+      for (int k = gl; k < L; k += kGroup) {
+        const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
+        const bool in = (v >> 31) != 0;
+        const int o = static_cast<int>(v & 0x7FFFFFFFu);
+        if (!HALF && (in ? o : a) >= erows) continue;  // uncounted senders carry no gradient
+        const Atom4<S> xo = m.atoms[o];
+        S dx, dy, dz;
+        const S r2 = geometry(xa, xo, dx, dy, dz);
+        if (!(r2 < m.cutsq)) continue;
+        const S rinv = rsqrt_nr(r2);
+        const S rr = r2 * rinv;
+        const Locator<S> L2 = locate_mul(rr, m.inv_dr, m.nr);
+        const int zo = clamp_species(static_cast<int>(xo.w), m.n_el);
+        // Past the table the non-extrapolated lookups saturate: slope 0 (eam.py:150).
+        const bool inside = !(L2.t_raw > S(1));
+        const int zs = in ? zo : za, zr = in ? za : zo;
+        const S fps = in ? m.fp[o] : fpa;
+        const S rho_r_p = inside ? cslope_t(rcoef(win, m, L2.node, zr), L2.t) * m.inv_dr : S(0);
+        const Coef<S> cp = rcoef(win, m, L2.node, m.n_el + pair_row(za, zo));
+        const S phi = cvalue(cp, L2.t) * rinv;
+        const S z2p = inside ? cslope_t(cp, L2.t) * m.inv_dr : S(0);
+        const S phip = (z2p - phi) * rinv;
+        S coef;
+        if (HALF) {
+          const S fpr = in ? fpa : m.fp[o];
+          const S rho_s_p = inside ? cslope_t(rcoef(win, m, L2.node, zs), L2.t) * m.inv_dr : S(0);
+          coef = (fps * rho_r_p + fpr * rho_s_p + phip) * rinv;
+        } else {
+          coef = (fps * rho_r_p + S(0.5) * phip) * rinv;
+        }
+        // sender += coef d, receiver -= coef d with d = x_r - x_s: either way coef (x_o - x_a)
+        fx += coef * dx;
+        fy += coef * dy;
+        fz += coef * dz;
+      }
+    }
+    fx = group_sum(fx);
+    fy = group_sum(fy);
+    fz = group_sum(fz);
+    if (gl == 0)
+      add_row_force<VIRIAL>(m.f, t.x, a, t.nadd, t.nall, t.fdotr, m.scale,
+                            static_cast<double>(fx), static_cast<double>(fy),
+                            static_cast<double>(fz), vt, g);
+    __syncthreads();
+    if (threadIdx.x < kWave && blk * kRowAtoms < t.nall)
+      store_tile_virial<VIRIAL>(m.partials, blk, vt, 0.0, false);
+    __syncthreads();
+  }
+  finalize_last_block(m.partials, t.nblk, m.scale, 1.0, m.flags, m.result, m.done,
+                      reinterpret_cast<double *>(lds));
+}
+
+template <typename S>
+struct LjModel {
+  const Atom4<S> *atoms;
+  S cutsq, sigsq, four_eps, edge_scale;
+  double scale;
+  double *f;
+  double *partials;
+  StepResult *result;
+  int *done;
+  int flags;
+};
+
+// LJ 12-6 plain (examples/export_model.py:16-50): e per edge on the sender row, g = 2 de/d(r^2) d
+// (times edge_energy_scale) to the sender and minus it to the receiver.
+template <typename S, bool VIRIAL>
+__global__ __launch_bounds__(kRowBlock) void k_lj_inc(LjModel<S> m, TwoSided t)
+{
+  __shared__ double vt[6][kRowAtoms];
+  __shared__ double et[kRowAtoms];
+  __shared__ double scratch[7 * kRowBlock];
+  const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
+  const int erows = energy_rows(t, m.result, false);
+  const S tiny = static_cast<S>(1.0e-12);
+  for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
+    const int a = blk * kRowAtoms + g;
+    S en = S(0), fx = S(0), fy = S(0), fz = S(0);
+    if (a < t.nall) {
+      const Atom4<S> xa = m.atoms[a];
+      const int b = inc_off(t.loc, t.part, a);
+      const int L = inc_off(t.loc, t.part, a + 1) - b;
+      for (int k = gl; k < L; k += kGroup) {
+        const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
+        const bool in = (v >> 31) != 0;
+        const int o = static_cast<int>(v & 0x7FFFFFFFu);
+        if ((in ? o : a) >= erows) continue;
+        const Atom4<S> xo = m.atoms[o];
+        S dx, dy, dz;
+        const S r2 = geometry(xa, xo, dx, dy, dz);
+        if (!(r2 > tiny && r2 < m.cutsq)) continue;  // export_model.py:22
+        const S inv_r2 = m.sigsq / r2;
+        const S inv_r6 = inv_r2 * inv_r2 * inv_r2;
+        if (!in) en += m.edge_scale * (m.four_eps * (inv_r6 * inv_r6 - inv_r6));
+        const S dedr2 = -m.four_eps * (S(6) * inv_r6 * inv_r6 - S(3) * inv_r6) / r2;
+        const S coef = m.edge_scale * S(2) * dedr2;
+        fx += coef * dx;
+        fy += coef * dy;
+        fz += coef * dz;
+      }
+    }
+    en = group_sum(en);
+    fx = group_sum(fx);
+    fy = group_sum(fy);
+    fz = group_sum(fz);
+    if (gl == 0) {
+      et[g] = a < erows ? static_cast<double>(en) : 0.0;
+      add_row_force<VIRIAL>(m.f, t.x, a, t.nadd, t.nall, t.fdotr, m.scale,
+                            static_cast<double>(fx), static_cast<double>(fy),
+                            static_cast<double>(fz), vt, g);
+    }
+    __syncthreads();
+    if (threadIdx.x < kWave && blk * kRowAtoms < t.nall) {
+      const double e_tile = wave_sum(et[threadIdx.x]);
+      store_tile_virial<VIRIAL>(m.partials, blk, vt, e_tile, true);
+    }
+    __syncthreads();
+  }
+  finalize_last_block(m.partials, t.nblk, m.scale, 1.0, m.flags, m.result, m.done, scratch);
+}
+
+static int grid_for(const Handle &h, long work, int per_block, int blocks_per_cu)
+{
+  long want = (work + per_block - 1) / per_block;
+  const long cap = static_cast<long>(blocks_per_cu) * (h.num_cus > 0 ? h.num_cus : 256);
+  if (want > cap) want = cap;
+  if (want < 1) want = 1;
+  return static_cast<int>(want);
+}
+
+static hipError_t build_incidence(Handle &h, hipStream_t s, int nall)
+{
+  IncArgs ia;
+  ia.senders = h.d_senders;
+  ia.receivers = h.d_receivers;
+  ia.mask = h.d_mask;
+  ia.result = h.d_result;
+  ia.max_edges = h.contract.max_edges;
+  ia.nrows = h.contract.max_atoms;
+  ia.deg = h.d_deg;
+  ia.loc = h.d_inc_loc;
+  ia.part = h.d_inc_part;
+  ia.tmp = h.d_inc_tmp;
+  ia.inc = h.d_inc;
+  const int egrid = grid_for(h, h.contract.max_edges, 256, 16);
+  {
+    StageTimer timer(h, s, "inc_count");
+    hipLaunchKernelGGL(k_inc_count, dim3(egrid), dim3(256), 0, s, ia);
+  }
+  {
+    StageTimer timer(h, s, "inc_scan");
+    const int n = h.contract.max_atoms + 1;
+    const int chunks = (n + kScanChunk - 1) / kScanChunk;
+    hipLaunchKernelGGL(k_scan_chunks, dim3(chunks), dim3(kScanThreads), 0, s, h.d_deg, n,
+                       h.d_inc_loc, h.d_inc_part);
+    hipLaunchKernelGGL(k_scan_parts, dim3(1), dim3(kScanThreads), 0, s, h.d_inc_part, chunks);
+  }
+  {
+    StageTimer timer(h, s, "inc_fill");
+    hipLaunchKernelGGL(k_inc_fill, dim3(egrid), dim3(256), 0, s, ia);
+  }
+  if (nall > 0) {
+    StageTimer timer(h, s, "inc_sort");
+    hipLaunchKernelGGL(k_inc_sort, dim3((nall + 3) / 4), dim3(256), 0, s, ia, nall);
+  }
+  return hipGetLastError();
+}
+
+static TwoSided two_sided_args(Handle &h, int nlocal, int nghost, const double *x)
+{
+  TwoSided t;
+  t.loc = h.d_inc_loc;
+  t.part = h.d_inc_part;
+  t.inc = h.d_inc;
+  t.nall = nlocal + nghost;
+  t.nlocal = nlocal;
+  t.nadd = h.contract.newton_pair ? t.nall : nlocal;
+  t.owned_rows_only = (h.contract.n_hops > 1 || h.contract.comm) ? 1 : 0;
+  t.fdotr = h.contract.newton_pair ? 1 : 0;
+  t.x = x;
+  t.ghost_off = nghost > 0 ? h.d_ghost_off : nullptr;
+  t.ghost_list = h.d_ghost_list;
+  t.nblk = (t.nall + kRowAtoms - 1) / kRowAtoms;
+  return t;
+}
+
+template <typename S, bool HALF>
+static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
+                                double scale, double *f, const double *x)
+{
+  EamArgs<S> m = eam_args<S>(h, nlocal, scale, f);
+  TwoSided t = two_sided_args(h, nlocal, nghost, x);
+  m.flags = flags;
+  S *rho_part = static_cast<S *>(h.d_rho_part);
+  S *epair = static_cast<S *>(h.d_epair);
+  const int nblk = t.nblk > 0 ? t.nblk : 1;
+  const int grid = grid_for(h, nblk, 1, 1);
+  if (t.nblk > 0) {
+    StageTimer timer(h, s, "eam_density");
+    hipLaunchKernelGGL((k_eam_density_inc<S, HALF>), dim3(grid), dim3(kRowBlock), 0, s, m, t,
+                       rho_part, epair);
+  }
+  if (t.nblk > 0) {
+    StageTimer timer(h, s, "eam_embed");
+    hipLaunchKernelGGL((k_eam_embed_inc<S, HALF>), dim3(t.nblk), dim3(kWave), 0, s, m, t,
+                       static_cast<const S *>(rho_part), static_cast<const S *>(epair));
+  }
+  // one launch even with no rows: its last block writes the step result
+  StageTimer timer(h, s, "eam_force");
+  if (flags & LK_VIRIAL)
+    hipLaunchKernelGGL((k_eam_force_inc<S, HALF, true>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+  else
+    hipLaunchKernelGGL((k_eam_force_inc<S, HALF, false>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+  return hipGetLastError();
+}
+
+template <typename S>
+static hipError_t lj_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
+                               double scale, double *f, const double *x)
+{
+  LjModel<S> m;
+  m.atoms = static_cast<const Atom4<S> *>(h.d_atoms);
+  m.cutsq = static_cast<S>(h.lj.cutoff * h.lj.cutoff);
+  m.sigsq = static_cast<S>(h.lj.sigma * h.lj.sigma);
+  m.four_eps = static_cast<S>(4.0 * h.lj.epsilon);
+  m.edge_scale = static_cast<S>(h.lj.edge_energy_scale);
+  m.scale = scale;
+  m.f = f;
+  m.partials = h.d_partials;
+  m.result = h.d_result;
+  m.done = h.d_done;
+  m.flags = flags;
+  TwoSided t = two_sided_args(h, nlocal, nghost, x);
+  const int grid = grid_for(h, t.nblk > 0 ? t.nblk : 1, 1, 2);
+  StageTimer timer(h, s, "lj_rows");
+  if (flags & LK_VIRIAL)
+    hipLaunchKernelGGL((k_lj_inc<S, true>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+  else
+    hipLaunchKernelGGL((k_lj_inc<S, false>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+  return hipGetLastError();
+}
+
+hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
+                            double scale, double *f, const double *x)
+{
+  hipError_t e = build_incidence(h, s, nlocal + nghost);
+  if (e != hipSuccess) return e;
+  const bool f64 = h.contract.precision == LK_FLOAT64;
+  const bool half = h.accum == LK_ACCUM_HALF;
+  if (h.model == 1) {
+    if (f64) return half ? eam_two_sided<double, true>(h, s, nlocal, nghost, flags, scale, f, x)
+                         : eam_two_sided<double, false>(h, s, nlocal, nghost, flags, scale, f, x);
+    return half ? eam_two_sided<float, true>(h, s, nlocal, nghost, flags, scale, f, x)
+                : eam_two_sided<float, false>(h, s, nlocal, nghost, flags, scale, f, x);
+  }
+  if (f64) return lj_two_sided<double>(h, s, nlocal, nghost, flags, scale, f, x);
+  return lj_two_sided<float>(h, s, nlocal, nghost, flags, scale, f, x);
+}
+
+}  // namespace lk

@@ -237,6 +237,9 @@ class PairJax:
         half_list = lst["kind"] == 1
         if comm is None:
             comm = accumulation in ("onesided", "half")
+        if accumulation == "half" and pairing == "full":
+            # a LAMMPS half list taken as is: each boundary pair packed once, on this rank
+            pairing = "half-unique"
         newton = "on" if newton_pair else "off"
         self.contract = contract_for(max_atoms=self.max_atoms, max_edges=self.max_edges,
                                      cutoff=cutoff, precision=precision, newton=newton,

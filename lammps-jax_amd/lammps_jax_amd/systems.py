@@ -157,7 +157,7 @@ def make_workload(name: str, *, cells=None, seed: int | None = None) -> Workload
         rng = np.random.default_rng(12345 if seed is None else seed)
         x = fcc_lattice(nx, ny, nz, a) + rng.uniform(-0.05, 0.05, size=(4 * nx * ny * nz, 3))
         return Workload(name, "lj", 8, wrap(x, box), np.ones(len(x), np.int32), box, 2.5, 0.3,
-                        1, LIST_FULL, 96, "onesided",
+                        1, LIST_FULL, 96, "plain",
                         lj=dict(epsilon=1.0, sigma=1.0, cutoff=2.5, edge_energy_scale=0.5))
     if name == "lj_ghost_262k":
         nx, ny, nz = cells or (64, 32, 32)

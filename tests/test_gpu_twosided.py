@@ -1,0 +1,143 @@
+"""GPU parity of the two-sided schemes against the oracle, row by row (ghost rows included).
+
+plain  the sparse-edge atom-force bundle (python/lammps_jax/export.py:153-209): density and pair
+       energy on the sender, sender += g and receiver -= g, ghost rows carry force rows for the
+       reverse comm; energy over the owned rows (n_hops = 2: owned rows only).
+half   the communicating half-edge bundle over a LAMMPS half list (eam.py:303-317): density to
+       both ends, ghost densities folded into their owners, both ends take the pair force.
+The engine's f gains scale * F over nall rows (newton on, cpp:175-192) and the virial is f.r
+over those rows of the total f (cpp:227-245). Tolerances: float64 1e-10 relative, float32 1e-5
+relative (normwise for forces and virial)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from lk_testutil import fold_ghosts, rel_err
+from lammps_jax_amd import harness, systems
+from lammps_jax_amd.pair import PairJax
+
+pytestmark = pytest.mark.gpu
+
+TOL = {8: 1e-10, 4: 1e-5}
+
+
+def _case(name, cells, precision, accumulation, kind, *, n_hops=1, seed=1, scale=1.0,
+          fused=False):
+    wl = systems.make_workload(name, cells=cells, seed=seed)
+    sysm = systems.System(wl.x, wl.types, wl.box, n_hops * wl.cutoff + wl.skin)
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=kind)
+    model = ("eam", wl.tables) if wl.model == "eam" else ("lj", wl.lj)
+    pj = PairJax(sysm, model, precision=precision, accumulation=accumulation, n_hops=n_hops,
+                 scale=scale, fused=fused)
+    print(f"two-sided case {name} cells={cells} precision={precision} {accumulation} "
+          f"n_hops={n_hops} nall={sysm.nall}", flush=True)
+    return wl, sysm, lst, pj
+
+
+def _oracle(wl, sysm, lst, pj, precision, mode, *, n_hops=1):
+    pos, sp = O.pack_atoms(sysm.x, sysm.type, sysm.nall, pj.max_atoms, precision)
+    s, r, m, _, _ = O.pack_neighbors(sysm.x, lst, max_atoms=pj.max_atoms, max_edges=pj.max_edges,
+                                     nlocal=sysm.nlocal, cutoff=wl.cutoff, n_hops=n_hops)
+    kw = dict(nlocal=sysm.nlocal, nghost=sysm.nghost, senders=s, receivers=r, mask=m, mode=mode,
+              precision=precision, owned_rows_only=n_hops > 1)
+    if wl.model == "eam":
+        return O.eam_compute(wl.tables, pos, sp, ghost_owner=sysm.ghost_owner, **kw)
+    return O.lj_compute(wl.lj, pos, **kw)
+
+
+def _check(pj, sysm, ref, precision, scale=1.0):
+    info = pj.compute()
+    f = pj.forces()
+    nall = sysm.nall
+    tol = TOL[precision]
+    f_ref = scale * ref["forces"][:nall]
+    assert info.edge_overflow == 0
+    assert info.energy == pytest.approx(scale * ref["energy"], rel=tol)
+    assert rel_err(f[:nall], f_ref) < tol
+    assert np.any(f[sysm.nlocal:nall] != 0.0)  # ghost rows carry their force rows
+    assert rel_err(info.virial, O.virial_fdotr(f_ref, sysm.x, nall)) < tol
+    return info, f
+
+
+@pytest.mark.parametrize("precision", [8, 4])
+def test_plain_eam_full_list(gpu, precision):
+    wl, sysm, lst, pj = _case("eam_alloy_131k", (4, 4, 4), precision, "plain", harness.LIST_FULL)
+    ref = _oracle(wl, sysm, lst, pj, precision, O.PLAIN)
+    _check(pj, sysm, ref, precision)
+    rho, fp = pj.model_rows()
+    tol = TOL[precision]
+    assert rel_err(rho[: sysm.nall], ref["rho"][: sysm.nall]) < tol
+    assert rel_err(fp[: sysm.nall], ref["fp"][: sysm.nall]) < tol
+
+
+@pytest.mark.parametrize("precision", [8, 4])
+def test_half_eam_half_list(gpu, precision):
+    """C2/C4 shape: a LAMMPS half list taken as is, half accumulation with the ghost fold."""
+    wl, sysm, lst, pj = _case("eam_alloy_8k", (4, 4, 4), precision, "half", harness.LIST_HALF)
+    ref = _oracle(wl, sysm, lst, pj, precision, O.HALF)
+    info, f = _check(pj, sysm, ref, precision)
+    rho, fp = pj.model_rows()
+    tol = TOL[precision]
+    nl = sysm.nlocal
+    assert rel_err(rho[:nl], ref["rho"][:nl]) < tol
+    assert np.all(rho[nl: sysm.nall] == 0.0)  # folded into the owners
+    assert rel_err(fp[: sysm.nall], ref["fp"][: sysm.nall]) < tol
+    # after LAMMPS' reverse comm, the full-list one-sided scheme gives the same owned forces
+    full = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    pos, sp = O.pack_atoms(sysm.x, sysm.type, sysm.nall, pj.max_atoms, precision)
+    s, r, m, _, _ = O.pack_neighbors(sysm.x, full, max_atoms=pj.max_atoms,
+                                     max_edges=pj.max_edges, nlocal=nl, cutoff=wl.cutoff)
+    one = O.eam_compute(wl.tables, pos, sp, nlocal=nl, nghost=sysm.nghost, senders=s,
+                        receivers=r, mask=m, mode=O.ONESIDED, precision=precision,
+                        ghost_owner=sysm.ghost_owner)
+    assert rel_err(fold_ghosts(f, nl, sysm.ghost_owner), one["forces"][:nl]) < 10 * tol
+    assert info.energy == pytest.approx(one["energy"], rel=10 * tol)
+
+
+def test_plain_eam_ghost_rows_n_hops_2(gpu):
+    """n_hops = 2: ghost rows are list rows too; the energy counts the owned rows only."""
+    wl, sysm, lst, pj = _case("eam_alloy_131k", (4, 4, 4), 8, "plain", harness.LIST_FULL_GHOST,
+                              n_hops=2)
+    ref = _oracle(wl, sysm, lst, pj, 8, O.PLAIN, n_hops=2)
+    _check(pj, sysm, ref, 8)
+
+
+def test_plain_lj_full_list(gpu):
+    """C1 shape: LJ 12-6 float64 on a full list, edge energy scale 0.5."""
+    wl, sysm, lst, pj = _case("lj_fcc_1k", (5, 5, 5), 8, "plain", harness.LIST_FULL)
+    ref = _oracle(wl, sysm, lst, pj, 8, O.PLAIN)
+    _check(pj, sysm, ref, 8)
+
+
+def test_plain_lj_ghost_rows_float32(gpu):
+    """C5 shape: LJ float32, n_hops = 2 over a full list with ghost rows."""
+    wl, sysm, lst, pj = _case("lj_ghost_262k", (4, 4, 4), 4, "plain", harness.LIST_FULL_GHOST,
+                              n_hops=2)
+    ref = _oracle(wl, sysm, lst, pj, 4, O.PLAIN, n_hops=2)
+    _check(pj, sysm, ref, 4)
+
+
+@pytest.mark.parametrize("name,kind,accum", [
+    ("eam_alloy_131k", harness.LIST_FULL, "plain"),
+    ("eam_alloy_8k", harness.LIST_HALF, "half"),
+    ("lj_fcc_1k", harness.LIST_FULL, "plain"),
+])
+def test_two_sided_scale_and_reproducibility(gpu, name, kind, accum):
+    wl, sysm, lst, pj = _case(name, (4, 4, 4), 8, accum, kind, seed=3, scale=0.5)
+    mode = O.HALF if accum == "half" else O.PLAIN
+    ref = _oracle(wl, sysm, lst, pj, 8, mode)
+    a, fa = _check(pj, sysm, ref, 8, scale=0.5)
+    fa = fa.copy()
+    b = pj.compute()  # the incidence counts returned to zero: same lists, same sums
+    np.testing.assert_array_equal(pj.forces(), fa)
+    assert a.energy == b.energy
+    np.testing.assert_array_equal(a.virial, b.virial)
+    c = pj.compute(fused=True)  # lk_pack_compute runs the entry points in order
+    np.testing.assert_array_equal(pj.forces(), fa)
+    assert c.energy == a.energy
+    bare = pj.compute(eflag=False, vflag=False)
+    assert bare.energy == 0.0 and np.all(bare.virial == 0.0)
+    np.testing.assert_array_equal(pj.forces(), fa)
