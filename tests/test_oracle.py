@@ -433,3 +433,11 @@ def test_pack_atoms_narrows_and_offsets_species():
     np.testing.assert_array_equal(pos8[:2], x)
     np.testing.assert_array_equal(pos4[:2], x.astype(np.float32).astype(np.float64))
     np.testing.assert_array_equal(sp, [0, 1, 0, 0])
+
+
+def test_add_forces_known_answer():
+    """AddForcesFunctor (cpp:175-192): f(i) += scale * F(i) for i < rows only."""
+    f0 = np.array([[1.0, 2.0, 3.0], [4.0, 5.0, 6.0], [7.0, 8.0, 9.0]])
+    mf = np.array([[1.0, 1.0, 1.0], [2.0, 2.0, 2.0], [3.0, 3.0, 3.0]])
+    out = O.add_forces(f0, mf, 2, scale=0.5)
+    np.testing.assert_array_equal(out, [[1.5, 2.5, 3.5], [5.0, 6.0, 7.0], [7.0, 8.0, 9.0]])
