@@ -23,6 +23,13 @@ __device__ __forceinline__ int lanes_below(uint64_t m)
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
 }
 
+// Index of this wave within the block as a wave-uniform (scalar) value: comparisons against it
+// become scalar branches instead of per-lane selects.
+__device__ __forceinline__ int wave_in_block()
+{
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+}
+
 __device__ __forceinline__ int lane_id() { return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0)); }
 
 // Butterfly sum across the 64 lanes; every lane ends with the same value. The order of the

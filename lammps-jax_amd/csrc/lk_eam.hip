@@ -37,8 +37,8 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_density_rows(EamArgs<S> a,
   __shared__ LdsEntry<S> lds[kDensLds];
   __shared__ S part[TPB][W][kWave];
   const Window<S> win = fill_window<S>(lds, kDensLds, a, a.n_el);
-  const int sub = threadIdx.x / (W * kWave);
-  const int wave = (threadIdx.x / kWave) % W;
+  const int sub = wave_in_block() / W;
+  const int wave = wave_in_block() % W;
   const int lane = threadIdx.x & (kWave - 1);
   for (GroupWalk gw = group_walk(ngroups); gw.g < gw.g_end; gw.g += gw.step) {
     const int tile = gw.g * TPB + sub;
@@ -120,8 +120,8 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
   __shared__ double vir[TPB][6][W];
   __shared__ double tpart[TPB][7];  // per tile: pair energy, virial 1..6
   const Window<S> win = fill_window<S>(lds, kForceLds, a, a.n_rtab);
-  const int sub = threadIdx.x / (W * kWave);
-  const int wave = (threadIdx.x / kWave) % W;
+  const int sub = wave_in_block() / W;
+  const int wave = wave_in_block() % W;
   const int lane = threadIdx.x & (kWave - 1);
   for (GroupWalk gw = group_walk(ngroups); gw.g < gw.g_end; gw.g += gw.step) {
     const int tile = gw.g * TPB + sub;
@@ -170,9 +170,17 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
           const S rr = r2 * rinv;
           const Locator<S> L = locate_mul(rr, a.inv_dr, a.nr);
           const int zj = clamp_species(static_cast<int>(r.at.w), a.n_el);
-          const Coef<S> cj = rcoef(win, a, L.node, zj);
-          const Coef<S> ci = rcoef(win, a, L.node, zi);
-          const Coef<S> cp = rcoef(win, a, L.node, a.n_el + pair_row(zi, zj));
+          const int tp = a.n_el + pair_row(zi, zj);
+          Coef<S> cj, ci, cp;
+          if (wave_ballot(L.node < win.lo) == 0) {  // every active lane reads the LDS window
+            cj = rcoef_lds(win, L.node, zj);
+            ci = rcoef_lds(win, L.node, zi);
+            cp = rcoef_lds(win, L.node, tp);
+          } else {
+            cj = rcoef(win, a, L.node, zj);
+            ci = rcoef(win, a, L.node, zi);
+            cp = rcoef(win, a, L.node, tp);
+          }
           // Past the table the non-extrapolated lookups saturate: autodiff slope 0 (eam.py:150).
           const bool inside = !(L.t_raw > S(1));
           const S rhojp = inside ? cslope_t(cj, L.t) * a.inv_dr : S(0);
@@ -184,18 +192,19 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
           const S psip = fpi * rhojp + r.fp * rhoip + phip;
           const S coef = psip * rinv;
           ep += S(0.5) * phi;
-          fx += coef * dx;
-          fy += coef * dy;
-          fz += coef * dz;
-          if (VIRIAL) {
-            const double c = -0.5 * static_cast<double>(coef);
+          const S gx = coef * dx, gy = coef * dy, gz = coef * dz;
+          fx += gx;
+          fy += gy;
+          fz += gz;
+          if (VIRIAL) {  // sum of g (x) d; the factor -1/2 is applied per row
+            const double hx = gx, hy = gy, hz = gz;
             const double ddx = dx, ddy = dy, ddz = dz;
-            w0 += c * ddx * ddx;
-            w1 += c * ddy * ddy;
-            w2 += c * ddz * ddz;
-            w3 += c * ddx * ddy;
-            w4 += c * ddx * ddz;
-            w5 += c * ddy * ddz;
+            w0 += hx * ddx;
+            w1 += hy * ddy;
+            w2 += hz * ddz;
+            w3 += hx * ddy;
+            w4 += hx * ddz;
+            w5 += hy * ddz;
           }
         });
     part[0][sub][wave][lane] = fx;
@@ -209,13 +218,13 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
       w3 = wave_sum(w3);
       w4 = wave_sum(w4);
       w5 = wave_sum(w5);
-      if (lane == 0) {
-        vir[sub][0][wave] = w0;
-        vir[sub][1][wave] = w1;
-        vir[sub][2][wave] = w2;
-        vir[sub][3][wave] = w3;
-        vir[sub][4][wave] = w4;
-        vir[sub][5][wave] = w5;
+      if (lane == 0) {  // pair virial: -1/2 per directed edge of the full list
+        vir[sub][0][wave] = -0.5 * w0;
+        vir[sub][1][wave] = -0.5 * w1;
+        vir[sub][2][wave] = -0.5 * w2;
+        vir[sub][3][wave] = -0.5 * w3;
+        vir[sub][4][wave] = -0.5 * w4;
+        vir[sub][5][wave] = -0.5 * w5;
       }
     }
     __syncthreads();

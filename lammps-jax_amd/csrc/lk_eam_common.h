@@ -111,6 +111,19 @@ __device__ __forceinline__ Coef<S> rcoef(const Window<S> &w, const EamArgs<S> &a
   return Coef<S>{c[0], c[1], c[2], c[3]};
 }
 
+// LDS-only lookup: node m must lie in the window (callers check the whole wave first).
+template <typename S>
+__device__ __forceinline__ Coef<S> rcoef_lds(const Window<S> &w, int m, int tab)
+{
+  const int q = (m - w.lo) * w.T + tab;
+  if constexpr (sizeof(S) == 8) {
+    return coef_from(w.lds[q], w.lds[q + w.T]);
+  } else {
+    const float4 e = w.lds[q];
+    return Coef<S>{e.x, e.y, e.z, e.w};
+  }
+}
+
 template <typename S>
 __device__ __forceinline__ S cvalue(const Coef<S> &c, S t)
 {

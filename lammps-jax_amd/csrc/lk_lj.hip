@@ -43,7 +43,7 @@ __global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
   // No early exit: every block counts itself in for the last-block reduction.
   const int tile = tile_of_block();
   const bool has_rows = tile * kWave < a.num_rows;
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_block();
   const int lane = threadIdx.x & (kWave - 1);
   const int ii = tile * kWave + lane;
   const bool row = has_rows && ii < a.num_rows;

@@ -49,7 +49,7 @@ __global__ __launch_bounds__(W * 64) void k_pack_count(PackArgs a)
   __shared__ int part[W][kWave];
   const int tile = tile_of_block();
   if (tile * kWave >= a.num_rows) return;
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_block();
   const int lane = threadIdx.x & (kWave - 1);
   const int ii = tile * kWave + lane;
   const bool row = ii < a.num_rows;
@@ -166,7 +166,7 @@ __device__ __forceinline__ void pack_write_tile(const PackArgs &a, int tile,
                                                      int *__restrict__ receivers,
                                                      unsigned char *__restrict__ mask)
 {
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_block();
   const int lane = threadIdx.x & (kWave - 1);
   const int ii = tile * kWave + lane;
   const bool row = ii < a.num_rows;

@@ -1,4 +1,4 @@
-// The one-sided step in four launches: pack + EAM (or LJ) energy, forces and virial.
+// The one-sided step in five launches: pack + EAM (or LJ) energy, forces and virial.
 //
 // What PairJaxKokkos::compute does per step (cpp/pair_jax_kokkos.cpp:989-1102) with the full-list
 // row scheme of the model (eam_pallas.py:181-249, full list): pack_atoms, pack_neighbors and the
@@ -6,10 +6,12 @@
 // virial (eam.py:385-398, cpp:175-245). The packed sender/receiver/mask arrays come out exactly as
 // the separate pack writes them (same row-tile positions).
 //
-//   K1 count:  atom records (grid-stride slice), the list walk with the cutoff filter, validity
-//              bits and row counts; on kept pairs the density of the row (float64: from the same
-//              r^2 the filter formed); then F(rho), F'(rho), F' copied to the row's ghost images
-//              (the forward comm of one rank) and the embedding energy of the tile.
+//   K0 atoms:  atom records and species (lk_pack.hip).
+//   K1 count:  the list walk with the cutoff filter (float64: positions gathered from the
+//              records, one 32-byte load per entry), validity bits and row counts; on kept pairs
+//              the density of the row (float64: from the same r^2 the filter formed); then
+//              F(rho), F'(rho), F' copied to the row's ghost images (the forward comm of one
+//              rank) and the embedding energy of the tile.
 //   K2 scan:   tile offsets, demand count and overflow flag (lk_pack.hip).
 //   K3 write:  the compacted write of the packed edges and the tail reset of the slots the
 //              previous step used (lk_pack.hip).
@@ -50,7 +52,7 @@ constexpr int kStepW = 4, kStepTPB = 4;
 // K1. Block-uniform control flow around every barrier: the group walk has the same trip count
 // for all threads of a block, and fill_window is entered by all of them.
 template <typename S, bool EAM>
-__global__ __launch_bounds__(kStepW * kStepTPB * 64) void k_step_count(StepPack p, EamArgs<S> a,
+__global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves_per_eu(8))) void k_step_count(StepPack p, EamArgs<S> a,
                                                                        int ngroups)
 {
   constexpr int W = kStepW, TPB = kStepTPB;
@@ -58,24 +60,10 @@ __global__ __launch_bounds__(kStepW * kStepTPB * 64) void k_step_count(StepPack 
   __shared__ int cpart[TPB][W][kWave];
   __shared__ S rpart[TPB][W][kWave];
 
-  // PackAtomsFunctor (cpp:35-52): atom records for owned and ghost rows, a slice per block.
-  Atom4<S> *atoms = const_cast<Atom4<S> *>(a.atoms);
-  const int span = p.nall < p.max_atoms ? p.nall : p.max_atoms;
-  for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < span; q += gridDim.x * blockDim.x) {
-    const int sp = p.type[q] - 1;
-    Atom4<S> r;
-    r.x = static_cast<S>(p.x[3L * q + 0]);
-    r.y = static_cast<S>(p.x[3L * q + 1]);
-    r.z = static_cast<S>(p.x[3L * q + 2]);
-    r.w = static_cast<S>(sp);
-    atoms[q] = r;
-    p.species[q] = sp;
-  }
-
   Window<S> win{};
   if constexpr (EAM) win = fill_window<S>(lds, kDensLdsFused, a, a.n_el);
-  const int sub = threadIdx.x / (W * kWave);
-  const int wave = (threadIdx.x / kWave) % W;
+  const int sub = wave_in_block() / W;
+  const int wave = wave_in_block() % W;
   const int lane = threadIdx.x & (kWave - 1);
   for (GroupWalk gw = group_walk(ngroups); gw.g < gw.g_end; gw.g += gw.step) {
     const int tile = gw.g * TPB + sub;
@@ -109,11 +97,22 @@ __global__ __launch_bounds__(kStepW * kStepTPB * 64) void k_step_count(StepPack 
         if (j >= p.max_atoms) continue;
         double rsq;
         double xj0, xj1, xj2;
-        {
-#pragma clang fp contract(off)
+        int zj = 0;
+        if constexpr (sizeof(S) == 8) {
+          // float64 records hold the engine's x exactly: one 32-byte gather brings x and species
+          const Atom4<double> rj = reinterpret_cast<const Atom4<double> *>(a.atoms)[j];
+          xj0 = rj.x;
+          xj1 = rj.y;
+          xj2 = rj.z;
+          zj = static_cast<int>(rj.w);
+        } else {
           xj0 = p.x[3L * j + 0];
           xj1 = p.x[3L * j + 1];
           xj2 = p.x[3L * j + 2];
+          if constexpr (EAM) zj = p.type[j] - 1;
+        }
+        {
+#pragma clang fp contract(off)
           const double dx = xi0 - xj0, dy = xi1 - xj1, dz = xi2 - xj2;
           rsq = dx * dx + dy * dy + dz * dz;
         }
@@ -134,8 +133,7 @@ __global__ __launch_bounds__(kStepW * kStepTPB * 64) void k_step_count(StepPack 
           if (r2 < a.cutsq) {  // valid = mask & r_sq < cutoff_sq (eam.py:288)
             const S rr = r2 * rsqrt_nr(r2);
             const Locator<S> L = locate_mul(rr, a.inv_dr, a.nr);
-            const int zj = clamp_species(p.type[j] - 1, a.n_el);
-            rho += cvalue(rcoef(win, a, L.node, zj), L.t);
+            rho += cvalue(rcoef(win, a, L.node, clamp_species(zj, a.n_el)), L.t);
           }
         }
       }
@@ -221,6 +219,8 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   p.ghost_list = h.d_ghost_list;
   const int ntiles = (num_rows + kWave - 1) / kWave;
   const int ngroups = ntiles > 0 ? (ntiles + kStepTPB - 1) / kStepTPB : 1;
+  // K0: atom records and species (the count pass gathers float64 records)
+  if (hipError_t e0 = launch_pack_atoms(h, s, x, type, nall); e0 != hipSuccess) return e0;
   {
     StageTimer timer(h, s, "step_count");
     const int grid = persistent_grid(ngroups, 2, h.num_cus);

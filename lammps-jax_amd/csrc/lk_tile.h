@@ -82,7 +82,8 @@ struct OwnEdges {
 
 // Software-pipelined walk over this wave's edges: the receiver of edge t+2 and the neighbour
 // record of edge t+1 are in flight while edge t is computed. fetch(j) returns the record of
-// neighbour j; use(rec) consumes it (rec.valid false on lanes without an edge).
+// neighbour j; use(rec) consumes it (rec.valid false on lanes without an edge). Unrolled by two
+// so the two records in flight live in fixed registers (no copy per edge).
 template <int W, class Rec, class Fetch, class Use>
 __device__ __forceinline__ void for_tile_edges_pipelined(int cnt, long base, int wave,
                                                          int max_edges,
@@ -90,23 +91,25 @@ __device__ __forceinline__ void for_tile_edges_pipelined(int cnt, long base, int
                                                          Fetch &&fetch, Use &&use)
 {
   OwnEdges<W> oe{cnt, base, wave, max_edges};
-  long e0 = -1, e1 = -1;
-  bool h0 = oe.next(e0);
-  if (!h0) return;
-  const int j0 = e0 >= 0 ? receivers[e0] : -1;
-  bool h1 = oe.next(e1);
-  int j1 = (h1 && e1 >= 0) ? receivers[e1] : -1;
-  Rec r0 = fetch(j0);
+  long e = -1;
+  if (!oe.next(e)) return;
+  const int jA = e >= 0 ? receivers[e] : -1;
+  bool hB = oe.next(e);
+  int jB = (hB && e >= 0) ? receivers[e] : -1;
+  Rec rA = fetch(jA);
   while (true) {
-    Rec r1 = fetch(j1);
-    long e2 = -1;
-    const bool h2 = h1 && oe.next(e2);
-    const int j2 = (h2 && e2 >= 0) ? receivers[e2] : -1;
-    use(r0);
-    if (!h1) break;
-    r0 = r1;
-    j1 = j2;
-    h1 = h2;
+    const Rec rB = fetch(jB);
+    const bool hC = hB && oe.next(e);
+    const int jC = (hC && e >= 0) ? receivers[e] : -1;
+    use(rA);
+    if (!hB) break;
+    rA = fetch(jC);
+    const bool hD = hC && oe.next(e);
+    const int jD = (hD && e >= 0) ? receivers[e] : -1;
+    use(rB);
+    if (!hC) break;
+    jB = jD;
+    hB = hD;
   }
 }
 
