@@ -50,6 +50,11 @@ def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: 
         return 8 * R + 4 * E + rec * A + 48 * N
     if stage == "forward_fp":
         return (A - N) * (4 + 2 * S)
+    if stage == "step_pack":
+        # list + row data, gathered atom records, validity bits and row counts, F' (owned +
+        # ghost images) and rho out, the packed arrays out
+        return (8 * R + 4 * entries + (rec + 4) * A + 4 * R * words + 8 * R + S * A + S * N
+                + 9 * E)
     if stage == "step_count":
         # list + row data, x and type of every atom once, atom records and species out,
         # validity bits, row counts, F' (owned + ghost images) and rho out

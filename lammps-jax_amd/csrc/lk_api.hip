@@ -55,7 +55,7 @@ void free_all(Handle &h)
                   h.d_tile_off,  h.d_bits,      h.d_fp,          h.d_rho,       h.d_partials,
                   h.d_result,    h.d_ghost_owner, h.d_ghost_off, h.d_ghost_list, h.d_done,
                   h.d_deg,       h.d_inc_loc,   h.d_inc_part,    h.d_inc_tmp,   h.d_inc,
-                  h.d_rho_part,  h.d_epair};
+                  h.d_rho_part,  h.d_epair,     h.d_pack_state};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -192,6 +192,7 @@ int lk_create(const lk_contract *c, lk_handle **out)
   if ((e = dalloc(&h.d_partials, 8 * tiles)) != hipSuccess) return hip_fail(h, e, "hipMalloc(partials)");
   if ((e = dalloc(&h.d_result, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(result)");
   if ((e = dalloc(&h.d_done, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(done)");
+  if ((e = dalloc(&h.d_pack_state, 2)) != hipSuccess) return hip_fail(h, e, "hipMalloc(pack state)");
   if ((e = hipHostMalloc(reinterpret_cast<void **>(&h.h_result), sizeof(lk::StepResult))) != hipSuccess)
     return hip_fail(h, e, "hipHostMalloc(result)");
   std::memset(h.h_result, 0, sizeof(lk::StepResult));
@@ -207,6 +208,7 @@ int lk_create(const lk_contract *c, lk_handle **out)
   (void)hipMemset(h.d_partials, 0, 8 * tiles * sizeof(double));
   (void)hipMemset(h.d_result, 0, sizeof(lk::StepResult));
   (void)hipMemset(h.d_done, 0, sizeof(int));
+  (void)hipMemset(h.d_pack_state, 0, 2 * sizeof(int));
   if (int rc = ensure_bits(h, 128)) return rc;
   e = hipDeviceSynchronize();
   if (e != hipSuccess) return hip_fail(h, e, "initialising buffers");

@@ -119,6 +119,7 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
   __shared__ S part[4][TPB][W][kWave];
   __shared__ double vir[TPB][6][W];
   __shared__ double tpart[TPB][7];  // per tile: pair energy, virial 1..6
+  fused_tail_reset(a.pack);
   const Window<S> win = fill_window<S>(lds, kForceLds, a, a.n_rtab);
   const int sub = wave_in_block() / W;
   const int wave = wave_in_block() % W;
@@ -268,7 +269,7 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
     }
   }
   finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done,
-                      reinterpret_cast<double *>(lds));
+                      reinterpret_cast<double *>(lds), a.pack);
 }
 
 template <typename S>

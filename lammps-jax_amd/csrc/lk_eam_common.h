@@ -31,6 +31,19 @@ __device__ __forceinline__ Coef<double> coef_from(double2 e0, double2 e1)
   return c;
 }
 
+__device__ __forceinline__ void fused_tail_reset(const FusedPack &fp)
+{
+  if (!fp.counter) return;
+  const long c = fp.counter[0];
+  const long count = c < fp.max_edges ? c : fp.max_edges;
+  for (long e = count + static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < fp.reset_end;
+       e += static_cast<long>(gridDim.x) * blockDim.x) {
+    fp.senders[e] = fp.pad;
+    fp.receivers[e] = fp.pad;
+    fp.mask[e] = 0;
+  }
+}
+
 template <typename S>
 struct EamArgs {
   const Atom4<S> *atoms;
@@ -62,6 +75,7 @@ struct EamArgs {
   int *done;
   int ntiles;
   int flags;
+  FusedPack pack;
 };
 
 // Species index into the tables. XLA clamps out-of-range gathers, so types past the table's
@@ -188,7 +202,8 @@ inline int persistent_grid(int ngroups, int blocks_per_cu, int num_cus)
 __device__ __forceinline__ void finalize_last_block(const double *partials, int ntiles,
                                                     double escale, double vscale, int flags,
                                                     StepResult *result, int *done,
-                                                    double *scratch)
+                                                    double *scratch,
+                                                    const FusedPack &pack = FusedPack{})
 {
   __shared__ int last_block;
   if (threadIdx.x < kWave) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -215,6 +230,11 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
     result->energy = (flags & LK_ENERGY) ? escale * scratch[0] : 0.0;
     for (int c = 0; c < 6; ++c)
       result->virial[c] = (flags & LK_VIRIAL) ? vscale * scratch[(c + 1) * nt] : 0.0;
+    if (pack.counter) {
+      result->edge_count = pack.counter[0];
+      result->edge_overflow = pack.counter[0] > pack.max_edges ? 1 : 0;
+      result->ghost_sender = pack.counter[1];
+    }
     *done = 0;  // ready for the next launch
   }
 }
@@ -254,6 +274,7 @@ inline EamArgs<S> eam_args(Handle &h, int nlocal, double scale, double *f)
   a.done = h.d_done;
   a.ntiles = (h.packed_rows + kWave - 1) / kWave;
   a.flags = 0;
+  a.pack = FusedPack{};
   return a;
 }
 

@@ -23,6 +23,19 @@ struct StepResult {
   int pad;
 };
 
+// The part of the fused one-sided pack that the force sweep completes: the tail reset of the
+// slots the previous step used (ResetEdgeTailFunctor, cpp/pair_jax_kokkos.cpp:157-173) and the
+// demand count, overflow and ghost-sender flags of the step result. counter == nullptr: unused.
+struct FusedPack {
+  const int *counter = nullptr;  // [0] edge demand count (atomic in the pack), [1] ghost sender
+  int *senders = nullptr;
+  int *receivers = nullptr;
+  unsigned char *mask = nullptr;
+  int max_edges = 0;
+  int pad = 0;                   // padding index (max_atoms)
+  long reset_end = 0;            // slots below it held the previous step's edges
+};
+
 struct Handle {
   lk_contract contract{};
   int accum = LK_ACCUM_PLAIN;
@@ -72,6 +85,7 @@ struct Handle {
   int *d_ghost_list = nullptr;  // [nghost] ghost rows, increasing within each owner
   int ghost_off_cap = 0;
   int *d_done = nullptr;        // block counter of the last-block result reduction
+  int *d_pack_state = nullptr;  // fused one-sided step: [0] edge demand count, [1] ghost sender
   int ghost_cap = 0;
   int ghost_n = 0;
   int ghost_nlocal = 0;
@@ -126,7 +140,8 @@ class StageTimer {
 };
 
 // launchers (stream-ordered, no host synchronisation)
-hipError_t launch_pack_atoms(Handle &h, hipStream_t s, const double *x, const int *type, int nall);
+hipError_t launch_pack_atoms(Handle &h, hipStream_t s, const double *x, const int *type, int nall,
+                             int *clear = nullptr);
 hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const int *ilist,
                              const int *numneigh, const int *neighbors, long stride, int num_rows,
                              int maxneighs, int nlocal, int duplicate, int half_edges,
@@ -134,7 +149,7 @@ hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const in
 hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
                                double *f, int flags);
 hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
-                              double *f, int flags);
+                              double *f, int flags, const FusedPack &pack = FusedPack{});
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles);
 
 hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,

@@ -30,6 +30,7 @@ struct LjArgs {
   int *done;
   int ntiles;
   int flags;
+  FusedPack pack;
 };
 
 // One-sided full list: the row atom takes the whole pair force 2 * de/d(r^2) * (x_j - x_i) and
@@ -41,6 +42,7 @@ __global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
   __shared__ double vir[6][W];
   __shared__ double scratch[7 * W * kWave];
   // No early exit: every block counts itself in for the last-block reduction.
+  fused_tail_reset(a.pack);
   const int tile = tile_of_block();
   const bool has_rows = tile * kWave < a.num_rows;
   const int wave = wave_in_block();
@@ -139,12 +141,13 @@ __global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
     a.partials[8L * tile + 1 + lane] = v;
   }
   }
-  finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done, scratch);
+  finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done, scratch,
+                      a.pack);
 }
 
 template <typename S>
 static hipError_t lj_onesided(Handle &h, hipStream_t s, int nlocal, double scale, double *f,
-                              int flags)
+                              int flags, const FusedPack &pack)
 {
   LjArgs<S> a;
   a.atoms = static_cast<const Atom4<S> *>(h.d_atoms);
@@ -168,6 +171,7 @@ static hipError_t lj_onesided(Handle &h, hipStream_t s, int nlocal, double scale
   const int ntiles = (h.packed_rows + kWave - 1) / kWave;
   a.ntiles = ntiles;
   a.flags = flags;
+  a.pack = pack;
   // One launch even with no rows: its last block writes the step result.
   const int grid = tile_grid(ntiles > 0 ? ntiles : 1);
   StageTimer timer(h, s, "lj_rows");
@@ -179,10 +183,11 @@ static hipError_t lj_onesided(Handle &h, hipStream_t s, int nlocal, double scale
 }
 
 hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int /*nghost*/, double scale,
-                              double *f, int flags)
+                              double *f, int flags, const FusedPack &pack)
 {
-  if (h.contract.precision == LK_FLOAT64) return lj_onesided<double>(h, s, nlocal, scale, f, flags);
-  return lj_onesided<float>(h, s, nlocal, scale, f, flags);
+  if (h.contract.precision == LK_FLOAT64)
+    return lj_onesided<double>(h, s, nlocal, scale, f, flags, pack);
+  return lj_onesided<float>(h, s, nlocal, scale, f, flags, pack);
 }
 
 }  // namespace lk

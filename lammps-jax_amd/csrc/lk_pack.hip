@@ -22,13 +22,17 @@ namespace lk {
 
 // PackAtomsFunctor (cpp/pair_jax_kokkos.cpp:35-52): positions narrowed to the contract precision,
 // species = type - 1. The record keeps the species beside the position for one-gather lookups.
+// `clear` (optional, two ints) is zeroed for the step that follows: the fused pack's demand
+// counter and ghost-sender flag.
 template <typename S>
 __global__ __launch_bounds__(256) void k_pack_atoms(const double *__restrict__ x,
                                                      const int *__restrict__ type, int span,
                                                      Atom4<S> *__restrict__ atoms,
-                                                     int *__restrict__ species)
+                                                     int *__restrict__ species,
+                                                     int *__restrict__ clear)
 {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (clear && i < 2) clear[i] = 0;
   if (i >= span) return;
   const int sp = type[i] - 1;
   Atom4<S> a;
@@ -237,18 +241,19 @@ hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int
   return hipGetLastError();
 }
 
-hipError_t launch_pack_atoms(Handle &h, hipStream_t s, const double *x, const int *type, int nall)
+hipError_t launch_pack_atoms(Handle &h, hipStream_t s, const double *x, const int *type, int nall,
+                             int *clear)
 {
   const int span = nall < h.contract.max_atoms ? nall : h.contract.max_atoms;
-  if (span <= 0) return hipSuccess;
-  const int blocks = (span + 255) / 256;
+  if (span <= 0 && !clear) return hipSuccess;
+  const int blocks = span > 0 ? (span + 255) / 256 : 1;
   StageTimer timer(h, s, "pack_atoms");
   if (h.contract.precision == LK_FLOAT64)
     hipLaunchKernelGGL(k_pack_atoms<double>, dim3(blocks), dim3(256), 0, s, x, type, span,
-                       static_cast<Atom4<double> *>(h.d_atoms), h.d_species);
+                       static_cast<Atom4<double> *>(h.d_atoms), h.d_species, clear);
   else
     hipLaunchKernelGGL(k_pack_atoms<float>, dim3(blocks), dim3(256), 0, s, x, type, span,
-                       static_cast<Atom4<float> *>(h.d_atoms), h.d_species);
+                       static_cast<Atom4<float> *>(h.d_atoms), h.d_species, clear);
   return hipGetLastError();
 }
 

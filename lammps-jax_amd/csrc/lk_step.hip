@@ -1,33 +1,35 @@
-// The one-sided step in five launches: pack + EAM (or LJ) energy, forces and virial.
+// The one-sided step in three launches: pack + EAM (or LJ) energy, forces and virial.
 //
 // What PairJaxKokkos::compute does per step (cpp/pair_jax_kokkos.cpp:989-1102) with the full-list
 // row scheme of the model (eam_pallas.py:181-249, full list): pack_atoms, pack_neighbors and the
 // tail reset (cpp:35-173, 794-874), the density and embedding (eam.py:298-321), the force and
-// virial (eam.py:385-398, cpp:175-245). The packed sender/receiver/mask arrays come out exactly as
-// the separate pack writes them (same row-tile positions).
+// virial (eam.py:385-398, cpp:175-245).
 //
-//   K0 atoms:  atom records and species (lk_pack.hip).
-//   K1 count:  the list walk with the cutoff filter (float64: positions gathered from the
-//              records, one 32-byte load per entry), validity bits and row counts; on kept pairs
-//              the density of the row (float64: from the same r^2 the filter formed); then
-//              F(rho), F'(rho), F' copied to the row's ghost images (the forward comm of one
-//              rank) and the embedding energy of the tile.
-//   K2 scan:   tile offsets, demand count and overflow flag (lk_pack.hip).
-//   K3 write:  the compacted write of the packed edges and the tail reset of the slots the
-//              previous step used (lk_pack.hip).
-//   K4 force:  the force sweep over the packed receivers (lk_eam.hip, lk_lj.hip); its last block
+//   K0 atoms:  atom records and species (lk_pack.hip); clears the pack's demand counter.
+//   K1 pack:   per 64-row tile, the list walk with the cutoff filter (float64: positions
+//              gathered from the records, one 32-byte load per entry), validity bits and row
+//              counts; on kept pairs the density of the row (float64: from the same r^2 the
+//              filter formed); then F(rho), F'(rho), F' copied to the row's ghost images (the
+//              forward comm of one rank) and the embedding energy of the tile. The tile then
+//              claims its slot range with one atomic add on the demand counter (the reference's
+//              packer claims slots the same way, per entry) and writes its edges in the
+//              row-tile order while its list lines are still in cache.
+//   K2 force:  the force sweep over the packed receivers (lk_eam.hip, lk_lj.hip); it also
+//              resets the slots the previous step used past the new count, and its last block
 //              reduces the tile partials in a fixed order into the step result.
+// The packed arrays equal the reference's after canonical ordering; the tiles' order in them
+// follows the atomic claims. Per-row sums never depend on it (each row's edges keep their order
+// inside its tile), so energies, forces and virials are bitwise reproducible.
 
 #include "lk_eam_common.h"
 #include "lk_pack.h"
 
 namespace lk {
 
-// Inputs and pack outputs of the count kernel besides the model arguments.
+// Inputs and pack outputs of the pack kernel besides the model arguments.
 struct StepPack {
   const double *x;
   const int *type;
-  int nall;
   const int *ilist;
   const int *numneigh;
   const int *neighbors;
@@ -35,33 +37,41 @@ struct StepPack {
   int num_rows;
   int maxneighs;
   int max_atoms;
+  int max_edges;
   double cutsq;
   int pitch;
   uint32_t *bits;
   int *row_count;
   int *row_atom;
-  int *tile_count;
-  int *tile_flags;
-  int *species;
+  int *tile_base;
+  int *state;  // [0] demand counter, [1] ghost-sender flag (cleared by K0)
+  int *senders;
+  int *receivers;
+  unsigned char *mask;
   const int *ghost_off;
   const int *ghost_list;
 };
 
 constexpr int kStepW = 4, kStepTPB = 4;
+constexpr int kStepLds = 3584;     // table window entries: 56 KB (two blocks per CU)
+constexpr int kStepMaxWords = 8;   // validity words kept in LDS for the write (256 list slots)
 
 // K1. Block-uniform control flow around every barrier: the group walk has the same trip count
 // for all threads of a block, and fill_window is entered by all of them.
 template <typename S, bool EAM>
-__global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves_per_eu(8))) void k_step_count(StepPack p, EamArgs<S> a,
-                                                                       int ngroups)
+__global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves_per_eu(8)))
+void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
 {
   constexpr int W = kStepW, TPB = kStepTPB;
-  __shared__ LdsEntry<S> lds[EAM ? kDensLdsFused : 1];
+  __shared__ LdsEntry<S> lds[EAM ? kStepLds : 1];
   __shared__ int cpart[TPB][W][kWave];
   __shared__ S rpart[TPB][W][kWave];
+  __shared__ uint32_t sbits[TPB][kStepMaxWords][kWave];
+  __shared__ int scnt[TPB][kWave];
+  __shared__ int sbase[TPB];
 
   Window<S> win{};
-  if constexpr (EAM) win = fill_window<S>(lds, kDensLdsFused, a, a.n_el);
+  if constexpr (EAM) win = fill_window<S>(lds, kStepLds, a, a.n_el);
   const int sub = wave_in_block() / W;
   const int wave = wave_in_block() % W;
   const int lane = threadIdx.x & (kWave - 1);
@@ -85,6 +95,7 @@ __global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves
     }
     const int nn_max = wave_max_int(nn);
     const int nwords = (nn_max + 31) >> 5;
+    const bool lds_bits = nwords <= kStepMaxWords;
     int cnt = 0;
     S rho = S(0);
     for (int w = wave; w < nwords; w += W) {
@@ -138,6 +149,7 @@ __global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves
         }
       }
       if (row) p.bits[static_cast<long>(w) * p.pitch + ii] = word;
+      if (lds_bits) sbits[sub][w][lane] = word;
     }
     cpart[sub][wave][lane] = cnt;
     if constexpr (EAM) rpart[sub][wave][lane] = rho;
@@ -154,6 +166,7 @@ __global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves
         p.row_count[ii] = cnt;
         p.row_atom[ii] = i;
       }
+      scnt[sub][lane] = cnt;
       const int total = wave_sum(cnt);
       const uint64_t gmask = wave_ballot(i >= a.nlocal && cnt > 0);
       double e_own = 0.0;
@@ -172,9 +185,47 @@ __global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves
       }
       const double esum = wave_sum(e_own);
       if (lane == 0 && tile * kWave < p.num_rows) {
-        p.tile_count[tile] = total;
-        p.tile_flags[tile] = gmask != 0 ? 1 : 0;
+        // the tile's slots [base, base + total): one claim per tile (cpp:102-110 claims per entry)
+        const int base = atomicAdd(&p.state[0], total);
+        sbase[sub] = base;
+        p.tile_base[tile] = base;
+        if (gmask != 0) atomicOr(&p.state[1], 1);
         a.partials[8L * tile + 0] = esum;
+      }
+    }
+    __syncthreads();
+    // Compacted write, W waves per tile (as k_pack_write): every wave pops its row's kept
+    // entries in order; wave k % W writes ordinal k, the rows with more than k entries (ballot M)
+    // storing popcount(M) consecutive edges. The list slot is read again from cache.
+    {
+      const int c = scnt[sub][lane];
+      const long base = sbase[sub];
+      int wd = 0;
+      uint32_t word = c > 0 ? (lds_bits ? sbits[sub][0][lane] : p.bits[ii]) : 0u;
+      long cursor = 0;
+      for (int k = 0;; ++k) {
+        const bool active = k < c;
+        const uint64_t M = wave_ballot(active);
+        if (M == 0) break;
+        if (active) {
+          while (word == 0) {
+            ++wd;
+            word = lds_bits ? sbits[sub][wd][lane] : p.bits[static_cast<long>(wd) * p.pitch + ii];
+          }
+          const int b = __builtin_ctz(word);
+          word &= word - 1u;
+          if ((k % W) == wave) {
+            const int jj = wd * 32 + b;
+            const int j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
+            const long e = base + cursor + lanes_below(M);
+            if (e < p.max_edges) {  // past the capacity the count still reports the demand
+              p.senders[e] = i;
+              p.receivers[e] = j;
+              p.mask[e] = 1;
+            }
+          }
+        }
+        cursor += __popcll(M);
       }
     }
     __syncthreads();
@@ -199,7 +250,6 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   StepPack p;
   p.x = x;
   p.type = type;
-  p.nall = nall;
   p.ilist = ilist;
   p.numneigh = numneigh;
   p.neighbors = neighbors;
@@ -207,37 +257,45 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   p.num_rows = num_rows;
   p.maxneighs = maxneighs;
   p.max_atoms = h.contract.max_atoms;
+  p.max_edges = h.contract.max_edges;
   p.cutsq = h.contract.cutoff * h.contract.cutoff;
   p.pitch = h.contract.max_atoms;
   p.bits = h.d_bits;
   p.row_count = h.d_row_count;
   p.row_atom = h.d_row_atom;
-  p.tile_count = h.d_tile_count;
-  p.tile_flags = h.d_tile_count + (h.contract.max_atoms / kWave + 2);
-  p.species = h.d_species;
+  p.tile_base = h.d_tile_off;
+  p.state = h.d_pack_state;
+  p.senders = h.d_senders;
+  p.receivers = h.d_receivers;
+  p.mask = h.d_mask;
   p.ghost_off = nghost > 0 ? h.d_ghost_off : nullptr;
   p.ghost_list = h.d_ghost_list;
   const int ntiles = (num_rows + kWave - 1) / kWave;
   const int ngroups = ntiles > 0 ? (ntiles + kStepTPB - 1) / kStepTPB : 1;
-  // K0: atom records and species (the count pass gathers float64 records)
-  if (hipError_t e0 = launch_pack_atoms(h, s, x, type, nall); e0 != hipSuccess) return e0;
-  {
-    StageTimer timer(h, s, "step_count");
+  // K0: atom records and species; zeroes the demand counter and the ghost-sender flag
+  if (hipError_t e0 = launch_pack_atoms(h, s, x, type, nall, h.d_pack_state); e0 != hipSuccess)
+    return e0;
+  if (ntiles > 0) {
+    StageTimer timer(h, s, "step_pack");
     const int grid = persistent_grid(ngroups, 2, h.num_cus);
-    hipLaunchKernelGGL((k_step_count<S, EAM>), dim3(grid), dim3(kStepW * kStepTPB * kWave), 0, s,
+    hipLaunchKernelGGL((k_step_pack<S, EAM>), dim3(grid), dim3(kStepW * kStepTPB * kWave), 0, s,
                        p, a, ngroups);
   }
-  {
-    StageTimer timer(h, s, "tile_scan");
-    (void)launch_tile_scan(h, s, p.tile_flags, ntiles);
-  }
-  // full list, one-sided: no duplication, no half filter, no boundary rule
-  hipError_t e = launch_pack_write(
-      h, s, pack_args(h, x, ilist, numneigh, neighbors, stride, num_rows, maxneighs, nlocal, 0, 0, 0));
   ++h.pack_serial;
-  if (e != hipSuccess) return e;
-  if constexpr (EAM) return launch_eam_force(h, s, a, flags);
-  return launch_lj_onesided(h, s, nlocal, nghost, scale, f, flags);
+  FusedPack fp;
+  fp.counter = h.d_pack_state;
+  fp.senders = h.d_senders;
+  fp.receivers = h.d_receivers;
+  fp.mask = h.d_mask;
+  fp.max_edges = h.contract.max_edges;
+  fp.pad = h.contract.max_atoms;
+  fp.reset_end = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
+                                                            : h.contract.max_edges;
+  if constexpr (EAM) {
+    a.pack = fp;
+    return launch_eam_force(h, s, a, flags);
+  }
+  return launch_lj_onesided(h, s, nlocal, nghost, scale, f, flags, fp);
 }
 
 hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lk_testutil import fold_ghosts, rel_err
+from lk_testutil import canonical, fold_ghosts, rel_err
 from lammps_jax_amd import harness, systems
 from lammps_jax_amd.pair import PairJax
 
@@ -114,15 +114,19 @@ def test_edge_capacity_error_message(gpu):
 
 @pytest.mark.parametrize("name", ["eam_alloy_131k", "lj_fcc_1k"])
 def test_fused_step_writes_the_same_packed_arrays(gpu, name):
-    """lk_pack_compute stores the packed edges at exactly the positions lk_pack_edges does."""
+    """lk_pack_compute packs the same edges as lk_pack_edges (canonical order; its tiles are
+    placed by atomic claims), with no holes below the count and padding above it."""
     cells = (5, 5, 5)
     wl, sysm, lst, fused = _case(name, cells, 8, seed=6, fused=True)
     _, _, _, split = _case(name, cells, 8, seed=6, fused=False)
     a = fused.compute()
     b = split.compute()
     assert a.edge_count == b.edge_count and a.edge_overflow == b.edge_overflow == 0
-    for u, v in zip(fused.edges(), split.edges()):
-        np.testing.assert_array_equal(u, v)
+    (s, r, m), (s2, r2, m2) = fused.edges(), split.edges()
+    np.testing.assert_array_equal(canonical(s, r, m), canonical(s2, r2, m2))
+    c = a.edge_count
+    assert np.all(m[:c] == 1) and not m[c:].any()
+    assert np.all(s[c:] == fused.max_atoms) and np.all(r[c:] == fused.max_atoms)
     fa, fb = fused.forces(), split.forces()
     assert rel_err(fa, fb) < 1e-12
     assert a.energy == pytest.approx(b.energy, rel=1e-12)
