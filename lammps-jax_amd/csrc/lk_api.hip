@@ -196,6 +196,8 @@ int lk_create(const lk_contract *c, lk_handle **out)
   if ((e = hipHostMalloc(reinterpret_cast<void **>(&h.h_result), sizeof(lk::StepResult))) != hipSuccess)
     return hip_fail(h, e, "hipHostMalloc(result)");
   std::memset(h.h_result, 0, sizeof(lk::StepResult));
+  if ((e = hipHostGetDevicePointer(reinterpret_cast<void **>(&h.d_host_result), h.h_result, 0)) != hipSuccess)
+    return hip_fail(h, e, "hipHostGetDevicePointer(result)");
   // Padding contract (cpp:368-383): unpacked slots index max_atoms with the mask off.
   const long fill_blocks = static_cast<long>((E + 255) / 256);
   hipLaunchKernelGGL(k_fill_int, dim3(fill_blocks), dim3(256), 0, 0, h.d_senders, static_cast<long>(E), c->max_atoms);
@@ -383,6 +385,7 @@ int lk_pack_atoms(lk_handle *w, void *stream, const double *x, const int *type, 
   h.x_last = x;
   hipError_t e = lk::launch_pack_atoms(h, as_stream(stream), x, type, nall);
   if (e != hipSuccess) return hip_fail(h, e, "pack_atoms");
+  h.result_mirrored = false;
   return LK_OK;
 }
 
@@ -417,6 +420,7 @@ int lk_pack_edges(lk_handle *w, void *stream, const double *x, const int *ilist,
                                        nb_stride, static_cast<int>(rows), max_neighbors_per_atom,
                                        nlocal, duplicate, half_filter, unique);
   if (e != hipSuccess) return hip_fail(h, e, "pack_edges");
+  h.result_mirrored = false;
   return LK_OK;
 }
 
@@ -455,6 +459,7 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
     e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, h.x_last);
   }
   if (e != hipSuccess) return hip_fail(h, e, "compute");
+  h.result_mirrored = true;
   return LK_OK;
 }
 
@@ -497,6 +502,7 @@ int lk_pack_compute(lk_handle *w, void *stream, const double *x, const int *type
                                           neighbors, nb_stride, static_cast<int>(rows),
                                           max_neighbors_per_atom, nlocal, nghost, flags, scale, f);
   if (e != hipSuccess) return hip_fail(h, e, "fused step");
+  h.result_mirrored = true;
   return LK_OK;
 }
 
@@ -505,7 +511,11 @@ int lk_step_result(lk_handle *w, void *stream, lk_step_info *out)
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
   hipStream_t s = as_stream(stream);
-  hipError_t e = hipMemcpyAsync(h.h_result, h.d_result, sizeof(lk::StepResult), hipMemcpyDeviceToHost, s);
+  // After a model pass its last block has already written the pinned copy; a pack alone
+  // leaves the counts on the device.
+  hipError_t e = hipSuccess;
+  if (!h.result_mirrored)
+    e = hipMemcpyAsync(h.h_result, h.d_result, sizeof(lk::StepResult), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_fail(h, e, "step result");
   for (const auto &p : h.pending) {

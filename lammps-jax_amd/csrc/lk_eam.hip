@@ -269,7 +269,7 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
     }
   }
   finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done,
-                      reinterpret_cast<double *>(lds), a.pack);
+                      reinterpret_cast<double *>(lds), a.pack, a.mirror);
 }
 
 template <typename S>

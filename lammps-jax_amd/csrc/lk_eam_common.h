@@ -76,6 +76,7 @@ struct EamArgs {
   int ntiles;
   int flags;
   FusedPack pack;
+  StepResult *mirror;  // device view of the host's pinned result
 };
 
 // Species index into the tables. XLA clamps out-of-range gathers, so types past the table's
@@ -203,7 +204,8 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
                                                     double escale, double vscale, int flags,
                                                     StepResult *result, int *done,
                                                     double *scratch,
-                                                    const FusedPack &pack = FusedPack{})
+                                                    const FusedPack &pack = FusedPack{},
+                                                    StepResult *mirror = nullptr)
 {
   __shared__ int last_block;
   if (threadIdx.x < kWave) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -235,6 +237,7 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
       result->edge_overflow = pack.counter[0] > pack.max_edges ? 1 : 0;
       result->ghost_sender = pack.counter[1];
     }
+    if (mirror) *mirror = *result;  // the host's pinned copy: no separate readback copy
     *done = 0;  // ready for the next launch
   }
 }
@@ -275,6 +278,7 @@ inline EamArgs<S> eam_args(Handle &h, int nlocal, double scale, double *f)
   a.ntiles = (h.packed_rows + kWave - 1) / kWave;
   a.flags = 0;
   a.pack = FusedPack{};
+  a.mirror = h.d_host_result;
   return a;
 }
 

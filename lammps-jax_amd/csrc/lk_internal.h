@@ -78,6 +78,8 @@ struct Handle {
   int partial_slots = 0;
   StepResult *d_result = nullptr;
   StepResult *h_result = nullptr;  // pinned
+  StepResult *d_host_result = nullptr;  // device view of h_result (written by the last block)
+  bool result_mirrored = false;         // the last enqueued work ends with that write
 
   // single-rank comm description (ghost -> owner), uploaded by lk_set_ghost_map
   int *d_ghost_owner = nullptr;

@@ -31,6 +31,7 @@ struct LjArgs {
   int ntiles;
   int flags;
   FusedPack pack;
+  StepResult *mirror;
 };
 
 // One-sided full list: the row atom takes the whole pair force 2 * de/d(r^2) * (x_j - x_i) and
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
   }
   }
   finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done, scratch,
-                      a.pack);
+                      a.pack, a.mirror);
 }
 
 template <typename S>
@@ -172,6 +173,7 @@ static hipError_t lj_onesided(Handle &h, hipStream_t s, int nlocal, double scale
   a.ntiles = ntiles;
   a.flags = flags;
   a.pack = pack;
+  a.mirror = h.d_host_result;
   // One launch even with no rows: its last block writes the step result.
   const int grid = tile_grid(ntiles > 0 ? ntiles : 1);
   StageTimer timer(h, s, "lj_rows");

@@ -452,7 +452,7 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
     __syncthreads();
   }
   finalize_last_block(m.partials, t.nblk, m.scale, 1.0, m.flags, m.result, m.done,
-                      reinterpret_cast<double *>(lds));
+                      reinterpret_cast<double *>(lds), FusedPack{}, m.mirror);
 }
 
 template <typename S>
@@ -465,6 +465,7 @@ struct LjModel {
   StepResult *result;
   int *done;
   int flags;
+  StepResult *mirror;
 };
 
 // LJ 12-6 plain (examples/export_model.py:16-50): e per edge on the sender row, g = 2 de/d(r^2) d
@@ -521,7 +522,8 @@ __global__ __launch_bounds__(kRowBlock) void k_lj_inc(LjModel<S> m, TwoSided t)
     }
     __syncthreads();
   }
-  finalize_last_block(m.partials, t.nblk, m.scale, 1.0, m.flags, m.result, m.done, scratch);
+  finalize_last_block(m.partials, t.nblk, m.scale, 1.0, m.flags, m.result, m.done, scratch,
+                      FusedPack{}, m.mirror);
 }
 
 static int grid_for(const Handle &h, long work, int per_block, int blocks_per_cu)
@@ -635,6 +637,7 @@ static hipError_t lj_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost,
   m.result = h.d_result;
   m.done = h.d_done;
   m.flags = flags;
+  m.mirror = h.d_host_result;
   TwoSided t = two_sided_args(h, nlocal, nghost, x);
   const int grid = grid_for(h, t.nblk > 0 ? t.nblk : 1, 1, 2);
   StageTimer timer(h, s, "lj_rows");
