@@ -194,19 +194,38 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
       }
     }
     __syncthreads();
-    // Compacted write, W waves per tile (as k_pack_write): every wave pops its row's kept
-    // entries in order; wave k % W writes ordinal k, the rows with more than k entries (ballot M)
-    // storing popcount(M) consecutive edges. The list slot is read again from cache.
+    // Compacted write: ordinal k of every row (rows with more than k entries form the ballot M)
+    // occupies popcount(M) consecutive slots after the slots of the ordinals below k. Wave w
+    // writes one contiguous range of ordinals [k0, k1): its first slot is the sum over the rows
+    // of min(count, k0); each lane skips its row's first k0 kept entries once, then pops them in
+    // order. The list slot is read again from cache.
     {
       const int c = scnt[sub][lane];
       const long base = sbase[sub];
+      const int kmax = wave_max_int(c);
+      const int per = (kmax + W - 1) / W;
+      const int k0 = min(wave * per, kmax);
+      const int k1 = min(k0 + per, kmax);
+      long cursor = wave_sum(min(c, k0));
       int wd = 0;
-      uint32_t word = c > 0 ? (lds_bits ? sbits[sub][0][lane] : p.bits[ii]) : 0u;
-      long cursor = 0;
-      for (int k = 0;; ++k) {
+      uint32_t word = 0;
+      if (k0 < c) {
+        word = lds_bits ? sbits[sub][0][lane] : p.bits[ii];
+        int skip = k0;
+        while (skip > 0) {
+          const int pc = __popc(word);
+          if (pc <= skip) {  // the k0-th entry lies in a later word
+            skip -= pc;
+            ++wd;
+            word = lds_bits ? sbits[sub][wd][lane] : p.bits[static_cast<long>(wd) * p.pitch + ii];
+          } else {
+            for (; skip > 0; --skip) word &= word - 1u;
+          }
+        }
+      }
+      for (int k = k0; k < k1; ++k) {
         const bool active = k < c;
         const uint64_t M = wave_ballot(active);
-        if (M == 0) break;
         if (active) {
           while (word == 0) {
             ++wd;
@@ -214,15 +233,13 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
           }
           const int b = __builtin_ctz(word);
           word &= word - 1u;
-          if ((k % W) == wave) {
-            const int jj = wd * 32 + b;
-            const int j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
-            const long e = base + cursor + lanes_below(M);
-            if (e < p.max_edges) {  // past the capacity the count still reports the demand
-              p.senders[e] = i;
-              p.receivers[e] = j;
-              p.mask[e] = 1;
-            }
+          const int jj = wd * 32 + b;
+          const int j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
+          const long e = base + cursor + lanes_below(M);
+          if (e < p.max_edges) {  // past the capacity the count still reports the demand
+            p.senders[e] = i;
+            p.receivers[e] = j;
+            p.mask[e] = 1;
           }
         }
         cursor += __popcll(M);
