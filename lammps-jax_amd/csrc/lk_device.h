@@ -91,16 +91,15 @@ __device__ __forceinline__ Locator<S> locate_mul(S x, S inv_delta, int n)
   return L;
 }
 
-// 1/sqrt(x), x > 0: the hardware estimate refined by Newton-Raphson steps
-// y <- y + y (1 - x y^2) / 2 (two in float64, one in float32), about one ulp.
+// 1/sqrt(x), x > 0: the hardware estimate refined by one Newton-Raphson step
+// y <- y + y (1 - x y^2) / 2. On gfx950 the float64 estimate is within 5.2e-8 relative and one
+// step brings it within 4.2e-15 (measured over x in [1, 49], the r^2 range of the pair tables);
+// the float32 estimate refined once is within about one ulp.
 __device__ __forceinline__ double rsqrt_nr(double x)
 {
   double y = __builtin_amdgcn_rsq(x);
-  double e = fma(-(x * y), y, 1.0);
-  y = fma(0.5 * y, e, y);
-  e = fma(-(x * y), y, 1.0);
-  y = fma(0.5 * y, e, y);
-  return y;
+  const double e = fma(-(x * y), y, 1.0);
+  return fma(0.5 * y, e, y);
 }
 
 __device__ __forceinline__ float rsqrt_nr(float x)
