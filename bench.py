@@ -30,12 +30,30 @@ HBM_PEAK_GBS = 8000.0
 
 
 def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: int,
-                words: int) -> float:
+                words: int, two_sided: bool = False) -> float:
     """Algorithmic (compulsory, unique) HBM bytes of one launch of a stage.
 
     R list rows, A = owned + ghost atoms, N owned, E packed edges, entries = list entries read,
-    S bytes per model scalar, words = validity words per row."""
+    S bytes per model scalar, words = validity words per row; two_sided: the plain / half
+    schemes (incidence lists, 2E incident entries)."""
     rec = 4 * S  # atom record: x, y, z, species
+    if two_sided:
+        if stage == "inc_count":
+            return 9 * E + 8 * A
+        if stage == "inc_scan":
+            return 8 * A
+        if stage == "inc_fill":
+            return 9 * E + 8 * E + 8 * A
+        if stage == "inc_sort":
+            return 8 * E + 8 * E + 8 * E
+        if stage == "eam_density":
+            return 8 * E + rec * A + 2 * S * A
+        if stage == "eam_embed":
+            return 6 * S * A
+        if stage == "eam_force":
+            return 8 * E + rec * A + S * A + 72 * A
+        if stage == "lj_rows":
+            return 8 * E + rec * A + 72 * A
     if stage == "pack_atoms":
         return A * (24 + 4) + A * (rec + 4)
     if stage == "pack_count":
@@ -219,10 +237,11 @@ def main() -> int:
     words = (lst["maxneighs"] + 31) // 32
     stage_us = {k: 1e3 * tot / cnt for k, (tot, cnt) in stages.items()}
     device_us = sum(stage_us.values())
-    kernel_stages = {k: v for k, v in stage_us.items() if stage_bytes(
-        k, R=R, A=A, N=N, E=E, entries=lst["entries"], S=S, words=words) > 0}
+    two = wl.accumulation != "onesided"
+    sb_kw = dict(R=R, A=A, N=N, E=E, entries=lst["entries"], S=S, words=words, two_sided=two)
+    kernel_stages = {k: v for k, v in stage_us.items() if stage_bytes(k, **sb_kw) > 0}
     dom = max(kernel_stages, key=kernel_stages.get)
-    dom_bytes = stage_bytes(dom, R=R, A=A, N=N, E=E, entries=lst["entries"], S=S, words=words)
+    dom_bytes = stage_bytes(dom, **sb_kw)
     achieved = dom_bytes / (stage_us[dom] * 1e-6) / 1e9
     sb = survey_bytes(R=R, A=A, N=N, E=E, entries=lst["entries"], S=S)
     ms_per_step = 1e3 * elapsed / args.steps
