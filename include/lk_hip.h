@@ -140,6 +140,15 @@ int lk_set_accumulation(lk_handle *h, int accum);
  */
 int lk_set_ghost_map(lk_handle *h, int nlocal, int nghost, const int *ghost_owner);
 
+/*
+ * Neighbour-list generation for the two-sided schemes (plain, half): the engine passes a value
+ * that changes whenever it rebuilds the list (LAMMPS: the step of the last build, the same event
+ * neighbor->ago == 0 marks in PairJaxKokkos::compute, cpp/pair_jax_kokkos.cpp:1010-1011). The
+ * per-atom incidence lists are then built from the list slots once per list and filtered each
+ * step by the pack's validity bits. -1 (the default): rebuilt at every compute.
+ */
+int lk_set_list_epoch(lk_handle *h, long epoch);
+
 /* x: LAMMPS positions [nall][3] double (device); type: 1-based LAMMPS types (device). */
 int lk_pack_atoms(lk_handle *h, void *stream, const double *x, const int *type, int nall);
 

@@ -55,7 +55,7 @@ void free_all(Handle &h)
                   h.d_tile_off,  h.d_bits,      h.d_fp,          h.d_rho,       h.d_partials,
                   h.d_result,    h.d_ghost_owner, h.d_ghost_off, h.d_ghost_list, h.d_done,
                   h.d_deg,       h.d_inc_loc,   h.d_inc_part,    h.d_inc_tmp,   h.d_inc,
-                  h.d_rho_part,  h.d_epair,     h.d_pack_state};
+                  h.d_rho_part,  h.d_epair,     h.d_pack_state,  h.d_inc_bit};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -81,26 +81,43 @@ int ensure_bits(Handle &h, int maxneighs)
   return LK_OK;
 }
 
-// Buffers of the two-sided schemes, sized from the contract once (first use).
-int ensure_incidence(Handle &h)
+// Buffers of the two-sided schemes: per-atom arrays sized from the contract once (first use),
+// incidence entries sized for `entries` (2 * max_edges for lists built from the packed edges,
+// 2 * rows * maxneighs for lists built from the neighbour-list slots); they grow, rarely, outside
+// any captured region.
+int ensure_incidence(Handle &h, long entries = 0)
 {
-  if (h.d_inc) return LK_OK;
   const long A = h.contract.max_atoms;
-  const long E2 = 2L * h.contract.max_edges;
-  if (E2 > static_cast<long>(INT_MAX))
-    return fail(h, LK_ERR_CAPACITY,
-                "LAMMPS-JAX edge capacity too large for two-sided accumulation (2 * max_edges "
-                "must fit in int)");
-  const long chunks = (A + 1 + 4095) / 4096;
   hipError_t e;
-  if ((e = dalloc(&h.d_deg, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence counts)");
-  if ((e = dalloc(&h.d_inc_loc, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence offsets)");
-  if ((e = dalloc(&h.d_inc_part, chunks)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence chunks)");
-  if ((e = dalloc(&h.d_inc_tmp, E2)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence staging)");
-  if ((e = dalloc(&h.d_inc, E2)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence lists)");
-  if ((e = hipMalloc(&h.d_rho_part, A * h.scalar_bytes())) != hipSuccess) return hip_fail(h, e, "hipMalloc(rho partials)");
-  if ((e = hipMalloc(&h.d_epair, A * h.scalar_bytes())) != hipSuccess) return hip_fail(h, e, "hipMalloc(pair energy)");
-  if ((e = hipMemset(h.d_deg, 0, sizeof(int) * (A + 1))) != hipSuccess) return hip_fail(h, e, "hipMemset(incidence counts)");
+  if (!h.d_deg) {
+    const long chunks = (A + 1 + 4095) / 4096;
+    if ((e = dalloc(&h.d_deg, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence counts)");
+    if ((e = dalloc(&h.d_inc_loc, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence offsets)");
+    if ((e = dalloc(&h.d_inc_part, chunks)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence chunks)");
+    if ((e = hipMalloc(&h.d_rho_part, A * h.scalar_bytes())) != hipSuccess) return hip_fail(h, e, "hipMalloc(rho partials)");
+    if ((e = hipMalloc(&h.d_epair, A * h.scalar_bytes())) != hipSuccess) return hip_fail(h, e, "hipMalloc(pair energy)");
+    if ((e = hipMemset(h.d_deg, 0, sizeof(int) * (A + 1))) != hipSuccess) return hip_fail(h, e, "hipMemset(incidence counts)");
+  }
+  const long need = entries > 2L * h.contract.max_edges ? entries : 2L * h.contract.max_edges;
+  if (need > static_cast<long>(INT_MAX))
+    return fail(h, LK_ERR_CAPACITY,
+                "LAMMPS-JAX capacity too large for two-sided accumulation (incidence entries must "
+                "fit in int)");
+  if (need > h.inc_cap) {
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(h, e, "hipDeviceSynchronize");
+    for (void *p : {static_cast<void *>(h.d_inc_tmp), static_cast<void *>(h.d_inc),
+                    static_cast<void *>(h.d_inc_bit)})
+      if (p) (void)hipFree(p);
+    h.d_inc_tmp = nullptr;
+    h.d_inc = nullptr;
+    h.d_inc_bit = nullptr;
+    h.inc_cap = 0;
+    if ((e = dalloc(&h.d_inc_tmp, need)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence staging)");
+    if ((e = dalloc(&h.d_inc, need)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence lists)");
+    if ((e = dalloc(&h.d_inc_bit, need)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence bits)");
+    h.inc_cap = need;
+    h.inc_key = Handle::IncKey{};  // rebuild
+  }
   if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(h, e, "initialising incidence buffers");
   return LK_OK;
 }
@@ -326,6 +343,13 @@ int lk_set_accumulation(lk_handle *w, int accum)
   return LK_OK;
 }
 
+int lk_set_list_epoch(lk_handle *w, long epoch)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  w->h.list_epoch = epoch < 0 ? -1 : epoch;
+  return LK_OK;
+}
+
 int lk_set_ghost_map(lk_handle *w, int nlocal, int nghost, const int *ghost_owner)
 {
   if (!w) return LK_ERR_ARGUMENT;
@@ -411,11 +435,20 @@ int lk_pack_edges(lk_handle *w, void *stream, const double *x, const int *ilist,
   if (int rc = ensure_bits(h, max_neighbors_per_atom)) return rc;
   h.x_last = x;
   const bool half_edges = c.pairing != LK_PAIRING_FULL;
+  h.list_ilist = ilist;
+  h.list_numneigh = numneigh;
+  h.list_neighbors = neighbors;
+  h.list_stride = nb_stride;
+  h.list_rows = static_cast<int>(rows);
+  h.list_maxneighs = max_neighbors_per_atom;
   const bool full_list = !c.half_list;
   // cpp/pair_jax_kokkos.cpp:850-867
   const int duplicate = c.newton_pair && c.pair_sum && !c.edge_force && !multi_hop && !c.comm;
   const int half_filter = half_edges && full_list;
   const int unique = half_edges && c.comm && full_list;
+  h.list_half_filter = half_filter;
+  h.list_unique = unique;
+  h.list_duplicate = duplicate;
   hipError_t e = lk::launch_pack_edges(h, as_stream(stream), x, ilist, numneigh, neighbors,
                                        nb_stride, static_cast<int>(rows), max_neighbors_per_atom,
                                        nlocal, duplicate, half_filter, unique);
@@ -455,8 +488,13 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
                   "density fold");
     if ((flags & LK_VIRIAL) && h.contract.newton_pair && nlocal + nghost > 0 && !h.x_last)
       return fail(h, LK_ERR_STATE, "the f.r virial needs the positions of a prior pack");
-    if (int rc = ensure_incidence(h)) return rc;
-    e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, h.x_last);
+    // incidence lists from the list slots unless the pack's filter depends on the positions
+    // (unique boundary) or duplicates edges, or a validity-bit address would not fit 27 bits
+    const long bit_words = static_cast<long>((h.list_maxneighs + 31) / 32) * h.contract.max_atoms;
+    const bool from_list = h.list_neighbors && !h.list_unique && !h.list_duplicate &&
+                           bit_words < (1L << 27);
+    if (int rc = ensure_incidence(h, from_list ? 2L * h.list_rows * h.list_maxneighs : 0)) return rc;
+    e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, h.x_last, from_list);
   }
   if (e != hipSuccess) return hip_fail(h, e, "compute");
   h.result_mirrored = true;

@@ -112,6 +112,28 @@ struct Handle {
   void *d_rho_part = nullptr;   // [max_atoms] per-row density before the ghost fold
   void *d_epair = nullptr;      // [max_atoms] per-row pair energy
   const double *x_last = nullptr;  // engine positions of the last pack (f.r virial)
+  uint32_t *d_inc_bit = nullptr;  // [capacity] validity-bit address of each list-built entry
+  long inc_cap = 0;               // capacity of d_inc_tmp / d_inc / d_inc_bit (entries)
+  // the neighbour list of the last lk_pack_edges: the two-sided incidence lists are built from
+  // its slots once per list (lk_set_list_epoch) and filtered each step by the pack's bits
+  const int *list_ilist = nullptr;
+  const int *list_numneigh = nullptr;
+  const int *list_neighbors = nullptr;
+  long list_stride = 0;
+  int list_rows = 0, list_maxneighs = 0;
+  int list_half_filter = 0, list_unique = 0, list_duplicate = 0;
+  long list_epoch = -1;  // -1: rebuild the incidence lists every step
+  struct IncKey {
+    long epoch = -2;
+    const int *ilist = nullptr, *neighbors = nullptr;
+    long stride = 0;
+    int rows = 0, maxneighs = 0, half_filter = 0;
+    bool operator==(const IncKey &o) const
+    {
+      return epoch == o.epoch && ilist == o.ilist && neighbors == o.neighbors && stride == o.stride &&
+             rows == o.rows && maxneighs == o.maxneighs && half_filter == o.half_filter;
+    }
+  } inc_key;
 
   size_t scalar_bytes() const { return contract.precision == LK_FLOAT64 ? 8 : 4; }
 };
@@ -155,7 +177,7 @@ hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, 
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles);
 
 hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
-                            double scale, double *f, const double *x);
+                            double scale, double *f, const double *x, bool from_list);
 
 hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,
                                 int nall, const int *ilist, const int *numneigh,

@@ -206,6 +206,105 @@ __global__ __launch_bounds__(256) void k_inc_sort(IncArgs a, int nsort)
   }
 }
 
+// Incidence lists from the neighbour-list slots (once per list). Slot f = jj * rows + ii (the
+// reference packer's flat order, cpp:77-83) passes the list's static filters of
+// PackNeighborFunctor (cpp:84-94: rows past max_atoms, jj >= numneigh, j >= max_atoms, the half
+// filter j < i); its distance filter is applied each step from the pack's validity bits.
+struct ListArgs {
+  const int *ilist;
+  const int *numneigh;
+  const int *neighbors;
+  long stride;
+  int rows;
+  int maxneighs;
+  int max_atoms;
+  int half_filter;
+  int pitch;  // row pitch of the validity bits
+  int *deg;
+  int *loc;
+  int *part;
+  uint32_t *tmp;
+  int *inc;
+  uint32_t *inc_bit;
+};
+
+__device__ __forceinline__ bool list_slot(const ListArgs &L, long f, int &i, int &j)
+{
+  const int ii = static_cast<int>(f % L.rows);
+  const int jj = static_cast<int>(f / L.rows);
+  i = L.ilist[ii];
+  if (i < 0 || i >= L.max_atoms) return false;
+  const int nn = min(L.numneigh[i], L.maxneighs);
+  if (jj >= nn) return false;
+  j = L.neighbors[static_cast<long>(jj) * L.stride + i] & kNeighMask;
+  if (j >= L.max_atoms) return false;
+  return !(L.half_filter && j < i);
+}
+
+__global__ __launch_bounds__(256) void k_inc_list_count(ListArgs L)
+{
+  const long n = static_cast<long>(L.rows) * L.maxneighs;
+  for (long f = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; f < n;
+       f += static_cast<long>(gridDim.x) * blockDim.x) {
+    int i, j;
+    if (!list_slot(L, f, i, j)) continue;
+    atomicAdd(&L.deg[i], 1);
+    atomicAdd(&L.deg[j], 1);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_inc_list_fill(ListArgs L)
+{
+  const long n = static_cast<long>(L.rows) * L.maxneighs;
+  for (long f = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; f < n;
+       f += static_cast<long>(gridDim.x) * blockDim.x) {
+    int i, j;
+    if (!list_slot(L, f, i, j)) continue;
+    const uint32_t key = static_cast<uint32_t>(f) << 1;
+    const int pi = inc_off(L.loc, L.part, i) + atomicSub(&L.deg[i], 1) - 1;
+    L.tmp[pi] = key;
+    const int pj = inc_off(L.loc, L.part, j) + atomicSub(&L.deg[j], 1) - 1;
+    L.tmp[pj] = key | 1u;
+  }
+}
+
+// As k_inc_sort: rank by slot, then store the other atom (side in the top bit) and the address
+// of the slot's validity bit, word ((jj >> 5) * pitch + ii), bit jj & 31.
+__global__ __launch_bounds__(256) void k_inc_list_sort(ListArgs L, int nsort)
+{
+  const int atom = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (atom >= nsort) return;  // whole wave
+  const int b = inc_off(L.loc, L.part, atom);
+  const int len = inc_off(L.loc, L.part, atom + 1) - b;
+  for (int c0 = 0; c0 < len; c0 += kWave) {
+    const bool mine = c0 + lane < len;
+    const uint32_t v = mine ? L.tmp[b + c0 + lane] : 0xFFFFFFFFu;
+    int rank = 0;
+    for (int c1 = 0; c1 < len; c1 += kWave) {
+      const uint32_t w = c1 + lane < len ? L.tmp[b + c1 + lane] : 0xFFFFFFFFu;
+#pragma unroll 16
+      for (int m = 0; m < kWave; ++m) {
+        const uint32_t wm = static_cast<uint32_t>(__shfl(static_cast<int>(w), m, kWave));
+        rank += wm < v ? 1 : 0;
+      }
+    }
+    if (mine) {
+      const long f = v >> 1;
+      const uint32_t side = v & 1u;
+      const int ii = static_cast<int>(f % L.rows);
+      const int jj = static_cast<int>(f / L.rows);
+      const int i = L.ilist[ii];
+      const int other =
+          side ? i : (L.neighbors[static_cast<long>(jj) * L.stride + i] & kNeighMask);
+      L.inc[b + rank] = static_cast<int>(static_cast<uint32_t>(other) | (side << 31));
+      L.inc_bit[b + rank] =
+          ((static_cast<uint32_t>(jj >> 5) * static_cast<uint32_t>(L.pitch) + static_cast<uint32_t>(ii))
+           << 5) | static_cast<uint32_t>(jj & 31);
+    }
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ T group_sum(T v)
 {
@@ -228,7 +327,17 @@ struct TwoSided {
   const int *ghost_off;
   const int *ghost_list;
   int nblk;             // 64-atom tiles over nall
+  const uint32_t *inc_bit;  // list-built entries: address of the slot's validity bit
+  const uint32_t *bits;     // the pack's validity bits of this step
 };
+
+// The pack kept this entry's list slot this step (lists built from packed edges: always).
+__device__ __forceinline__ bool slot_kept(const TwoSided &t, int q)
+{
+  if (!t.inc_bit) return true;
+  const uint32_t ba = t.inc_bit[q];
+  return ((t.bits[ba >> 5] >> (ba & 31u)) & 1u) != 0;
+}
 
 // Rows whose energy counts (export.py:183-194).
 __device__ __forceinline__ int energy_rows(const TwoSided &t, const StepResult *r, bool half)
@@ -268,6 +377,7 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
         const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
         const bool in = (v >> 31) != 0;
         if (!HALF && in) continue;  // plain: density and pair energy stay on the sender
+        if (!slot_kept(t, b + k)) continue;
         const int o = static_cast<int>(v & 0x7FFFFFFFu);
         const Atom4<S> xo = m.atoms[o];
         S dx, dy, dz;
@@ -408,6 +518,7 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
         const bool in = (v >> 31) != 0;
         const int o = static_cast<int>(v & 0x7FFFFFFFu);
         if (!HALF && (in ? o : a) >= erows) continue;  // uncounted senders carry no gradient
+        if (!slot_kept(t, b + k)) continue;
         const Atom4<S> xo = m.atoms[o];
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
@@ -491,6 +602,7 @@ __global__ __launch_bounds__(kRowBlock) void k_lj_inc(LjModel<S> m, TwoSided t)
         const bool in = (v >> 31) != 0;
         const int o = static_cast<int>(v & 0x7FFFFFFFu);
         if ((in ? o : a) >= erows) continue;
+        if (!slot_kept(t, b + k)) continue;
         const Atom4<S> xo = m.atoms[o];
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
@@ -573,6 +685,49 @@ static hipError_t build_incidence(Handle &h, hipStream_t s, int nall)
   return hipGetLastError();
 }
 
+static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall)
+{
+  ListArgs L;
+  L.ilist = h.list_ilist;
+  L.numneigh = h.list_numneigh;
+  L.neighbors = h.list_neighbors;
+  L.stride = h.list_stride;
+  L.rows = h.list_rows;
+  L.maxneighs = h.list_maxneighs;
+  L.max_atoms = h.contract.max_atoms;
+  L.half_filter = h.list_half_filter;
+  L.pitch = h.contract.max_atoms;
+  L.deg = h.d_deg;
+  L.loc = h.d_inc_loc;
+  L.part = h.d_inc_part;
+  L.tmp = h.d_inc_tmp;
+  L.inc = h.d_inc;
+  L.inc_bit = h.d_inc_bit;
+  const long slots = static_cast<long>(L.rows) * L.maxneighs;
+  const int grid = grid_for(h, slots > 0 ? slots : 1, 256, 16);
+  if (slots > 0) {
+    StageTimer timer(h, s, "inc_count");
+    hipLaunchKernelGGL(k_inc_list_count, dim3(grid), dim3(256), 0, s, L);
+  }
+  {
+    StageTimer timer(h, s, "inc_scan");
+    const int n = h.contract.max_atoms + 1;
+    const int chunks = (n + kScanChunk - 1) / kScanChunk;
+    hipLaunchKernelGGL(k_scan_chunks, dim3(chunks), dim3(kScanThreads), 0, s, h.d_deg, n,
+                       h.d_inc_loc, h.d_inc_part);
+    hipLaunchKernelGGL(k_scan_parts, dim3(1), dim3(kScanThreads), 0, s, h.d_inc_part, chunks);
+  }
+  if (slots > 0) {
+    StageTimer timer(h, s, "inc_fill");
+    hipLaunchKernelGGL(k_inc_list_fill, dim3(grid), dim3(256), 0, s, L);
+  }
+  if (nall > 0) {
+    StageTimer timer(h, s, "inc_sort");
+    hipLaunchKernelGGL(k_inc_list_sort, dim3((nall + 3) / 4), dim3(256), 0, s, L, nall);
+  }
+  return hipGetLastError();
+}
+
 static TwoSided two_sided_args(Handle &h, int nlocal, int nghost, const double *x)
 {
   TwoSided t;
@@ -588,15 +743,18 @@ static TwoSided two_sided_args(Handle &h, int nlocal, int nghost, const double *
   t.ghost_off = nghost > 0 ? h.d_ghost_off : nullptr;
   t.ghost_list = h.d_ghost_list;
   t.nblk = (t.nall + kRowAtoms - 1) / kRowAtoms;
+  t.inc_bit = nullptr;
+  t.bits = h.d_bits;
   return t;
 }
 
 template <typename S, bool HALF>
 static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
-                                double scale, double *f, const double *x)
+                                double scale, double *f, const double *x, bool from_list)
 {
   EamArgs<S> m = eam_args<S>(h, nlocal, scale, f);
   TwoSided t = two_sided_args(h, nlocal, nghost, x);
+  if (from_list) t.inc_bit = h.d_inc_bit;
   m.flags = flags;
   S *rho_part = static_cast<S *>(h.d_rho_part);
   S *epair = static_cast<S *>(h.d_epair);
@@ -623,7 +781,7 @@ static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost
 
 template <typename S>
 static hipError_t lj_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
-                               double scale, double *f, const double *x)
+                               double scale, double *f, const double *x, bool from_list)
 {
   LjModel<S> m;
   m.atoms = static_cast<const Atom4<S> *>(h.d_atoms);
@@ -639,6 +797,7 @@ static hipError_t lj_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost,
   m.flags = flags;
   m.mirror = h.d_host_result;
   TwoSided t = two_sided_args(h, nlocal, nghost, x);
+  if (from_list) t.inc_bit = h.d_inc_bit;
   const int grid = grid_for(h, t.nblk > 0 ? t.nblk : 1, 1, 2);
   StageTimer timer(h, s, "lj_rows");
   if (flags & LK_VIRIAL)
@@ -649,20 +808,39 @@ static hipError_t lj_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost,
 }
 
 hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
-                            double scale, double *f, const double *x)
+                            double scale, double *f, const double *x, bool from_list)
 {
-  hipError_t e = build_incidence(h, s, nlocal + nghost);
+  hipError_t e = hipSuccess;
+  if (from_list) {
+    // once per list: the engine's epoch (or every step when it gives none) and the list's shape
+    Handle::IncKey key;
+    key.epoch = h.list_epoch;
+    key.ilist = h.list_ilist;
+    key.neighbors = h.list_neighbors;
+    key.stride = h.list_stride;
+    key.rows = h.list_rows;
+    key.maxneighs = h.list_maxneighs;
+    key.half_filter = h.list_half_filter;
+    if (h.list_epoch < 0 || !(key == h.inc_key)) {
+      e = build_incidence_from_list(h, s, nlocal + nghost);
+      h.inc_key = key;
+    }
+  } else {
+    e = build_incidence(h, s, nlocal + nghost);
+    h.inc_key = Handle::IncKey{};  // the entries are edge-built now
+  }
   if (e != hipSuccess) return e;
   const bool f64 = h.contract.precision == LK_FLOAT64;
   const bool half = h.accum == LK_ACCUM_HALF;
   if (h.model == 1) {
-    if (f64) return half ? eam_two_sided<double, true>(h, s, nlocal, nghost, flags, scale, f, x)
-                         : eam_two_sided<double, false>(h, s, nlocal, nghost, flags, scale, f, x);
-    return half ? eam_two_sided<float, true>(h, s, nlocal, nghost, flags, scale, f, x)
-                : eam_two_sided<float, false>(h, s, nlocal, nghost, flags, scale, f, x);
+    if (f64)
+      return half ? eam_two_sided<double, true>(h, s, nlocal, nghost, flags, scale, f, x, from_list)
+                  : eam_two_sided<double, false>(h, s, nlocal, nghost, flags, scale, f, x, from_list);
+    return half ? eam_two_sided<float, true>(h, s, nlocal, nghost, flags, scale, f, x, from_list)
+                : eam_two_sided<float, false>(h, s, nlocal, nghost, flags, scale, f, x, from_list);
   }
-  if (f64) return lj_two_sided<double>(h, s, nlocal, nghost, flags, scale, f, x);
-  return lj_two_sided<float>(h, s, nlocal, nghost, flags, scale, f, x);
+  if (f64) return lj_two_sided<double>(h, s, nlocal, nghost, flags, scale, f, x, from_list);
+  return lj_two_sided<float>(h, s, nlocal, nghost, flags, scale, f, x, from_list);
 }
 
 }  // namespace lk

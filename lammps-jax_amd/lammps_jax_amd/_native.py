@@ -29,7 +29,7 @@ LK_VIRIAL = 2
 # Every symbol include/lk_hip.h declares.
 EXPORTED = (
     "lk_create", "lk_destroy", "lk_last_error", "lk_set_eam", "lk_set_lj",
-    "lk_set_accumulation", "lk_set_ghost_map", "lk_pack_atoms", "lk_pack_edges", "lk_compute",
+    "lk_set_accumulation", "lk_set_list_epoch", "lk_set_ghost_map", "lk_pack_atoms", "lk_pack_edges", "lk_compute",
     "lk_pack_compute", "lk_step_result", "lk_timing_enable", "lk_timing_read", "lk_edge_buffers",
     "lk_staging_buffers", "lk_model_buffers",
 )
@@ -112,6 +112,8 @@ def load() -> ctypes.CDLL:
     lib.lk_set_lj.restype = ip
     lib.lk_set_accumulation.argtypes = [vp, ip]
     lib.lk_set_accumulation.restype = ip
+    lib.lk_set_list_epoch.argtypes = [vp, ctypes.c_long]
+    lib.lk_set_list_epoch.restype = ip
     lib.lk_set_ghost_map.argtypes = [vp, ip, ip, pp(ctypes.c_int)]
     lib.lk_set_ghost_map.restype = ip
     lib.lk_pack_atoms.argtypes = [vp, vp, vp, vp, ip]

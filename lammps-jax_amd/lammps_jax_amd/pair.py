@@ -109,6 +109,9 @@ class Handle:
     def set_accumulation(self, name: str) -> None:
         self.check(self.lib.lk_set_accumulation(self.ptr, ACCUM[name]))
 
+    def set_list_epoch(self, epoch: int) -> None:
+        self.check(self.lib.lk_set_list_epoch(self.ptr, int(epoch)))
+
     def set_ghost_map(self, nlocal: int, ghost_owner: np.ndarray) -> None:
         go = np.ascontiguousarray(ghost_owner, np.int32)
         self.check(self.lib.lk_set_ghost_map(self.ptr, int(nlocal), int(len(go)),
@@ -254,6 +257,7 @@ class PairJax:
         if accumulation is not None:
             self.h.set_accumulation(accumulation)
         self.h.set_ghost_map(system.nlocal, system.ghost_owner)
+        self.list_epoch = 0
         self.upload()
 
     def upload(self) -> None:
@@ -267,6 +271,9 @@ class PairJax:
         self.numneigh = torch.from_numpy(lst["numneigh"]).to(dev)
         self.neighbors = torch.from_numpy(lst["neighbors"]).to(dev)
         torch.cuda.synchronize(dev)
+        # a new list on the device: the engine's rebuild signal (neighbor->ago == 0)
+        self.list_epoch += 1
+        self.h.set_list_epoch(self.list_epoch)
 
     def stream(self) -> int:
         return self.torch.cuda.current_stream(self.device).cuda_stream

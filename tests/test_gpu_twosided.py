@@ -141,3 +141,41 @@ def test_two_sided_scale_and_reproducibility(gpu, name, kind, accum):
     bare = pj.compute(eflag=False, vflag=False)
     assert bare.energy == 0.0 and np.all(bare.virial == 0.0)
     np.testing.assert_array_equal(pj.forces(), fa)
+
+
+@pytest.mark.parametrize("name,kind,accum,precision", [
+    ("eam_alloy_8k", harness.LIST_HALF, "half", 4),
+    ("lj_fcc_1k", harness.LIST_FULL, "plain", 8),
+])
+def test_incidence_lists_persist_across_steps(gpu, name, kind, accum, precision):
+    """The incidence lists are built once per list; the next step moves the atoms (same list) and
+    only the pack's validity bits of that step decide which slots count."""
+    import torch
+
+    wl, sysm, lst, pj = _case(name, (4, 4, 4), precision, accum, kind, seed=8)
+    mode = O.HALF if accum == "half" else O.PLAIN
+    _check(pj, sysm, _oracle(wl, sysm, lst, pj, precision, mode), precision)
+    rng = np.random.default_rng(9)
+    moved = sysm.x + rng.normal(0.0, 0.05, size=sysm.x.shape)  # well inside the skin
+    sysm.x = moved
+    pj.x = torch.from_numpy(np.ascontiguousarray(moved)).to(pj.device)
+    ref = _oracle(wl, sysm, lst, pj, precision, mode)
+    _check(pj, sysm, ref, precision)
+
+
+def test_half_unique_boundary_bundle_on_full_list(gpu):
+    """A communicating half-edge bundle over a full list: the pack keeps j >= i and, across the
+    boundary, the ghost above its owner (cpp:95-101); the incidence lists follow the packed
+    edges of each step."""
+    wl = systems.make_workload("eam_alloy_8k", cells=(4, 4, 4), seed=10)
+    sysm = systems.System(wl.x, wl.types, wl.box, wl.cutoff + wl.skin)
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    pj = PairJax(sysm, ("eam", wl.tables), precision=8, accumulation="half", fused=False)
+    pos, sp = O.pack_atoms(sysm.x, sysm.type, sysm.nall, pj.max_atoms, 8)
+    s, r, m, _, _ = O.pack_neighbors(sysm.x, lst, max_atoms=pj.max_atoms, max_edges=pj.max_edges,
+                                     nlocal=sysm.nlocal, cutoff=wl.cutoff, half_edges=True,
+                                     unique_boundary=True)
+    ref = O.eam_compute(wl.tables, pos, sp, nlocal=sysm.nlocal, nghost=sysm.nghost, senders=s,
+                        receivers=r, mask=m, mode=O.HALF, ghost_owner=sysm.ghost_owner,
+                        owned_rows_only=True)
+    _check(pj, sysm, ref, 8)
