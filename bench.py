@@ -155,6 +155,9 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--split-steps", type=int, default=20,
                     help="steps through the separate pack entry points, for packing us/step")
+    ap.add_argument("--nve", type=int, default=100, metavar="STEPS",
+                    help="velocity-Verlet NVE steps at 600 K after the timed loop (EAM one-sided "
+                         "workloads; 0: skip)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB ten times (scales the PMC "
                          "byte counters) and exit")
@@ -246,9 +249,21 @@ def main() -> int:
     sb = survey_bytes(R=R, A=A, N=N, E=E, entries=lst["entries"], S=S)
     ms_per_step = 1e3 * elapsed / args.steps
 
+    max_edges = pj.max_edges
+    nve = None
+    if args.nve > 0 and wl.model == "eam" and wl.accumulation == "onesided":
+        from lammps_jax_amd.md import Nve
+
+        del pj
+        torch.cuda.empty_cache()
+        md = Nve(wl, temperature=600.0, dt=0.002, device="cuda:0")
+        nve = md.run(args.nve).summary()
+        print(f"[bench] nve {nve}", file=sys.stderr, flush=True)
+        del md
+
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(wl, sysm, lst, max_atoms, pj.max_edges, args.cpu_budget, 50)
+        cpu = cpu_baseline(wl, sysm, lst, max_atoms, max_edges, args.cpu_budget, 50)
 
     line = {
         "metric": METRIC,
@@ -283,6 +298,7 @@ def main() -> int:
             "traffic": pmc_traffic(dom, wl.name),
         },
         "cpu_baseline": cpu,
+        "nve": nve,
         "stages_us": {k: round(v, 2) for k, v in sorted(stage_us.items())},
         "stage_timing_ms_per_step": round(events_ms, 4),
         "device_us_per_step": round(device_us, 2),

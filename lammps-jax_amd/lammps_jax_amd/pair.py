@@ -260,6 +260,19 @@ class PairJax:
         self.list_epoch = 0
         self.upload()
 
+    def rebind(self, system) -> None:
+        """A new step of the engine after reneighboring: new ghosts and a new list."""
+        if system.list is None:
+            raise ValueError("build the neighbour list first")
+        if system.nall > self.max_atoms:
+            raise N.LammpsJaxError(
+                N.LK_ERR_CAPACITY,
+                f"LAMMPS-JAX atom capacity exceeded: global max {system.nall} atoms, "
+                f"capacity {self.max_atoms}")
+        self.system = system
+        self.h.set_ghost_map(system.nlocal, system.ghost_owner)
+        self.upload()
+
     def upload(self) -> None:
         """Engine arrays onto the device (the Kokkos views of x, type, f and the list)."""
         torch, dev, s = self.torch, self.device, self.system
