@@ -195,6 +195,33 @@ int lk_timing_enable(lk_handle *h, int on);
 int lk_timing_read(lk_handle *h, int index, char *name, int name_len, double *total_ms,
                    long *count);
 
+/*
+ * Model bundles (`pair_coeff * * bundle.json`), host only. lk_bundle_load replaces
+ * lammps_jax::load_bundle_file (cpp/lammps_jax_model.cpp:212-315): the same JSON contract keys,
+ * defaults for older bundles, validation order and messages (returned in err, status
+ * LK_ERR_ARGUMENT). It accepts the reference's format tags (lammps-jax-json, -distributed,
+ * -half-edge), whose StableHLO programs it does not read, and this library's tag
+ * "lammps-jax-hip-json", whose "model" section names what the kernels run: "model_kind"
+ * "eam/alloy" with "eam_setfl" (a setfl file, relative to the bundle, optionally gzipped) or
+ * "lj/cut" with "lj_epsilon", "lj_sigma", "lj_cutoff", "lj_edge_energy_scale"; optional
+ * "model_accumulation" ("plain" | "half" | "onesided").
+ *
+ * lk_bundle_contract fills an lk_contract for lk_create from the bundle and the run's newton
+ * pair setting, the list kind following PairJaxKokkos::half_list (cpp/pair_jax_kokkos.cpp:
+ * 425-431); LK_ERR_UNSUPPORTED (contract still filled) for the neighbor-matrix layout, which
+ * this library does not run.
+ * lk_bundle_model gives the model for lk_set_eam / lk_set_lj (table pointers stay valid until
+ * lk_bundle_free); kind 1 eam/alloy, 2 lj/cut, 0 none (a reference bundle: LK_ERR_UNSUPPORTED);
+ * accumulation -1 when the bundle names none.
+ */
+typedef struct lk_bundle lk_bundle;
+int lk_bundle_load(const char *path, lk_bundle **out, char *err, int errlen);
+void lk_bundle_free(lk_bundle *b);
+int lk_bundle_contract(const lk_bundle *b, int newton_pair, lk_contract *out);
+int lk_bundle_model(const lk_bundle *b, int *kind, lk_eam_tables *eam, lk_lj_params *lj,
+                    int *accumulation);
+const char *lk_bundle_unit_style(const lk_bundle *b);
+
 /* Device pointers of the handle's buffers (for tests and for engines that read them). */
 int lk_edge_buffers(lk_handle *h, int **senders, int **receivers, unsigned char **mask);
 int lk_staging_buffers(lk_handle *h, void **atoms, int **species);

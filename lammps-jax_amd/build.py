@@ -23,6 +23,10 @@ BUILD = ROOT / "_build"
 
 HIP_SOURCES = ["lk_api.hip", "lk_pack.hip", "lk_eam.hip", "lk_lj.hip", "lk_step.hip",
                "lk_twosided.hip"]
+# host-only parts of liblkhip.so; -ffp-contract=off keeps the spline coefficients of the setfl
+# reader rounding as the numpy restatement does
+HOST_SOURCES = ["lk_bundle.cpp"]
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", f"-I{REPO / 'include'}"]
 
 OFFLOAD_ARCH = os.environ.get("LK_OFFLOAD_ARCH", "gfx950")
 HIPCC_FLAGS = [
@@ -61,11 +65,17 @@ def build_hip() -> Path:
         _run([hipcc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
         return obj
 
+    def compile_host(src: str) -> Path:
+        obj = BUILD / (Path(src).stem + ".o")
+        _run(["g++", *HOST_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        return obj
+
     with ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as pool:
-        objs = list(pool.map(compile_one, HIP_SOURCES))
+        objs = list(pool.map(compile_one, HIP_SOURCES)) + list(pool.map(compile_host, HOST_SOURCES))
     out = PKG / "liblkhip.so"
     tmp = PKG / "liblkhip.so.tmp"
-    _run([hipcc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    _run([hipcc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *map(str, objs), "-lz",
+          "-o", str(tmp)])
     tmp.replace(out)
     return out
 

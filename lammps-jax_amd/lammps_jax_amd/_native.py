@@ -31,7 +31,8 @@ EXPORTED = (
     "lk_create", "lk_destroy", "lk_last_error", "lk_set_eam", "lk_set_lj",
     "lk_set_accumulation", "lk_set_list_epoch", "lk_set_ghost_map", "lk_pack_atoms", "lk_pack_edges", "lk_compute",
     "lk_pack_compute", "lk_step_result", "lk_timing_enable", "lk_timing_read", "lk_edge_buffers",
-    "lk_staging_buffers", "lk_model_buffers",
+    "lk_staging_buffers", "lk_model_buffers", "lk_bundle_load", "lk_bundle_free",
+    "lk_bundle_contract", "lk_bundle_model", "lk_bundle_unit_style",
 )
 
 
@@ -137,6 +138,16 @@ def load() -> ctypes.CDLL:
     lib.lk_staging_buffers.restype = ip
     lib.lk_model_buffers.argtypes = [vp, pp(vp), pp(vp)]
     lib.lk_model_buffers.restype = ip
+    lib.lk_bundle_load.argtypes = [ctypes.c_char_p, pp(vp), ctypes.c_char_p, ip]
+    lib.lk_bundle_load.restype = ip
+    lib.lk_bundle_free.argtypes = [vp]
+    lib.lk_bundle_free.restype = None
+    lib.lk_bundle_contract.argtypes = [vp, ip, pp(LkContract)]
+    lib.lk_bundle_contract.restype = ip
+    lib.lk_bundle_model.argtypes = [vp, pp(ip), pp(LkEamTables), pp(LkLjParams), pp(ip)]
+    lib.lk_bundle_model.restype = ip
+    lib.lk_bundle_unit_style.argtypes = [vp]
+    lib.lk_bundle_unit_style.restype = ctypes.c_char_p
     _lib = lib
     return lib
 

@@ -244,11 +244,14 @@ class PairJax:
             # a LAMMPS half list taken as is: each boundary pair packed once, on this rank
             pairing = "half-unique"
         newton = "on" if newton_pair else "off"
-        self.contract = contract_for(max_atoms=self.max_atoms, max_edges=self.max_edges,
-                                     cutoff=cutoff, precision=precision, newton=newton,
-                                     pairing=pairing, n_hops=n_hops, comm=comm,
-                                     newton_pair=newton_pair, half_list=half_list,
-                                     pair_sum=pair_sum)
+        contract = contract_for(max_atoms=self.max_atoms, max_edges=self.max_edges,
+                                cutoff=cutoff, precision=precision, newton=newton,
+                                pairing=pairing, n_hops=n_hops, comm=comm,
+                                newton_pair=newton_pair, half_list=half_list, pair_sum=pair_sum)
+        self._setup(contract, accumulation)
+
+    def _setup(self, contract: N.LkContract, accumulation) -> None:
+        self.contract = contract
         self.h = Handle(self.contract)
         if self.kind == "eam":
             self.h.set_eam(self.model)
@@ -256,9 +259,58 @@ class PairJax:
             self.h.set_lj(self.model)
         if accumulation is not None:
             self.h.set_accumulation(accumulation)
-        self.h.set_ghost_map(system.nlocal, system.ghost_owner)
+        self.h.set_ghost_map(self.system.nlocal, self.system.ghost_owner)
         self.list_epoch = 0
         self.upload()
+
+    @classmethod
+    def from_bundle(cls, path, system, *, newton_pair=True, units="metal", ntypes=None,
+                    scale=1.0, accumulation=None, device="cuda:0", fused=True) -> "PairJax":
+        """`pair_coeff * * bundle.json [scale]` (PairJaxKokkos::coeff, cpp/pair_jax_kokkos.cpp:
+        582-663, and the newton checks of init_style, 665-673): the bundle's contract and
+        capacities, its unit style and species count checked against the run, its model
+        uploaded. accumulation overrides the bundle's scheme; neither: the contract's default."""
+        from .bundle import Bundle
+
+        bundle = Bundle(path)
+        if bundle.unit_style != units:
+            raise N.LammpsJaxError(N.LK_ERR_ARGUMENT,
+                                   "LAMMPS-JAX model unit style does not match current units")
+        contract = bundle.contract(newton_pair)
+        nt = int(ntypes if ntypes is not None else np.max(system.type, initial=1))
+        if contract.n_species > 0 and nt > contract.n_species:
+            raise N.LammpsJaxError(
+                N.LK_ERR_ARGUMENT,
+                f"LAMMPS-JAX model distinguishes {contract.n_species} species but the system "
+                f"defines {nt} atom types; types beyond the model's range would silently map to "
+                f"its last species")
+        if system.list is None:
+            raise ValueError("build the neighbour list first")
+        if bool(system.list["kind"] == 1) != bool(contract.half_list):
+            want = "half" if contract.half_list else "full"
+            raise N.LammpsJaxError(N.LK_ERR_ARGUMENT,
+                                   f"the bundle takes a {want} neighbour list")
+        kind, _, bundle_accum = bundle.model()
+        self = cls.__new__(cls)
+        torch = _torch()
+        self.torch = torch
+        self.device = torch.device(device)
+        self.system = system
+        self.bundle = bundle
+        self.kind = kind
+        if kind == "eam":
+            self.model = bundle.eam_tables()
+        else:
+            _, lj, _ = bundle.model()
+            self.model = dict(epsilon=lj.epsilon, sigma=lj.sigma, cutoff=lj.cutoff,
+                              edge_energy_scale=lj.edge_energy_scale)
+        self.max_atoms = int(contract.max_atoms)
+        self.max_edges = int(contract.max_edges)
+        self.scale = float(scale)
+        self.n_hops = int(contract.n_hops)
+        self.fused = fused
+        self._setup(contract, accumulation or bundle_accum)
+        return self
 
     def rebind(self, system) -> None:
         """A new step of the engine after reneighboring: new ghosts and a new list."""
