@@ -145,6 +145,38 @@ def pmc_traffic(kernel: str, workload: str):
     return None
 
 
+def lean_step(pj, eflag: bool = True, vflag: bool = True):
+    """One engine step as a C++ caller makes it: lk_pack_compute then lk_step_result, with the
+    argument list bound once (ctypes calls, no torch dispatch). The forces add into f without a
+    clear in between: LAMMPS zeroes f in its own force_clear, outside the pair style."""
+    import ctypes
+
+    from lammps_jax_amd import _native as N
+
+    lib, h, s = pj.h.lib, pj.h.ptr, pj.system
+    lst = s.list
+    flags = (N.LK_ENERGY if eflag else 0) | (N.LK_VIRIAL if vflag else 0)
+    vp = ctypes.c_void_p
+    stream = vp(pj.stream())
+    args = (h, stream, vp(pj.x.data_ptr()), vp(pj.type.data_ptr()), ctypes.c_int(s.nall),
+            vp(pj.ilist.data_ptr()), vp(pj.numneigh.data_ptr()), vp(pj.neighbors.data_ptr()),
+            ctypes.c_long(lst["stride"]), ctypes.c_int(lst["inum"]), ctypes.c_int(lst["gnum"]),
+            ctypes.c_int(lst["maxneighs"]), ctypes.c_int(s.nlocal), ctypes.c_int(s.nghost),
+            ctypes.c_int(flags), ctypes.c_double(pj.scale), vp(pj.f.data_ptr()))
+    info = N.LkStepInfo()
+    ref = ctypes.byref(info)
+    pack_compute, step_result = lib.lk_pack_compute, lib.lk_step_result
+
+    def step():
+        if pack_compute(*args) != N.LK_OK or step_result(h, stream, ref) != N.LK_OK:
+            raise N.LammpsJaxError(1, pj.h.error())
+        if info.edge_overflow:
+            raise N.LammpsJaxError(N.LK_ERR_CAPACITY, "LAMMPS-JAX edge capacity exceeded")
+        return info
+
+    return step
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -193,15 +225,24 @@ def main() -> int:
           f"max_atoms={max_atoms} max_edges={pj.max_edges} setup {setup_s:.1f}s", file=sys.stderr,
           flush=True)
 
+    step = lean_step(pj)
     for _ in range(args.warmup):
-        info = pj.compute()
+        info = step()
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        info = pj.compute()
+        info = step()
     torch.cuda.synchronize(dev)
     elapsed = time.perf_counter() - t0
     print(f"[bench] timed {args.steps} steps in {elapsed:.4f}s", file=sys.stderr, flush=True)
+    # the same steps through the Python host mirror (PairJax.compute: f cleared by torch each
+    # step, result wrapped in Python objects), reported beside the C-caller rate
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        pj.compute()
+    torch.cuda.synchronize(dev)
+    python_loop_ms = 1e3 * (time.perf_counter() - t0) / args.steps
     # stage timing: the same steps again with HIP events recorded around every launch on the
     # launch stream (lk_timing_*); kept out of the timed loop above, whose rate they would slow
     pj.h.timing_enable(True)
@@ -215,8 +256,9 @@ def main() -> int:
     # forces-only steps (eflag = vflag = 0), as most MD steps run between thermo outputs
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
+    step_f = lean_step(pj, eflag=False, vflag=False)
     for _ in range(args.steps):
-        pj.compute(eflag=False, vflag=False)
+        step_f()
     torch.cuda.synchronize(dev)
     forces_only_ms = 1e3 * (time.perf_counter() - t0) / args.steps
     # packing alone: the separate entry points (lk_pack_atoms, lk_pack_edges) with their timers
@@ -286,7 +328,8 @@ def main() -> int:
             "edges": E,
             "edge_capacity_per_atom": wl.edges_per_atom,
             "accumulation": wl.accumulation,
-            "step": "pack_atoms + pack_edges + model E/F/virial + f add + host readback",
+            "step": "pack_atoms + pack_edges + model E/F/virial + f add + host readback "
+                    "(lk_pack_compute + lk_step_result; f cleared by the engine, not timed)",
         },
         "roofline": {
             "bound": "hbm",
@@ -302,6 +345,7 @@ def main() -> int:
         "stages_us": {k: round(v, 2) for k, v in sorted(stage_us.items())},
         "stage_timing_ms_per_step": round(events_ms, 4),
         "device_us_per_step": round(device_us, 2),
+        "python_loop_ms_per_step": round(python_loop_ms, 4),
         "forces_only": {"ms_per_step": forces_only_ms,
                         "atom_steps_per_s": N / (forces_only_ms * 1e-3)},
         "packing_us_per_step": round(sum(pack_us.values()), 2) if pack_us else None,

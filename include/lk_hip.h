@@ -172,8 +172,9 @@ int lk_compute(lk_handle *h, void *stream, int nlocal, int nghost, int flags, do
 
 /*
  * One MD step's device work: lk_pack_atoms + lk_pack_edges + lk_compute with the same results.
- * The one-sided scheme runs fused in three launches (the model reads the neighbour list where the
- * pack reads it and never reads the packed arrays back); other schemes run the three in order.
+ * The one-sided scheme runs fused in three launches: the atom records; the pack, which filters
+ * the list, sums each row's density while the list slots are in registers and writes the packed
+ * arrays; the force sweep over the packed receivers. Other schemes run the three in order.
  * Replaces the pack/execute/add sequence of PairJaxKokkos::compute (cpp/pair_jax_kokkos.cpp:
  * 1023-1100).
  */
