@@ -228,6 +228,16 @@ int lk_edge_buffers(lk_handle *h, int **senders, int **receivers, unsigned char 
 int lk_staging_buffers(lk_handle *h, void **atoms, int **species);
 int lk_model_buffers(lk_handle *h, void **rho, void **fp);
 
+/*
+ * Edge-force contracts (force_output edge-force): the model's per-edge output, [max_edges][3] at
+ * the contract precision, the force on each packed edge's sender (r_ij = x_receiver - x_sender).
+ * The buffer the reference lends through Runtime::consume_force_output (cpp/pjrt/runtime.cpp:
+ * 475-482) to AddEdgeForcesFunctor (cpp/pair_jax_kokkos.cpp:194-225, 959-970); lk_compute has
+ * already added it into f (f(s) += scale F_e, and f(r) -= scale F_e with newton pair). Slots past
+ * the step's edge count hold zeros. LK_ERR_STATE for atom-force contracts.
+ */
+int lk_edge_forces(lk_handle *h, void **edge_forces);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,7 +55,7 @@ void free_all(Handle &h)
                   h.d_tile_off,  h.d_bits,      h.d_fp,          h.d_rho,       h.d_partials,
                   h.d_result,    h.d_ghost_owner, h.d_ghost_off, h.d_ghost_list, h.d_done,
                   h.d_deg,       h.d_inc_loc,   h.d_inc_part,    h.d_inc_tmp,   h.d_inc,
-                  h.d_rho_part,  h.d_epair,     h.d_pack_state,  h.d_inc_bit};
+                  h.d_rho_part,  h.d_epair,     h.d_pack_state,  h.d_inc_bit,   h.d_edge_f};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -170,8 +170,10 @@ int lk_create(const lk_contract *c, lk_handle **out)
     return fail(h, LK_ERR_ARGUMENT,
                 "Communicating bundles require newton on unless they pair fully and return atom "
                 "forces; ghost force rows flow back through the LAMMPS reverse communication");
-  if (c->edge_force)
-    return fail(h, LK_ERR_UNSUPPORTED, "edge-force output is not implemented by this build");
+  if (c->comm && c->edge_force && !half_edges)
+    return fail(h, LK_ERR_ARGUMENT,
+                "Communicating edge-force bundles require half-edge packing; full pairing packs "
+                "both directions and the newton scatter doubles forces");
   // init_style newton checks (cpp/pair_jax_kokkos.cpp:668-673)
   if (c->newton == LK_NEWTON_ON && !c->newton_pair)
     return fail(h, LK_ERR_ARGUMENT,
@@ -207,9 +209,15 @@ int lk_create(const lk_contract *c, lk_handle **out)
   if ((e = hipMalloc(&h.d_fp, A * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(fp)");
   if ((e = hipMalloc(&h.d_rho, A * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(rho)");
   if ((e = dalloc(&h.d_partials, 8 * tiles)) != hipSuccess) return hip_fail(h, e, "hipMalloc(partials)");
+  h.partial_slots = static_cast<int>(tiles);
   if ((e = dalloc(&h.d_result, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(result)");
   if ((e = dalloc(&h.d_done, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(done)");
   if ((e = dalloc(&h.d_pack_state, 2)) != hipSuccess) return hip_fail(h, e, "hipMalloc(pack state)");
+  if (c->edge_force) {
+    // the model's per-edge force output, [max_edges][3] at the contract precision
+    if ((e = hipMalloc(&h.d_edge_f, E * 3 * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(edge forces)");
+    (void)hipMemset(h.d_edge_f, 0, E * 3 * S);
+  }
   if ((e = hipHostMalloc(reinterpret_cast<void **>(&h.h_result), sizeof(lk::StepResult))) != hipSuccess)
     return hip_fail(h, e, "hipHostMalloc(result)");
   std::memset(h.h_result, 0, sizeof(lk::StepResult));
@@ -251,6 +259,10 @@ int lk_set_eam(lk_handle *w, const lk_eam_tables *t)
       !(t->drho > 0) || !(t->dr > 0))
     return fail(h, LK_ERR_ARGUMENT, "invalid EAM tables");
   if (h.model != 0) return fail(h, LK_ERR_STATE, "a model is already loaded on this handle");
+  if (h.contract.edge_force && !(h.contract.comm && h.contract.pairing == LK_PAIRING_HALF_UNIQUE))
+    return fail(h, LK_ERR_UNSUPPORTED,
+                "edge-force EAM is the communicating half-edge export (make_setfl_edge_force "
+                "with half_edges): half-unique pairing with a communication schedule");
   const int n_el = t->n_el, npair = n_el * (n_el + 1) / 2, n_rtab = n_el + npair;
   const size_t S = h.scalar_bytes();
   // node-major r-tables: [node][table][4], density tables first, then the pair tables
@@ -312,6 +324,10 @@ int lk_set_lj(lk_handle *w, const lk_lj_params *p)
   Handle &h = w->h;
   if (!p || !(p->cutoff >= 0) || !(p->sigma > 0)) return fail(h, LK_ERR_ARGUMENT, "invalid LJ parameters");
   if (h.model != 0) return fail(h, LK_ERR_STATE, "a model is already loaded on this handle");
+  if (h.contract.edge_force && (h.contract.comm || h.contract.pairing != LK_PAIRING_FULL))
+    return fail(h, LK_ERR_UNSUPPORTED,
+                "edge-force LJ is the plain export (make_lj_edge_force): full pairing, no "
+                "communication schedule");
   h.lj = *p;
   h.model = 2;
   return LK_OK;
@@ -322,6 +338,10 @@ int lk_set_accumulation(lk_handle *w, int accum)
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
   const bool half_edges = h.contract.pairing != LK_PAIRING_FULL;
+  if (h.contract.edge_force && accum != (half_edges ? LK_ACCUM_HALF : LK_ACCUM_PLAIN))
+    return fail(h, LK_ERR_ARGUMENT,
+                "edge-force output runs the two-sided scheme of its pairing (half for half-edge "
+                "bundles, plain otherwise)");
   switch (accum) {
     case LK_ACCUM_ONESIDED:
       if (half_edges || h.contract.half_list || h.contract.n_hops != 1)
@@ -493,8 +513,14 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
     const long bit_words = static_cast<long>((h.list_maxneighs + 31) / 32) * h.contract.max_atoms;
     const bool from_list = h.list_neighbors && !h.list_unique && !h.list_duplicate &&
                            bit_words < (1L << 27);
-    if (int rc = ensure_incidence(h, from_list ? 2L * h.list_rows * h.list_maxneighs : 0)) return rc;
-    e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, h.x_last, from_list);
+    if (h.contract.edge_force && h.model == 2) {
+      e = lk::launch_edge_force(h, s, nlocal, nghost, flags, scale, f, h.x_last, false);
+    } else {
+      if (int rc = ensure_incidence(h, from_list ? 2L * h.list_rows * h.list_maxneighs : 0)) return rc;
+      e = h.contract.edge_force
+              ? lk::launch_edge_force(h, s, nlocal, nghost, flags, scale, f, h.x_last, from_list)
+              : lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, h.x_last, from_list);
+    }
   }
   if (e != hipSuccess) return hip_fail(h, e, "compute");
   h.result_mirrored = true;
@@ -625,6 +651,14 @@ int lk_staging_buffers(lk_handle *w, void **atoms, int **species)
   if (!w) return LK_ERR_ARGUMENT;
   if (atoms) *atoms = w->h.d_atoms;
   if (species) *species = w->h.d_species;
+  return LK_OK;
+}
+
+int lk_edge_forces(lk_handle *w, void **edge_forces)
+{
+  if (!w || !edge_forces) return LK_ERR_ARGUMENT;
+  *edge_forces = w->h.d_edge_f;
+  if (!w->h.d_edge_f) return fail(w->h, LK_ERR_STATE, "the contract returns atom forces");
   return LK_OK;
 }
 

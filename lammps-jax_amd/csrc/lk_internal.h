@@ -74,6 +74,7 @@ struct Handle {
   void *d_fp = nullptr;      // F'(rho) [max_atoms]
   void *d_rho = nullptr;     // rho [max_atoms]
   // block partials: energy and virial, reduced in a fixed order
+  void *d_edge_f = nullptr;     // edge-force contracts: per-edge model forces [max_edges][3]
   double *d_partials = nullptr;
   int partial_slots = 0;
   StepResult *d_result = nullptr;
@@ -175,6 +176,8 @@ hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
 hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
                               double *f, int flags, const FusedPack &pack = FusedPack{});
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles);
+hipError_t launch_edge_force(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
+                             double scale, double *f, const double *x, bool from_list);
 
 hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
                             double scale, double *f, const double *x, bool from_list);

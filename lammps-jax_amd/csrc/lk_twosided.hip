@@ -807,6 +807,332 @@ static hipError_t lj_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost,
   return hipGetLastError();
 }
 
+// ----------------------------------------------------------------------------------------------
+// Edge-force output (force_output = edge-force). The model's output is the force on each packed
+// edge's sender, [max_edges][3] at the contract precision: make_setfl_edge_force for the
+// communicating half-edge EAM export (eam.py:336-409: the half scheme's density and F' above,
+// then psip / r * r_ij per edge) and make_lj_edge_force (examples/export_model.py:52-74:
+// dU/d(r_ij)). The pair style then adds them into f (AddEdgeForcesFunctor,
+// cpp/pair_jax_kokkos.cpp:194-225, 959-970): f(s) += scale * F_e over [0, count), and with newton
+// pair f(r) -= scale * F_e, with atomic adds as the reference's functor does. The virial is f.r
+// of the total f over nall rows after the add (cpp:1092-1100). Slots from the count up to the
+// previous step's count are cleared, so the buffer past the live edges holds zeros.
+// ----------------------------------------------------------------------------------------------
+template <typename S>
+struct EdgeOut {
+  const int *senders;
+  const int *receivers;
+  const unsigned char *mask;
+  const StepResult *count;  // the pack's demand count of this step
+  int max_edges;
+  long reset_end;           // slots below it held the previous step's forces
+  S *edge_f;
+  double *f;
+  double scale;
+  double *partials;
+  int ntiles;               // partial tiles the finalize reduces
+  int slot0_from;           // first tile whose slot 0 (row energy) this launch clears
+  int block_energy;         // each block stores its edge energy in its own slot 7
+  int nlocal;
+  int nall;
+};
+
+template <typename S>
+__device__ __forceinline__ long live_edges(const EdgeOut<S> &o)
+{
+  const long c = o.count->edge_count;
+  return c < o.max_edges ? c : o.max_edges;
+}
+
+template <typename S, bool NEWTON>
+__device__ __forceinline__ void store_edge_force(const EdgeOut<S> &o, long e, int snd, int rcv,
+                                                 S gx, S gy, S gz, bool live)
+{
+  S *q = o.edge_f + 3 * e;
+  q[0] = gx;
+  q[1] = gy;
+  q[2] = gz;
+  if (!live) return;
+  const double vx = o.scale * static_cast<double>(gx);
+  const double vy = o.scale * static_cast<double>(gy);
+  const double vz = o.scale * static_cast<double>(gz);
+  atomicAdd(o.f + 3L * snd + 0, vx);
+  atomicAdd(o.f + 3L * snd + 1, vy);
+  atomicAdd(o.f + 3L * snd + 2, vz);
+  if (NEWTON) {
+    atomicAdd(o.f + 3L * rcv + 0, -vx);
+    atomicAdd(o.f + 3L * rcv + 1, -vy);
+    atomicAdd(o.f + 3L * rcv + 2, -vz);
+  }
+}
+
+// Clears the slots of the previous step past this step's count and the partial slots this
+// launch owns (7 everywhere, 0 from slot0_from on).
+template <typename S>
+__device__ __forceinline__ void edge_tail_and_slots(const EdgeOut<S> &o, long ne)
+{
+  const long stride = static_cast<long>(gridDim.x) * blockDim.x;
+  const long tid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  for (long e = ne + tid; e < o.reset_end; e += stride) {
+    S *q = o.edge_f + 3 * e;
+    q[0] = S(0);
+    q[1] = S(0);
+    q[2] = S(0);
+  }
+  for (long t = tid; t < o.ntiles; t += stride) {
+    if (!o.block_energy || t >= gridDim.x) o.partials[8 * t + 7] = 0.0;
+    if (t >= o.slot0_from) o.partials[8 * t] = 0.0;
+  }
+}
+
+template <typename S, bool NEWTON>
+__global__ __launch_bounds__(kRowBlock) void k_eam_edge_force(EamArgs<S> m, EdgeOut<S> o)
+{
+  __shared__ LdsEntry<S> lds[kIncLds];
+  const Window<S> win = fill_window<S>(lds, kIncLds, m, m.n_rtab);
+  const long ne = live_edges(o);
+  const long stride = static_cast<long>(gridDim.x) * blockDim.x;
+  for (long e = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < ne; e += stride) {
+    const int snd = o.senders[e], rcv = o.receivers[e];
+    S gx = S(0), gy = S(0), gz = S(0);
+    bool live = false;
+    if (o.mask[e] && snd < o.nall && rcv < o.nall) {
+      const Atom4<S> xs = m.atoms[snd], xr = m.atoms[rcv];
+      S dx, dy, dz;
+      const S r2 = geometry(xs, xr, dx, dy, dz);  // d = x_r - x_s
+      if (r2 < m.cutsq) {
+        const S rinv = rsqrt_nr(r2);
+        const S rr = r2 * rinv;
+        const Locator<S> L = locate_mul(rr, m.inv_dr, m.nr);
+        const int zs = clamp_species(static_cast<int>(xs.w), m.n_el);
+        const int zr = clamp_species(static_cast<int>(xr.w), m.n_el);
+        // Past the table the non-extrapolated lookups saturate: slope 0 (eam.py:150).
+        const bool inside = !(L.t_raw > S(1));
+        const S rhojp = inside ? cslope_t(rcoef(win, m, L.node, zr), L.t) * m.inv_dr : S(0);
+        const S rhoip = inside ? cslope_t(rcoef(win, m, L.node, zs), L.t) * m.inv_dr : S(0);
+        const Coef<S> cp = rcoef(win, m, L.node, m.n_el + pair_row(zs, zr));
+        const S phi = cvalue(cp, L.t) * rinv;
+        const S z2p = inside ? cslope_t(cp, L.t) * m.inv_dr : S(0);
+        const S phip = (z2p - phi) * rinv;
+        const S coef = (m.fp[snd] * rhojp + m.fp[rcv] * rhoip + phip) * rinv;
+        gx = coef * dx;
+        gy = coef * dy;
+        gz = coef * dz;
+        live = true;
+      }
+    }
+    store_edge_force<S, NEWTON>(o, e, snd, rcv, gx, gy, gz, live);
+  }
+  edge_tail_and_slots(o, ne);
+}
+
+// LJ: the per-edge energy (scale edge_energy_scale) of senders below the energy rows goes to the
+// block's partial slot 7, summed in a fixed order.
+template <typename S, bool NEWTON>
+__global__ __launch_bounds__(256) void k_lj_edge_force(LjModel<S> m, EdgeOut<S> o)
+{
+  __shared__ double red[256];
+  const long ne = live_edges(o);
+  const int erows = o.count->ghost_sender ? o.nall : o.nlocal;  // export.py:183-194
+  const S tiny = static_cast<S>(1.0e-12);
+  const long stride = static_cast<long>(gridDim.x) * blockDim.x;
+  double en = 0.0;
+  for (long e = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < ne; e += stride) {
+    const int snd = o.senders[e], rcv = o.receivers[e];
+    S gx = S(0), gy = S(0), gz = S(0);
+    bool live = false;
+    if (o.mask[e] && snd < o.nall && rcv < o.nall) {
+      const Atom4<S> xs = m.atoms[snd], xr = m.atoms[rcv];
+      S dx, dy, dz;
+      const S r2 = geometry(xs, xr, dx, dy, dz);
+      if (r2 > tiny && r2 < m.cutsq) {  // export_model.py:22
+        const S u = m.sigsq / r2;
+        const S u3 = u * u * u;
+        if (snd < erows) en += static_cast<double>(m.edge_scale * (m.four_eps * (u3 * u3 - u3)));
+        const S dedr2 = -m.four_eps * (S(6) * u3 * u3 - S(3) * u3) / r2;
+        const S coef = S(2) * dedr2;
+        gx = coef * dx;
+        gy = coef * dy;
+        gz = coef * dz;
+        live = true;
+      }
+    }
+    store_edge_force<S, NEWTON>(o, e, snd, rcv, gx, gy, gz, live);
+  }
+  red[threadIdx.x] = en;
+  __syncthreads();
+  for (int off = blockDim.x / 2; off >= 1; off >>= 1) {
+    if (threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0 && blockIdx.x < o.ntiles) o.partials[8L * blockIdx.x + 7] = red[0];
+  edge_tail_and_slots(o, ne);
+}
+
+// f.r of the total f over the nall rows (cpp:227-245) into slots 1..6 of each 64-row tile, then
+// the last block reduces every slot into the step result.
+template <bool VIRIAL>
+__global__ __launch_bounds__(256) void k_fdotr_rows(const double *__restrict__ f,
+                                                    const double *__restrict__ x, int nall,
+                                                    int fdotr, double *partials, int ntiles,
+                                                    double escale, int flags, StepResult *result,
+                                                    int *done, StepResult *mirror)
+{
+  __shared__ double scratch[7 * 256];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int waves = static_cast<int>(gridDim.x) * (blockDim.x / kWave);
+  for (int t = blockIdx.x * (blockDim.x / kWave) + wave_in_block(); t < ntiles; t += waves) {
+    const int a = t * kWave + lane;
+    double w[6] = {0, 0, 0, 0, 0, 0};
+    if (VIRIAL && fdotr && a < nall) {
+      const double *fa = f + 3L * a;
+      const double *xa = x + 3L * a;
+      w[0] = fa[0] * xa[0];
+      w[1] = fa[1] * xa[1];
+      w[2] = fa[2] * xa[2];
+      w[3] = fa[1] * xa[0];
+      w[4] = fa[2] * xa[0];
+      w[5] = fa[2] * xa[1];
+    }
+#pragma unroll
+    for (int c = 0; c < 6; ++c) {
+      const double v = wave_sum(w[c]);
+      if (lane == 0) partials[8L * t + 1 + c] = v;
+    }
+  }
+  finalize_last_block(partials, ntiles, escale, 1.0, flags, result, done, scratch, FusedPack{},
+                      mirror);
+}
+
+template <typename S>
+static EdgeOut<S> edge_out(Handle &h, int nlocal, int nghost, double scale, double *f, int ntiles,
+                           int slot0_from, int block_energy)
+{
+  EdgeOut<S> o;
+  o.senders = h.d_senders;
+  o.receivers = h.d_receivers;
+  o.mask = h.d_mask;
+  o.count = h.d_result;
+  o.max_edges = h.contract.max_edges;
+  o.reset_end = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
+                                                           : h.contract.max_edges;
+  o.edge_f = static_cast<S *>(h.d_edge_f);
+  o.f = f;
+  o.scale = scale;
+  o.partials = h.d_partials;
+  o.ntiles = ntiles;
+  o.slot0_from = slot0_from;
+  o.block_energy = block_energy;
+  o.nlocal = nlocal;
+  o.nall = nlocal + nghost;
+  return o;
+}
+
+static hipError_t launch_fdotr(Handle &h, hipStream_t s, double *f, const double *x, int nall,
+                               int ntiles, double scale, int flags)
+{
+  const int fdotr = h.contract.newton_pair ? 1 : 0;
+  const int grid = grid_for(h, ntiles, 4, 2);
+  StageTimer timer(h, s, "virial_fdotr");
+  if ((flags & LK_VIRIAL) && fdotr)
+    hipLaunchKernelGGL((k_fdotr_rows<true>), dim3(grid), dim3(256), 0, s, f, x, nall, fdotr,
+                       h.d_partials, ntiles, scale, flags, h.d_result, h.d_done, h.d_host_result);
+  else
+    hipLaunchKernelGGL((k_fdotr_rows<false>), dim3(grid), dim3(256), 0, s, f, x, nall, fdotr,
+                       h.d_partials, ntiles, scale, flags, h.d_result, h.d_done, h.d_host_result);
+  return hipGetLastError();
+}
+
+template <typename S>
+static hipError_t eam_edge_force(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
+                                 double scale, double *f, const double *x, bool from_list)
+{
+  EamArgs<S> m = eam_args<S>(h, nlocal, scale, f);
+  TwoSided t = two_sided_args(h, nlocal, nghost, x);
+  if (from_list) t.inc_bit = h.d_inc_bit;
+  m.flags = flags;
+  S *rho_part = static_cast<S *>(h.d_rho_part);
+  S *epair = static_cast<S *>(h.d_epair);
+  if (t.nblk > 0) {
+    StageTimer timer(h, s, "eam_density");
+    hipLaunchKernelGGL((k_eam_density_inc<S, true>), dim3(grid_for(h, t.nblk, 1, 1)),
+                       dim3(kRowBlock), 0, s, m, t, rho_part, epair);
+  }
+  if (t.nblk > 0) {
+    StageTimer timer(h, s, "eam_embed");
+    hipLaunchKernelGGL((k_eam_embed_inc<S, true>), dim3(t.nblk), dim3(kWave), 0, s, m, t,
+                       static_cast<const S *>(rho_part), static_cast<const S *>(epair));
+  }
+  int egrid = grid_for(h, h.contract.max_edges, kRowBlock, 1);
+  if (egrid > h.partial_slots) egrid = h.partial_slots;
+  const int ntiles = t.nblk > egrid ? t.nblk : egrid;
+  const EdgeOut<S> o = edge_out<S>(h, nlocal, nghost, scale, f, ntiles, t.nblk, 0);
+  {
+    StageTimer timer(h, s, "edge_force");
+    if (h.contract.newton_pair)
+      hipLaunchKernelGGL((k_eam_edge_force<S, true>), dim3(egrid), dim3(kRowBlock), 0, s, m, o);
+    else
+      hipLaunchKernelGGL((k_eam_edge_force<S, false>), dim3(egrid), dim3(kRowBlock), 0, s, m, o);
+  }
+  return launch_fdotr(h, s, f, x, nlocal + nghost, ntiles, scale, flags);
+}
+
+template <typename S>
+static hipError_t lj_edge_force(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
+                                double scale, double *f, const double *x)
+{
+  LjModel<S> m{};
+  m.atoms = static_cast<const Atom4<S> *>(h.d_atoms);
+  m.cutsq = static_cast<S>(h.lj.cutoff * h.lj.cutoff);
+  m.sigsq = static_cast<S>(h.lj.sigma * h.lj.sigma);
+  m.four_eps = static_cast<S>(4.0 * h.lj.epsilon);
+  m.edge_scale = static_cast<S>(h.lj.edge_energy_scale);
+  const int nall = nlocal + nghost;
+  const int nblk = (nall + kWave - 1) / kWave;
+  int egrid = grid_for(h, h.contract.max_edges, 256, 4);
+  if (egrid > h.partial_slots) egrid = h.partial_slots;
+  const int ntiles = nblk > egrid ? nblk : egrid;
+  const EdgeOut<S> o = edge_out<S>(h, nlocal, nghost, scale, f, ntiles, 0, 1);
+  {
+    StageTimer timer(h, s, "edge_force");
+    if (h.contract.newton_pair)
+      hipLaunchKernelGGL((k_lj_edge_force<S, true>), dim3(egrid), dim3(256), 0, s, m, o);
+    else
+      hipLaunchKernelGGL((k_lj_edge_force<S, false>), dim3(egrid), dim3(256), 0, s, m, o);
+  }
+  return launch_fdotr(h, s, f, x, nall, ntiles, scale, flags);
+}
+
+hipError_t launch_edge_force(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
+                             double scale, double *f, const double *x, bool from_list)
+{
+  const bool f64 = h.contract.precision == LK_FLOAT64;
+  if (h.model == 2)
+    return f64 ? lj_edge_force<double>(h, s, nlocal, nghost, flags, scale, f, x)
+               : lj_edge_force<float>(h, s, nlocal, nghost, flags, scale, f, x);
+  hipError_t e = hipSuccess;
+  if (from_list) {
+    Handle::IncKey key;
+    key.epoch = h.list_epoch;
+    key.ilist = h.list_ilist;
+    key.neighbors = h.list_neighbors;
+    key.stride = h.list_stride;
+    key.rows = h.list_rows;
+    key.maxneighs = h.list_maxneighs;
+    key.half_filter = h.list_half_filter;
+    if (h.list_epoch < 0 || !(key == h.inc_key)) {
+      e = build_incidence_from_list(h, s, nlocal + nghost);
+      h.inc_key = key;
+    }
+  } else {
+    e = build_incidence(h, s, nlocal + nghost);
+    h.inc_key = Handle::IncKey{};
+  }
+  if (e != hipSuccess) return e;
+  return f64 ? eam_edge_force<double>(h, s, nlocal, nghost, flags, scale, f, x, from_list)
+             : eam_edge_force<float>(h, s, nlocal, nghost, flags, scale, f, x, from_list);
+}
+
 hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
                             double scale, double *f, const double *x, bool from_list)
 {

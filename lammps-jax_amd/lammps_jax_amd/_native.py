@@ -31,7 +31,7 @@ EXPORTED = (
     "lk_create", "lk_destroy", "lk_last_error", "lk_set_eam", "lk_set_lj",
     "lk_set_accumulation", "lk_set_list_epoch", "lk_set_ghost_map", "lk_pack_atoms", "lk_pack_edges", "lk_compute",
     "lk_pack_compute", "lk_step_result", "lk_timing_enable", "lk_timing_read", "lk_edge_buffers",
-    "lk_staging_buffers", "lk_model_buffers", "lk_bundle_load", "lk_bundle_free",
+    "lk_staging_buffers", "lk_model_buffers", "lk_edge_forces", "lk_bundle_load", "lk_bundle_free",
     "lk_bundle_contract", "lk_bundle_model", "lk_bundle_unit_style",
 )
 
@@ -138,6 +138,8 @@ def load() -> ctypes.CDLL:
     lib.lk_staging_buffers.restype = ip
     lib.lk_model_buffers.argtypes = [vp, pp(vp), pp(vp)]
     lib.lk_model_buffers.restype = ip
+    lib.lk_edge_forces.argtypes = [vp, pp(vp)]
+    lib.lk_edge_forces.restype = ip
     lib.lk_bundle_load.argtypes = [ctypes.c_char_p, pp(vp), ctypes.c_char_p, ip]
     lib.lk_bundle_load.restype = ip
     lib.lk_bundle_free.argtypes = [vp]

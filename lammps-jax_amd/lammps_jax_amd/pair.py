@@ -221,7 +221,8 @@ class PairJax:
 
     def __init__(self, system, model, *, precision=8, accumulation="onesided", n_hops=1,
                  max_atoms=None, edges_per_atom=128, max_edges=None, scale=1.0, device="cuda:0",
-                 newton_pair=True, comm=None, pairing="full", pair_sum=False, fused=True):
+                 newton_pair=True, comm=None, pairing="full", pair_sum=False, fused=True,
+                 edge_force=False):
         torch = _torch()
         self.torch = torch
         self.device = torch.device(device)
@@ -247,7 +248,8 @@ class PairJax:
         contract = contract_for(max_atoms=self.max_atoms, max_edges=self.max_edges,
                                 cutoff=cutoff, precision=precision, newton=newton,
                                 pairing=pairing, n_hops=n_hops, comm=comm,
-                                newton_pair=newton_pair, half_list=half_list, pair_sum=pair_sum)
+                                newton_pair=newton_pair, half_list=half_list, pair_sum=pair_sum,
+                                edge_force=edge_force)
         self._setup(contract, accumulation)
 
     def _setup(self, contract: N.LkContract, accumulation) -> None:
@@ -404,6 +406,13 @@ class PairJax:
         dt = np.float64 if self.contract.precision == 8 else np.float32
         atoms = read_device(a_ptr, 4 * self.max_atoms, dt).reshape(self.max_atoms, 4)
         return atoms, read_device(sp_ptr, self.max_atoms, np.int32)
+
+    def edge_forces(self) -> np.ndarray:
+        """The per-edge model forces of an edge-force contract, [max_edges, 3]."""
+        ptr = ctypes.c_void_p()
+        self.h.check(self.h.lib.lk_edge_forces(self.h.ptr, ctypes.byref(ptr)))
+        dt = np.float64 if self.contract.precision == 8 else np.float32
+        return read_device(ptr.value, 3 * self.max_edges, dt).reshape(self.max_edges, 3)
 
     def model_rows(self):
         rho_ptr, fp_ptr = self.h.model_buffers()

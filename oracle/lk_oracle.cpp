@@ -21,6 +21,9 @@
 //   python/lammps_jax/eam_pallas.py:181-249 row kernels, full list -> or_eam_compute (onesided)
 //   python/lammps_jax/export.py:54-59, 153-209 energy selection, autodiff forces
 //   examples/export_model.py:16-74     LJ 12-6                      -> or_lj_compute
+//   python/lammps_jax/eam.py:336-409   make_setfl_edge_force        -> or_eam_edge_forces
+//   examples/export_model.py:52-74     make_lj_edge_force           -> or_lj_edge_forces
+//   cpp/pair_jax_kokkos.cpp:194-225    AddEdgeForcesFunctor         -> or_add_edge_forces
 //
 // Forces are the closed-form gradient of the restated energy (the reference takes them by
 // autodiff); tests pin them by finite differences of or_eam_compute's energy, by the dense
@@ -353,9 +356,148 @@ double lj_compute(double epsilon, double sigma, double cutoff, double edge_energ
   return energy;
 }
 
+// make_setfl_edge_force (python/lammps_jax/eam.py:336-409), the communicating half-edge export:
+// density to both endpoints, ghost partials folded into their owners and the completed density
+// forwarded back (reverse then forward comm), F' on every row; per edge the force on the sender
+// psip / r * (x_r - x_s), psip = F'_s rho'_{Z_r}(r) + F'_r rho'_{Z_s}(r) + phi'(r); zero on
+// invalid edges (masked, or r^2 >= cutoff^2).
+template <typename S>
+void eam_edge_forces(const Tables<S> &T, const double *positions_d, const int *species,
+                     int max_atoms, int nlocal, int nghost, const int *senders,
+                     const int *receivers, const unsigned char *mask, long n_edges,
+                     const int *ghost_owner, double *edge_forces)
+{
+  const int nall = nlocal + nghost;
+  std::vector<S> pos(static_cast<size_t>(max_atoms) * 3);
+  for (long k = 0; k < static_cast<long>(max_atoms) * 3; ++k) pos[k] = static_cast<S>(positions_d[k]);
+  const S *dens = T.dens.data();
+  const S *pairt = T.pair.data();
+  const S *emb = T.emb.data();
+  const long nr4 = 4L * T.nr, nrho4 = 4L * T.nrho;
+  auto geom = [&](long e, int &s, int &r, S d[3], S &rr) -> bool {
+    if (!mask[e]) return false;
+    s = senders[e];
+    r = receivers[e];
+    if (s < 0 || s >= max_atoms || r < 0 || r >= max_atoms) return false;
+    for (int k = 0; k < 3; ++k) d[k] = pos[3 * r + k] - pos[3 * s + k];
+    const S r2 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
+    if (!(r2 < T.cutsq)) return false;
+    rr = std::sqrt(r2);
+    return true;
+  };
+  std::vector<S> rho(max_atoms, S(0)), fp(max_atoms, S(0));
+  for (long e = 0; e < n_edges; ++e) {
+    int s, r;
+    S d[3], rr;
+    if (!geom(e, s, r, d, rr)) continue;
+    rho[s] += spline_value(dens + species[r] * nr4, T.nr, T.dr, rr, false);
+    rho[r] += spline_value(dens + species[s] * nr4, T.nr, T.dr, rr, false);
+  }
+  if (ghost_owner) {
+    for (int g = nlocal; g < nall; ++g) rho[ghost_owner[g - nlocal]] += rho[g];
+    for (int g = nlocal; g < nall; ++g) rho[g] = rho[ghost_owner[g - nlocal]];
+  }
+  for (int i = 0; i < max_atoms; ++i)
+    fp[i] = spline_slope(emb + species[i] * nrho4, T.nrho, T.drho, rho[i], true);
+  for (long e = 0; e < n_edges; ++e) {
+    int s, r;
+    S d[3], rr;
+    double *out = edge_forces + 3 * e;
+    out[0] = out[1] = out[2] = 0.0;
+    if (!geom(e, s, r, d, rr)) continue;
+    const int zs = species[s], zr = species[r];
+    const S *cp = pairt + pair_row(zs, zr) * nr4;
+    const S z2 = spline_value(cp, T.nr, T.dr, rr, false);
+    const S z2p = spline_slope(cp, T.nr, T.dr, rr, false);
+    const S phi = z2 / rr;
+    const S phip = (z2p - phi) / rr;
+    const S rhojp = spline_slope(dens + zr * nr4, T.nr, T.dr, rr, false);
+    const S rhoip = spline_slope(dens + zs * nr4, T.nr, T.dr, rr, false);
+    const S psip = fp[s] * rhojp + fp[r] * rhoip + phip;
+    const S coef = psip / rr;
+    for (int k = 0; k < 3; ++k) out[k] = static_cast<double>(coef * d[k]);
+  }
+}
+
+// make_lj_edge_force (examples/export_model.py:52-74): per edge dU/d(r_ij), r_ij = x_r - x_s, the
+// force on the sender; U = 4 eps (u^6 - u^3) with u = sigma^2 / r^2, zero on invalid edges.
+template <typename S>
+void lj_edge_forces(double epsilon, double sigma, double cutoff, const double *positions_d,
+                    int max_atoms, const int *senders, const int *receivers,
+                    const unsigned char *mask, long n_edges, double *edge_forces)
+{
+  const S cutsq = static_cast<S>(cutoff * cutoff);
+  const S sigsq = static_cast<S>(sigma * sigma);
+  const S four_eps = static_cast<S>(4.0 * epsilon);
+  const S tiny = static_cast<S>(1.0e-12);
+  for (long e = 0; e < n_edges; ++e) {
+    double *out = edge_forces + 3 * e;
+    out[0] = out[1] = out[2] = 0.0;
+    if (!mask[e]) continue;
+    const int s = senders[e], r = receivers[e];
+    if (s < 0 || s >= max_atoms || r < 0 || r >= max_atoms) continue;
+    S d[3];
+    for (int k = 0; k < 3; ++k)
+      d[k] = static_cast<S>(positions_d[3 * r + k]) - static_cast<S>(positions_d[3 * s + k]);
+    const S r2 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
+    if (!(r2 > tiny && r2 < cutsq)) continue;
+    const S u = sigsq / r2;
+    const S u3 = u * u * u;
+    const S dedr2 = -four_eps * (S(6) * u3 * u3 - S(3) * u3) / r2;
+    for (int k = 0; k < 3; ++k) out[k] = static_cast<double>(S(2) * dedr2 * d[k]);
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+double or_eam_edge_forces(int n_el, int nrho, double drho, int nr, double dr, double cutoff,
+                          const double *emb, const double *dens, const double *pair,
+                          int precision, const double *positions, const int *species,
+                          int max_atoms, int nlocal, int nghost, const int *senders,
+                          const int *receivers, const unsigned char *mask, long n_edges,
+                          const int *ghost_owner, double *edge_forces)
+{
+  if (precision == 4) {
+    auto T = make_tables<float>(n_el, nrho, drho, nr, dr, cutoff, emb, dens, pair);
+    eam_edge_forces<float>(T, positions, species, max_atoms, nlocal, nghost, senders, receivers,
+                           mask, n_edges, ghost_owner, edge_forces);
+  } else {
+    auto T = make_tables<double>(n_el, nrho, drho, nr, dr, cutoff, emb, dens, pair);
+    eam_edge_forces<double>(T, positions, species, max_atoms, nlocal, nghost, senders,
+                            receivers, mask, n_edges, ghost_owner, edge_forces);
+  }
+  return 0.0;
+}
+
+void or_lj_edge_forces(double epsilon, double sigma, double cutoff, int precision,
+                       const double *positions, int max_atoms, const int *senders,
+                       const int *receivers, const unsigned char *mask, long n_edges,
+                       double *edge_forces)
+{
+  if (precision == 4)
+    lj_edge_forces<float>(epsilon, sigma, cutoff, positions, max_atoms, senders, receivers, mask,
+                          n_edges, edge_forces);
+  else
+    lj_edge_forces<double>(epsilon, sigma, cutoff, positions, max_atoms, senders, receivers,
+                           mask, n_edges, edge_forces);
+}
+
+// cpp/pair_jax_kokkos.cpp:194-225 and 963-970 — over [0, count): f(i) += scale * F_e, and with
+// newton pair f(j) -= scale * F_e (in edge order here; the reference adds atomically).
+void or_add_edge_forces(double *f, const double *edge_forces, const int *senders,
+                        const int *receivers, long count, int newton_pair, double scale)
+{
+  for (long e = 0; e < count; ++e) {
+    const int i = senders[e], j = receivers[e];
+    for (int k = 0; k < 3; ++k) {
+      const double v = scale * edge_forces[3 * e + k];
+      f[3 * i + k] += v;
+      if (newton_pair) f[3 * j + k] -= v;
+    }
+  }
+}
 
 // eam.py:115-135 — PairEAM::interpolate coefficients for a uniformly tabulated function.
 void or_spline_coefficients(const double *f, int n, double *coef)

@@ -59,6 +59,13 @@ def _load():
     lib.or_lj_compute.argtypes = [dp, dp, dp, dp, ip, vp, ip, ip, ip, vp, vp, vp, lp, ip, ip, vp,
                                   vp]
     lib.or_lj_compute.restype = dp
+    lib.or_eam_edge_forces.argtypes = [ip, ip, dp, ip, dp, dp, vp, vp, vp, ip, vp, vp, ip, ip,
+                                       ip, vp, vp, vp, lp, vp, vp]
+    lib.or_eam_edge_forces.restype = dp
+    lib.or_lj_edge_forces.argtypes = [dp, dp, dp, ip, vp, ip, vp, vp, vp, lp, vp]
+    lib.or_lj_edge_forces.restype = None
+    lib.or_add_edge_forces.argtypes = [vp, vp, vp, vp, lp, ip, dp]
+    lib.or_add_edge_forces.restype = None
     lib.or_num_threads.argtypes = []
     lib.or_num_threads.restype = ip
     _lib = lib
@@ -163,6 +170,48 @@ def lj_compute(params, positions, *, nlocal, nghost, senders, receivers, mask, m
         int(max_atoms), int(nlocal), int(nghost), s.ctypes.data, r.ctypes.data, m.ctypes.data,
         int(len(s)), int(mode), int(owned_rows_only), forces.ctypes.data, vir.ctypes.data)
     return dict(energy=e, forces=forces, virial=vir)
+
+
+def eam_edge_forces(tables, positions, species, *, nlocal, nghost, senders, receivers, mask,
+                    precision=8, ghost_owner=None):
+    """make_setfl_edge_force of the communicating half-edge export (eam.py:336-409): the force
+    on each edge's sender, [n_edges, 3], zero on invalid edges."""
+    pos = _c(positions, np.float64)
+    max_atoms = pos.shape[0]
+    sp = _c(species, np.int32)
+    s, r, m = _c(senders, np.int32), _c(receivers, np.int32), _c(mask, np.uint8)
+    emb, dens, pair = (_c(tables[k], np.float64) for k in ("embedding", "density", "pair"))
+    go = None if ghost_owner is None else _c(ghost_owner, np.int32)
+    out = np.zeros((len(s), 3))
+    _load().or_eam_edge_forces(
+        int(emb.shape[0]), int(tables["nrho"]), float(tables["drho"]), int(tables["nr"]),
+        float(tables["dr"]), float(tables["cutoff"]), emb.ctypes.data, dens.ctypes.data,
+        pair.ctypes.data, int(precision), pos.ctypes.data, sp.ctypes.data, int(max_atoms),
+        int(nlocal), int(nghost), s.ctypes.data, r.ctypes.data, m.ctypes.data, int(len(s)),
+        None if go is None else go.ctypes.data, out.ctypes.data)
+    return out
+
+
+def lj_edge_forces(params, positions, *, senders, receivers, mask, precision=8):
+    """make_lj_edge_force (examples/export_model.py:52-74): dU/d(r_ij) per edge."""
+    pos = _c(positions, np.float64)
+    s, r, m = _c(senders, np.int32), _c(receivers, np.int32), _c(mask, np.uint8)
+    out = np.zeros((len(s), 3))
+    _load().or_lj_edge_forces(float(params["epsilon"]), float(params["sigma"]),
+                              float(params["cutoff"]), int(precision), pos.ctypes.data,
+                              int(pos.shape[0]), s.ctypes.data, r.ctypes.data, m.ctypes.data,
+                              int(len(s)), out.ctypes.data)
+    return out
+
+
+def add_edge_forces(f, edge_forces, senders, receivers, count, newton_pair=True, scale=1.0):
+    """AddEdgeForcesFunctor (cpp:194-225) over [0, count)."""
+    f = _c(f, np.float64).copy()
+    ef = _c(edge_forces, np.float64)
+    s, r = _c(senders, np.int32), _c(receivers, np.int32)
+    _load().or_add_edge_forces(f.ctypes.data, ef.ctypes.data, s.ctypes.data, r.ctypes.data,
+                               int(count), int(bool(newton_pair)), float(scale))
+    return f
 
 
 def add_forces(f, model_forces, rows, scale=1.0):

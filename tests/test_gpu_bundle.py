@@ -94,3 +94,27 @@ def test_negative_control_edge_capacity(gpu, tmp_path):
     pb = PairJax.from_bundle(path, sysm)
     with pytest.raises(N.LammpsJaxError, match="capacity exceeded"):
         pb.compute()
+
+
+def test_lj_edge_force_bundle_takes_the_half_list(gpu, tmp_path):
+    """force_output edge-force with newton on: the bundle takes the LAMMPS half list
+    (PairJaxKokkos::half_list, cpp:425-431) and the step equals the directly built handle."""
+    wl = systems.make_workload("lj_fcc_1k", cells=(5, 5, 5), seed=15)
+    sysm = wl.system()
+    sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_HALF)
+    lj = dict(wl.lj, edge_energy_scale=1.0)
+    max_atoms = sysm.nall + 64
+    path = tmp_path / "lj_edge.json"
+    write_bundle(path, kind="lj/cut", max_atoms=max_atoms, max_edges=max_atoms * 48,
+                 cutoff=wl.cutoff, unit_style="lj", lj=lj, force_output="edge-force",
+                 accumulation="plain")
+    print("bundle case lj edge-force half list", flush=True)
+    pb = PairJax.from_bundle(path, sysm, units="lj")
+    assert pb.contract.edge_force == 1 and pb.contract.half_list == 1
+    info = pb.compute()
+    pd = PairJax(sysm, ("lj", lj), precision=8, accumulation="plain", edge_force=True,
+                 max_atoms=max_atoms, max_edges=max_atoms * 48)
+    ref = pd.compute()
+    assert info.energy == pytest.approx(ref.energy, rel=1e-12)
+    assert rel_err(pb.forces(), pd.forces()) < 1e-12
+    np.testing.assert_array_equal(pb.edge_forces(), pd.edge_forces())

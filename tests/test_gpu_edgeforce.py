@@ -1,0 +1,142 @@
+"""GPU parity of the edge-force output (force_output = edge-force) against the oracle.
+
+The model writes the force on each packed edge's sender (make_setfl_edge_force, eam.py:336-409,
+for the communicating half-edge EAM export; make_lj_edge_force, examples/export_model.py:52-74,
+for LJ) and the pair style adds them into f (AddEdgeForcesFunctor, cpp/pair_jax_kokkos.cpp:
+194-225): f(s) += scale F_e, and f(r) -= scale F_e with newton pair. The packed edge order differs
+from the reference's (atomic) order, so per-edge forces are compared keyed by (sender,
+receiver). Tolerances: float64 1e-10 relative, float32 1e-5 relative (normwise)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from lk_testutil import rel_err
+from lammps_jax_amd import harness, systems
+from lammps_jax_amd.pair import PairJax
+
+pytestmark = pytest.mark.gpu
+
+TOL = {8: 1e-10, 4: 1e-5}
+
+
+def _keyed(senders, receivers, mask, forces, count):
+    """Live edges of [0, count) as {(sender, receiver): force row}, sorted by key."""
+    live = np.asarray(mask[:count]).astype(bool)
+    keys = np.stack([senders[:count][live], receivers[:count][live]], axis=1).astype(np.int64)
+    order = np.lexsort((keys[:, 1], keys[:, 0]))
+    return keys[order], np.asarray(forces[:count][live], dtype=np.float64)[order]
+
+
+def _check_edges(pj, count, s, r, m, ef_ref, tol):
+    ds, dr, dm = pj.edges()
+    ef = pj.edge_forces()
+    k_dev, f_dev = _keyed(ds, dr, dm, ef, count)
+    k_ref, f_ref = _keyed(s, r, m, ef_ref, count)
+    np.testing.assert_array_equal(k_dev, k_ref)
+    assert rel_err(f_dev, f_ref) < tol
+    assert np.all(ef[count:] == 0.0)
+
+
+@pytest.mark.parametrize("precision", [8, 4])
+def test_lj_edge_force_newton_on_half_list(gpu, precision):
+    wl = systems.make_workload("lj_fcc_1k", cells=(5, 5, 5), seed=11)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_HALF)
+    lj = dict(wl.lj, edge_energy_scale=1.0)  # newton-on edge-force export (export_model.py:106)
+    pj = PairJax(sysm, ("lj", lj), precision=precision, accumulation="plain", edge_force=True,
+                 scale=0.75)
+    print(f"edge-force case lj half list precision={precision} nall={sysm.nall}", flush=True)
+    info = pj.compute()
+    f = pj.forces()
+    pos, _ = O.pack_atoms(sysm.x, sysm.type, sysm.nall, pj.max_atoms, precision)
+    s, r, m, count, _ = O.pack_neighbors(sysm.x, lst, max_atoms=pj.max_atoms,
+                                         max_edges=pj.max_edges, nlocal=sysm.nlocal,
+                                         cutoff=wl.cutoff)
+    ef = O.lj_edge_forces(lj, pos, senders=s, receivers=r, mask=m, precision=precision)
+    tol = TOL[precision]
+    assert info.edge_count == count and info.edge_overflow == 0
+    _check_edges(pj, count, s, r, m, ef, tol)
+    f_ref = O.add_edge_forces(np.zeros((pj.max_atoms, 3)), ef, s, r, count, newton_pair=True,
+                              scale=0.75)
+    nall = sysm.nall
+    assert rel_err(f[:nall], f_ref[:nall]) < tol
+    e_ref = O.lj_compute(lj, pos, nlocal=sysm.nlocal, nghost=sysm.nghost, senders=s,
+                         receivers=r, mask=m, precision=precision)["energy"]
+    assert info.energy == pytest.approx(0.75 * e_ref, rel=tol)
+    assert rel_err(info.virial, O.virial_fdotr(f_ref, sysm.x, nall)) < tol
+
+
+def test_lj_edge_force_newton_off_full_list(gpu):
+    wl = systems.make_workload("lj_fcc_1k", cells=(5, 5, 5), seed=12)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    pj = PairJax(sysm, ("lj", wl.lj), precision=8, accumulation="plain", edge_force=True,
+                 newton_pair=False)
+    print(f"edge-force case lj full list newton off nall={sysm.nall}", flush=True)
+    info = pj.compute()
+    f = pj.forces()
+    pos, _ = O.pack_atoms(sysm.x, sysm.type, sysm.nall, pj.max_atoms, 8)
+    s, r, m, count, _ = O.pack_neighbors(sysm.x, lst, max_atoms=pj.max_atoms,
+                                         max_edges=pj.max_edges, nlocal=sysm.nlocal,
+                                         cutoff=wl.cutoff)
+    ef = O.lj_edge_forces(wl.lj, pos, senders=s, receivers=r, mask=m)
+    _check_edges(pj, count, s, r, m, ef, 1e-10)
+    f_ref = O.add_edge_forces(np.zeros((pj.max_atoms, 3)), ef, s, r, count, newton_pair=False)
+    nl = sysm.nlocal
+    assert rel_err(f[:nl], f_ref[:nl]) < 1e-10
+    assert np.all(f[nl:sysm.nall] == 0.0)  # newton off: receivers are left alone
+    e_ref = O.lj_compute(wl.lj, pos, nlocal=nl, nghost=sysm.nghost, senders=s, receivers=r,
+                         mask=m)["energy"]
+    assert info.energy == pytest.approx(e_ref, rel=1e-10)
+    assert np.all(info.virial == 0.0)  # newton off reports no pair virial (cpp:733-736)
+
+
+@pytest.mark.parametrize("precision", [8, 4])
+def test_eam_edge_force_communicating_half_list(gpu, precision):
+    wl = systems.make_workload("eam_alloy_8k", cells=(4, 4, 4), seed=13)
+    sysm = systems.System(wl.x, wl.types, wl.box, wl.cutoff + wl.skin)
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_HALF)
+    pj = PairJax(sysm, ("eam", wl.tables), precision=precision, accumulation="half",
+                 edge_force=True)
+    print(f"edge-force case eam half-unique precision={precision} nall={sysm.nall}", flush=True)
+    info = pj.compute()
+    f = pj.forces()
+    nl, ng, nall = sysm.nlocal, sysm.nghost, sysm.nall
+    pos, sp = O.pack_atoms(sysm.x, sysm.type, nall, pj.max_atoms, precision)
+    s, r, m, count, _ = O.pack_neighbors(sysm.x, lst, max_atoms=pj.max_atoms,
+                                         max_edges=pj.max_edges, nlocal=nl, cutoff=wl.cutoff)
+    ef = O.eam_edge_forces(wl.tables, pos, sp, nlocal=nl, nghost=ng, senders=s, receivers=r,
+                           mask=m, precision=precision, ghost_owner=sysm.ghost_owner)
+    tol = TOL[precision]
+    assert info.edge_count == count
+    _check_edges(pj, count, s, r, m, ef, tol)
+    f_ref = O.add_edge_forces(np.zeros((pj.max_atoms, 3)), ef, s, r, count, newton_pair=True)
+    assert rel_err(f[:nall], f_ref[:nall]) < tol
+    half = O.eam_compute(wl.tables, pos, sp, nlocal=nl, nghost=ng, senders=s, receivers=r,
+                         mask=m, mode=O.HALF, precision=precision, ghost_owner=sysm.ghost_owner)
+    assert info.energy == pytest.approx(half["energy"], rel=tol)
+    assert rel_err(info.virial, O.virial_fdotr(f_ref, sysm.x, nall)) < tol
+
+
+def test_edge_force_slots_past_the_count_are_cleared(gpu):
+    """A second step with fewer edges: the buffer past the new count holds zeros again."""
+    import torch
+
+    wl = systems.make_workload("lj_fcc_1k", cells=(5, 5, 5), seed=14)
+    sysm = wl.system()
+    sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_HALF)
+    pj = PairJax(sysm, ("lj", dict(wl.lj, edge_energy_scale=1.0)), precision=8,
+                 accumulation="plain", edge_force=True)
+    first = pj.compute()
+    # same list, atoms spread by 3%: fewer pairs inside the cutoff
+    center = sysm.x.mean(0)
+    spread = center + 1.03 * (sysm.x - center)
+    pj.x = torch.from_numpy(np.ascontiguousarray(spread)).to(pj.device)
+    second = pj.compute()
+    assert second.edge_count < first.edge_count
+    ef = pj.edge_forces()
+    assert np.all(ef[second.edge_count:] == 0.0)
+    assert np.any(ef[: second.edge_count] != 0.0)

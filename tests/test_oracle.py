@@ -441,3 +441,86 @@ def test_add_forces_known_answer():
     mf = np.array([[1.0, 1.0, 1.0], [2.0, 2.0, 2.0], [3.0, 3.0, 3.0]])
     out = O.add_forces(f0, mf, 2, scale=0.5)
     np.testing.assert_array_equal(out, [[1.5, 2.5, 3.5], [5.0, 6.0, 7.0], [7.0, 8.0, 9.0]])
+
+
+# --------------------------------------------------------------------------------------------
+# edge-force output (eam.py:336-409, export_model.py:52-74, cpp/pair_jax_kokkos.cpp:194-225)
+# --------------------------------------------------------------------------------------------
+
+def test_eam_edge_forces_scatter_to_the_dense_forces():
+    """Communicating half-edge export over a LAMMPS half list: the scattered per-edge forces
+    (sender +F, receiver -F, newton on) equal the half scheme's atom forces row by row, and after
+    the ghost rows fold into their owners they equal the dense pair_eam restatement."""
+    wl, sysm, _ = _periodic_alloy(seed=9)
+    t = wl.tables
+    nlocal, nghost = sysm.nlocal, sysm.nghost
+    nall = nlocal + nghost
+    max_atoms, max_edges = nall + 5, 64 * (nall + 5)
+    pos, sp = O.pack_atoms(sysm.x, sysm.type, nall, max_atoms, 8)
+    lst_h = sysm.build_list(wl.cutoff + wl.skin, kind=1)
+    s, r, m, count, ovf = O.pack_neighbors(sysm.x, lst_h, max_atoms=max_atoms,
+                                           max_edges=max_edges, nlocal=nlocal, cutoff=wl.cutoff)
+    assert ovf == 0
+    ef = O.eam_edge_forces(t, pos, sp, nlocal=nlocal, nghost=nghost, senders=s, receivers=r,
+                           mask=m, ghost_owner=sysm.ghost_owner)
+    assert np.all(ef[count:] == 0.0)
+    f = O.add_edge_forces(np.zeros((max_atoms, 3)), ef, s, r, count, newton_pair=True)
+    half = O.eam_compute(t, pos, sp, nlocal=nlocal, nghost=nghost, senders=s, receivers=r,
+                         mask=m, mode=O.HALF, ghost_owner=sysm.ghost_owner)
+    assert rel_err(f[:nall], half["forces"][:nall]) < 1e-12
+    _, f_d, _ = O.dense_eam(t, sysm.x[:nlocal], sp[:nlocal], box=sysm.box)
+    assert rel_err(fold_ghosts(f, nlocal, sysm.ghost_owner), f_d) < 1e-11
+    # scale multiplies every row; newton off leaves the receivers alone
+    f2 = O.add_edge_forces(np.zeros((max_atoms, 3)), ef, s, r, count, newton_pair=True, scale=0.5)
+    np.testing.assert_allclose(f2, 0.5 * f, rtol=0, atol=1e-12 * np.abs(f).max())
+    f_off = O.add_edge_forces(np.zeros((max_atoms, 3)), ef, s, r, count, newton_pair=False)
+    assert np.all(f_off[np.setdiff1d(np.arange(max_atoms), s[:count])] == 0.0)
+
+
+def test_lj_edge_forces_scatter_to_the_dense_forces():
+    """LJ edge forces: newton off over a full list (each owned row adds its own edges) and newton
+    on over a half list (both ends, ghost rows folded) both give the dense forces."""
+    wl = systems.make_workload("lj_fcc_1k", cells=(4, 4, 4), seed=6)
+    sysm = wl.system()
+    nlocal, nghost = sysm.nlocal, sysm.nghost
+    nall = nlocal + nghost
+    pos, _ = O.pack_atoms(sysm.x, sysm.type, nall, nall, 8)
+    _, f_d = O.dense_lj(sysm.x[:nlocal], box=sysm.box)
+    full = sysm.build_list(wl.cutoff + wl.skin)
+    s, r, m, count, _ = O.pack_neighbors(sysm.x, full, max_atoms=nall, max_edges=96 * nall,
+                                         nlocal=nlocal, cutoff=wl.cutoff)
+    ef = O.lj_edge_forces(LJ, pos, senders=s, receivers=r, mask=m)
+    f_off = O.add_edge_forces(np.zeros((nall, 3)), ef, s, r, count, newton_pair=False)
+    assert rel_err(f_off[:nlocal], f_d) < 1e-12
+    assert np.all(f_off[nlocal:] == 0.0)
+    half = sysm.build_list(wl.cutoff + wl.skin, kind=1)
+    hs, hr, hm, hcount, _ = O.pack_neighbors(sysm.x, half, max_atoms=nall, max_edges=96 * nall,
+                                             nlocal=nlocal, cutoff=wl.cutoff)
+    hef = O.lj_edge_forces(LJ, pos, senders=hs, receivers=hr, mask=hm)
+    f_on = O.add_edge_forces(np.zeros((nall, 3)), hef, hs, hr, hcount, newton_pair=True)
+    assert rel_err(fold_ghosts(f_on, nlocal, sysm.ghost_owner), f_d) < 1e-12
+    # the energy of a newton-on edge-force bundle counts each half-list pair once (scale 1.0)
+    e_d, _ = O.dense_lj(sysm.x[:nlocal], box=sysm.box)
+    e_half = O.lj_compute(dict(LJ, edge_energy_scale=1.0), pos, nlocal=nlocal, nghost=nghost,
+                          senders=hs, receivers=hr, mask=hm)["energy"]
+    assert e_half == pytest.approx(e_d, rel=1e-12)
+
+
+def test_lj_edge_force_is_the_pair_energy_gradient():
+    """dU/d(r_ij) of one edge by central differences of the oracle's pair energy."""
+    x = np.array([[0.3, -0.2, 0.1], [1.35, 0.4, -0.25]])
+    s, r, m = np.array([0]), np.array([1]), np.array([1], np.uint8)
+    ef = O.lj_edge_forces(LJ, x, senders=s, receivers=r, mask=m)[0]
+
+    def energy(xr):
+        pos = np.array([x[0], xr])
+        return O.lj_compute(dict(LJ, edge_energy_scale=1.0), pos, nlocal=2, nghost=0,
+                            senders=s, receivers=r, mask=m)["energy"]
+
+    h = 1e-6
+    grad = np.array([(energy(x[1] + h * e) - energy(x[1] - h * e)) / (2 * h) for e in np.eye(3)])
+    np.testing.assert_allclose(ef, grad, rtol=1e-7)
+    # past the cutoff and on masked slots: zero
+    far = np.array([[0.0, 0, 0], [3.0, 0, 0]])
+    assert np.all(O.lj_edge_forces(LJ, far, senders=s, receivers=r, mask=m) == 0.0)
+    assert np.all(O.lj_edge_forces(LJ, x, senders=s, receivers=r, mask=np.zeros(1, np.uint8)) == 0.0)
