@@ -51,6 +51,10 @@ extern "C" {
 #define LK_NEWTON_ON 1
 #define LK_NEWTON_OFF 2
 
+/* input layout (lammps_jax_model.h:12-16): packed sparse edges or the neighbour matrix */
+#define LK_LAYOUT_SPARSE_EDGE 0
+#define LK_LAYOUT_NEIGHBOR_MATRIX 1
+
 /* edge pairing (export.py:548-549): full, half, half-unique */
 #define LK_PAIRING_FULL 0
 #define LK_PAIRING_HALF 1
@@ -76,10 +80,10 @@ extern "C" {
 
 typedef struct lk_handle lk_handle;
 
-/* The bundle contract (lammps_jax_model.h:43-76), sparse-edge layout. */
+/* The bundle contract (lammps_jax_model.h:43-76). */
 typedef struct lk_contract {
   int max_atoms;     /* owned + ghost rows */
-  int max_edges;     /* packed edge slots */
+  int max_edges;     /* packed edge slots (sparse-edge layout) */
   int n_species;     /* 0: species-blind */
   int precision;     /* LK_FLOAT32 | LK_FLOAT64 */
   int newton;        /* LK_NEWTON_* */
@@ -91,6 +95,9 @@ typedef struct lk_contract {
   int newton_pair;   /* the run's newton pair setting (force->newton_pair) */
   int half_list;     /* the LAMMPS list is a half list (PairJaxKokkos::half_list, cpp:425-431) */
   double cutoff;     /* model cutoff (init_one) */
+  int input_layout;  /* LK_LAYOUT_*; 0 (sparse edges) for a zero-initialised contract */
+  int max_neighbors; /* neighbour-matrix slots per row */
+  int max_owned;     /* neighbour-matrix rows when > 0 (owned atoms only), else max_atoms */
 } lk_contract;
 
 /* setfl EAM tables: PairEAM::interpolate coefficients (eam.py:115-135), float64. */
@@ -153,6 +160,15 @@ int lk_set_list_epoch(lk_handle *h, long epoch);
 int lk_pack_atoms(lk_handle *h, void *stream, const double *x, const int *type, int nall);
 
 /*
+ * Sparse-edge contracts: cutoff-filters and compacts the Kokkos neighbour list into the packed
+ * edge arrays (described below). Neighbour-matrix contracts: copies the list into the
+ * [max_neighbors][rows] matrix instead (CopyNeighborMatrixFunctor, cpp/pair_jax_kokkos.cpp:
+ * 120-155, 824-842): column i is atom i's list (row i is atom i, ilist is not read), unused slots
+ * hold max_atoms, rows past the list are empty; the step result's edge count is the widest row
+ * and its overflow flag marks a row longer than max_neighbors (LAMMPS: "neighbor capacity
+ * exceeded"). The engine calls it on list rebuilds only (neighbor->ago == 0, cpp:1011-1012);
+ * lk_pack_compute copies when the list epoch changes.
+ *
  * Cutoff-filters and compacts the Kokkos neighbour list into the packed edge arrays.
  * ilist [inum+gnum], numneigh [nall], neighbors: LayoutLeft, entry (i, jj) at
  * neighbors[jj * nb_stride + i]; special-bond bits are masked off. Rows scanned are
@@ -237,6 +253,13 @@ int lk_model_buffers(lk_handle *h, void **rho, void **fp);
  * the step's edge count hold zeros. LK_ERR_STATE for atom-force contracts.
  */
 int lk_edge_forces(lk_handle *h, void **edge_forces);
+
+/*
+ * Neighbour-matrix contracts: the device matrix [max_neighbors][rows] and the per-row counts
+ * [rows] the model reads (the reference's d_neighbors / d_num_neighbors views, cpp:369-376).
+ * LK_ERR_STATE for sparse-edge contracts.
+ */
+int lk_neighbor_matrix(lk_handle *h, int **neighbors, int **num_neighbors);
 
 #ifdef __cplusplus
 }

@@ -55,7 +55,8 @@ void free_all(Handle &h)
                   h.d_tile_off,  h.d_bits,      h.d_fp,          h.d_rho,       h.d_partials,
                   h.d_result,    h.d_ghost_owner, h.d_ghost_off, h.d_ghost_list, h.d_done,
                   h.d_deg,       h.d_inc_loc,   h.d_inc_part,    h.d_inc_tmp,   h.d_inc,
-                  h.d_rho_part,  h.d_epair,     h.d_pack_state,  h.d_inc_bit,   h.d_edge_f};
+                  h.d_rho_part,  h.d_epair,     h.d_pack_state,  h.d_inc_bit,   h.d_edge_f,
+                  h.d_matrix,    h.d_num_neighbors, h.d_identity};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -138,9 +139,16 @@ int lk_create(const lk_contract *c, lk_handle **out)
   }
   h.contract = *c;
   *out = wrap;
+  const bool matrix = c->input_layout == LK_LAYOUT_NEIGHBOR_MATRIX;
+  if (!matrix && c->input_layout != LK_LAYOUT_SPARSE_EDGE)
+    return fail(h, LK_ERR_ARGUMENT,
+                "Unsupported LAMMPS-JAX input layout; re-export the bundle with the current "
+                "lammps_jax exporter");
   // cpp/lammps_jax_model.cpp:277-279
-  if (c->max_atoms <= 0 || c->max_edges <= 0)
+  if (c->max_atoms <= 0 || (matrix ? c->max_neighbors : c->max_edges) <= 0)
     return fail(h, LK_ERR_ARGUMENT, "Invalid fixed capacities in bundle");
+  if (c->max_owned < 0 || c->max_owned > c->max_atoms)
+    return fail(h, LK_ERR_ARGUMENT, "Invalid max_owned in bundle");
   if (c->precision != LK_FLOAT32 && c->precision != LK_FLOAT64)
     return fail(h, LK_ERR_ARGUMENT, "Unsupported LAMMPS-JAX precision; expected float32 or float64");
   if (c->n_hops < 1) return fail(h, LK_ERR_ARGUMENT, "Invalid n_hops in bundle");
@@ -174,6 +182,31 @@ int lk_create(const lk_contract *c, lk_handle **out)
     return fail(h, LK_ERR_ARGUMENT,
                 "Communicating edge-force bundles require half-edge packing; full pairing packs "
                 "both directions and the newton scatter doubles forces");
+  // cpp/lammps_jax_model.cpp:283-297 and cpp/pair_jax_kokkos.cpp:369-373
+  if (matrix && c->edge_force)
+    return fail(h, LK_ERR_ARGUMENT,
+                "Neighbor-matrix bundles return per-atom forces; edge-force output needs sparse "
+                "edges");
+  if (c->max_owned > 0 && !c->comm && !(matrix && c->n_hops == 1))
+    return fail(h, LK_ERR_ARGUMENT,
+                "max_owned needs a communicating or single-hop neighbor-matrix bundle; other "
+                "layouts hold ghost rows past the owned ones");
+  if (matrix && half_edges && !c->comm)
+    return fail(h, LK_ERR_ARGUMENT,
+                "Neighbor-matrix half pairing needs a communication schedule; the pair style "
+                "hands the model the LAMMPS half list as is");
+  if (matrix) {
+    const long rows = c->max_owned > 0 ? c->max_owned : c->max_atoms;
+    if (rows * c->max_neighbors > static_cast<long>(INT_MAX))
+      return fail(h, LK_ERR_ARGUMENT,
+                  "neighbor matrix rows times max_neighbors exceeds the int range; lower "
+                  "max_owned, max_atoms, or max_neighbors");
+    h.matrix = true;
+    h.matrix_rows = static_cast<int>(rows);
+    // the row kernels' internal edge capacity: every matrix slot (never exceeded)
+    h.contract.max_edges = static_cast<int>(rows * c->max_neighbors);
+    h.list_bits_filter = false;  // the model masks the matrix slots itself
+  }
   // init_style newton checks (cpp/pair_jax_kokkos.cpp:668-673)
   if (c->newton == LK_NEWTON_ON && !c->newton_pair)
     return fail(h, LK_ERR_ARGUMENT,
@@ -181,8 +214,11 @@ int lk_create(const lk_contract *c, lk_handle **out)
   if (c->newton == LK_NEWTON_OFF && c->newton_pair)
     return fail(h, LK_ERR_ARGUMENT,
                 "LAMMPS-JAX bundle was exported for newton pair off; this run uses newton on");
-  // default accumulation from the contract
-  if (half_edges)
+  // default accumulation from the contract; matrix bundles run the row models of their list
+  // (eam_pallas.py:313-343): half lists the half scheme, full lists the one-sided rows
+  if (matrix)
+    h.accum = half_edges ? LK_ACCUM_HALF : LK_ACCUM_ONESIDED;
+  else if (half_edges)
     h.accum = LK_ACCUM_HALF;
   else if (c->comm && !c->newton_pair)
     h.accum = LK_ACCUM_ONESIDED;
@@ -194,7 +230,7 @@ int lk_create(const lk_contract *c, lk_handle **out)
   e = hipDeviceGetAttribute(&h.num_cus, hipDeviceAttributeMultiprocessorCount, h.device);
   if (e != hipSuccess) return hip_fail(h, e, "hipDeviceGetAttribute");
   const size_t A = static_cast<size_t>(c->max_atoms);
-  const size_t E = static_cast<size_t>(c->max_edges);
+  const size_t E = static_cast<size_t>(h.contract.max_edges);
   const size_t S = h.scalar_bytes();
   const size_t tiles = A / lk::kWave + 2;
   if ((e = hipMalloc(&h.d_atoms, A * 4 * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(atoms)");
@@ -213,6 +249,19 @@ int lk_create(const lk_contract *c, lk_handle **out)
   if ((e = dalloc(&h.d_result, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(result)");
   if ((e = dalloc(&h.d_done, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(done)");
   if ((e = dalloc(&h.d_pack_state, 2)) != hipSuccess) return hip_fail(h, e, "hipMalloc(pack state)");
+  if (matrix) {
+    const size_t R = static_cast<size_t>(h.matrix_rows);
+    const size_t M = static_cast<size_t>(c->max_neighbors);
+    if ((e = dalloc(&h.d_matrix, R * M)) != hipSuccess) return hip_fail(h, e, "hipMalloc(neighbor matrix)");
+    if ((e = dalloc(&h.d_num_neighbors, R)) != hipSuccess) return hip_fail(h, e, "hipMalloc(num_neighbors)");
+    if ((e = dalloc(&h.d_identity, R)) != hipSuccess) return hip_fail(h, e, "hipMalloc(row ids)");
+    const long mblocks = static_cast<long>((R * M + 255) / 256);
+    hipLaunchKernelGGL(k_fill_int, dim3(mblocks), dim3(256), 0, 0, h.d_matrix,
+                       static_cast<long>(R * M), c->max_atoms);
+    (void)hipMemset(h.d_num_neighbors, 0, R * sizeof(int));
+    if ((e = lk::launch_iota(0, h.d_identity, static_cast<int>(R))) != hipSuccess)
+      return hip_fail(h, e, "row ids");
+  }
   if (c->edge_force) {
     // the model's per-edge force output, [max_edges][3] at the contract precision
     if ((e = hipMalloc(&h.d_edge_f, E * 3 * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(edge forces)");
@@ -324,6 +373,9 @@ int lk_set_lj(lk_handle *w, const lk_lj_params *p)
   Handle &h = w->h;
   if (!p || !(p->cutoff >= 0) || !(p->sigma > 0)) return fail(h, LK_ERR_ARGUMENT, "invalid LJ parameters");
   if (h.model != 0) return fail(h, LK_ERR_STATE, "a model is already loaded on this handle");
+  if (h.matrix)
+    return fail(h, LK_ERR_UNSUPPORTED,
+                "neighbor-matrix bundles run the EAM row models (eam_pallas.py:181-249)");
   if (h.contract.edge_force && (h.contract.comm || h.contract.pairing != LK_PAIRING_FULL))
     return fail(h, LK_ERR_UNSUPPORTED,
                 "edge-force LJ is the plain export (make_lj_edge_force): full pairing, no "
@@ -338,6 +390,10 @@ int lk_set_accumulation(lk_handle *w, int accum)
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
   const bool half_edges = h.contract.pairing != LK_PAIRING_FULL;
+  if (h.matrix && accum != (half_edges ? LK_ACCUM_HALF : LK_ACCUM_ONESIDED))
+    return fail(h, LK_ERR_ARGUMENT,
+                "neighbor-matrix bundles run the row model of their list (half scheme on half "
+                "lists, one-sided rows on full lists)");
   if (h.contract.edge_force && accum != (half_edges ? LK_ACCUM_HALF : LK_ACCUM_PLAIN))
     return fail(h, LK_ERR_ARGUMENT,
                 "edge-force output runs the two-sided scheme of its pairing (half for half-edge "
@@ -427,6 +483,7 @@ int lk_pack_atoms(lk_handle *w, void *stream, const double *x, const int *type, 
   Handle &h = w->h;
   if (nall < 0 || (nall > 0 && (!x || !type))) return fail(h, LK_ERR_ARGUMENT, "invalid atom arrays");
   h.x_last = x;
+  h.type_last = type;
   hipError_t e = lk::launch_pack_atoms(h, as_stream(stream), x, type, nall);
   if (e != hipSuccess) return hip_fail(h, e, "pack_atoms");
   h.result_mirrored = false;
@@ -452,6 +509,35 @@ int lk_pack_edges(lk_handle *w, void *stream, const double *x, const int *ilist,
   if (rows > 0 && (!x || !ilist || !numneigh || !neighbors))
     return fail(h, LK_ERR_ARGUMENT, "invalid neighbor list arrays");
   if (rows > 0 && nb_stride < 1) return fail(h, LK_ERR_ARGUMENT, "invalid neighbor stride");
+  if (h.matrix) {
+    // cpp/pair_jax_kokkos.cpp:824-842: row i is atom i, so the list must cover every owned atom
+    if (inum != nlocal)
+      return fail(h, LK_ERR_ARGUMENT,
+                  "LAMMPS-JAX neighbor-matrix bundles need a list over every atom; pair hybrid "
+                  "skip lists are unsupported");
+    const int num_rows = static_cast<int>(rows < h.matrix_rows ? rows : h.matrix_rows);
+    if (int rc = ensure_bits(h, c.max_neighbors)) return rc;
+    if (x) h.x_last = x;
+    hipError_t e = lk::launch_copy_matrix(h, as_stream(stream), numneigh, neighbors, nb_stride,
+                                          num_rows);
+    if (e != hipSuccess) return hip_fail(h, e, "copy_neighbor_matrix");
+    // the row kernels and the half scheme's incidence lists read the matrix as a list
+    h.list_ilist = h.d_identity;
+    h.list_numneigh = h.d_num_neighbors;
+    h.list_neighbors = h.d_matrix;
+    h.list_stride = h.matrix_rows;
+    h.list_rows = num_rows;
+    h.list_maxneighs = c.max_neighbors;
+    h.list_half_filter = 0;
+    h.list_unique = 0;
+    h.list_duplicate = 0;
+    h.inc_key = Handle::IncKey{};  // a new matrix: incidence lists are rebuilt
+    h.packed_rows = num_rows;
+    h.matrix_copied = true;
+    h.matrix_epoch = h.list_epoch;
+    h.result_mirrored = false;
+    return LK_OK;
+  }
   if (int rc = ensure_bits(h, max_neighbors_per_atom)) return rc;
   h.x_last = x;
   const bool half_edges = c.pairing != LK_PAIRING_FULL;
@@ -488,6 +574,37 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
   if (h.contract.pair_sum) return fail(h, LK_ERR_UNSUPPORTED, "pair-sum bundles carry no EAM/LJ model");
   hipStream_t s = as_stream(stream);
   hipError_t e = hipSuccess;
+  if (h.matrix) {
+    // cpp/pair_jax_kokkos.cpp:1043-1045
+    if (h.contract.max_owned > 0 && nlocal > h.contract.max_owned)
+      return fail(h, LK_ERR_CAPACITY,
+                  "LAMMPS-JAX owned-row capacity exceeded: global max " + std::to_string(nlocal) +
+                      " owned atoms, capacity " + std::to_string(h.contract.max_owned));
+    if (!h.matrix_copied)
+      return fail(h, LK_ERR_STATE,
+                  "the neighbor matrix has not been copied (lk_pack_edges on a list rebuild)");
+    if (nlocal + nghost > 0 && (!h.x_last || !h.type_last))
+      return fail(h, LK_ERR_STATE, "the row models need the atoms of a prior lk_pack_atoms");
+    if (nghost > 0 && (h.ghost_n != nghost || h.ghost_nlocal != nlocal))
+      return fail(h, LK_ERR_STATE,
+                  "the row models need the ghost map of this step (lk_set_ghost_map) for the "
+                  "density exchange");
+    if (h.accum == LK_ACCUM_ONESIDED) {
+      if (int rc = ensure_bits(h, h.contract.max_neighbors)) return rc;
+      e = lk::launch_step_onesided(h, s, h.x_last, h.type_last, nlocal + nghost, h.d_identity,
+                                   h.d_num_neighbors, h.d_matrix, h.matrix_rows, h.list_rows,
+                                   h.contract.max_neighbors, nlocal, nghost, flags, scale, f,
+                                   true, false);
+    } else {
+      if ((flags & LK_VIRIAL) && h.contract.newton_pair && nlocal + nghost > 0 && !h.x_last)
+        return fail(h, LK_ERR_STATE, "the f.r virial needs the positions of a prior pack");
+      if (int rc = ensure_incidence(h, 2L * h.list_rows * h.list_maxneighs)) return rc;
+      e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, h.x_last, true);
+    }
+    if (e != hipSuccess) return hip_fail(h, e, "compute");
+    h.result_mirrored = true;
+    return LK_OK;
+  }
   if (h.accum == LK_ACCUM_ONESIDED) {
     if (h.model == 1) {
       if (nghost > 0 && (h.ghost_n != nghost || h.ghost_nlocal != nlocal))
@@ -535,6 +652,15 @@ int lk_pack_compute(lk_handle *w, void *stream, const double *x, const int *type
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
   if (h.model == 0) return fail(h, LK_ERR_STATE, "LAMMPS-JAX runtime is not initialized");
+  if (h.matrix) {
+    // pack_atoms every step; the matrix copy only when the list was rebuilt (cpp:1011-1012)
+    int rc = lk_pack_atoms(w, stream, x, type, nall);
+    if (rc == LK_OK && (!h.matrix_copied || h.list_epoch < 0 || h.list_epoch != h.matrix_epoch))
+      rc = lk_pack_edges(w, stream, x, ilist, numneigh, neighbors, nb_stride, inum, gnum,
+                         maxneighs, nlocal);
+    if (rc == LK_OK) rc = lk_compute(w, stream, nlocal, nghost, flags, scale, f);
+    return rc;
+  }
   if (h.accum != LK_ACCUM_ONESIDED || h.contract.pair_sum) {
     // schemes without a fused form run the three entry points in order
     int rc = lk_pack_atoms(w, stream, x, type, nall);
@@ -659,6 +785,15 @@ int lk_edge_forces(lk_handle *w, void **edge_forces)
   if (!w || !edge_forces) return LK_ERR_ARGUMENT;
   *edge_forces = w->h.d_edge_f;
   if (!w->h.d_edge_f) return fail(w->h, LK_ERR_STATE, "the contract returns atom forces");
+  return LK_OK;
+}
+
+int lk_neighbor_matrix(lk_handle *w, int **neighbors, int **num_neighbors)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  if (!w->h.matrix) return fail(w->h, LK_ERR_STATE, "the contract has no neighbor matrix");
+  if (neighbors) *neighbors = w->h.d_matrix;
+  if (num_neighbors) *num_neighbors = w->h.d_num_neighbors;
   return LK_OK;
 }
 

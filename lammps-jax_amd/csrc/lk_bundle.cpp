@@ -428,8 +428,10 @@ int lk_bundle_contract(const lk_bundle *b, int newton_pair, lk_contract *out)
   else if (matrix) c.half_list = 0;
   else c.half_list = b->n_hops == 1 && (c.edge_force || b->pair_sum) ? 1 : 0;
   c.cutoff = b->cutoff;
+  c.input_layout = matrix ? LK_LAYOUT_NEIGHBOR_MATRIX : LK_LAYOUT_SPARSE_EDGE;
+  c.max_neighbors = b->max_neighbors;
+  c.max_owned = b->max_owned;
   *out = c;
-  if (b->input_layout != "sparse-edge") return LK_ERR_UNSUPPORTED;
   return LK_OK;
 }
 

@@ -113,6 +113,16 @@ struct Handle {
   void *d_rho_part = nullptr;   // [max_atoms] per-row density before the ghost fold
   void *d_epair = nullptr;      // [max_atoms] per-row pair energy
   const double *x_last = nullptr;  // engine positions of the last pack (f.r virial)
+  const int *type_last = nullptr;  // engine types of the last atom pack
+  // neighbour-matrix contracts (cpp/pair_jax_kokkos.cpp:369-376): [max_neighbors][matrix_rows]
+  bool matrix = false;
+  int matrix_rows = 0;             // max_owned when set, else max_atoms
+  int *d_matrix = nullptr;
+  int *d_num_neighbors = nullptr;
+  int *d_identity = nullptr;       // row i is atom i
+  bool matrix_copied = false;
+  long matrix_epoch = -2;          // list epoch of the last copy
+  bool list_bits_filter = true;    // list-built incidence filtered by the pack's validity bits
   uint32_t *d_inc_bit = nullptr;  // [capacity] validity-bit address of each list-built entry
   long inc_cap = 0;               // capacity of d_inc_tmp / d_inc / d_inc_bit (entries)
   // the neighbour list of the last lk_pack_edges: the two-sided incidence lists are built from
@@ -176,6 +186,9 @@ hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
 hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
                               double *f, int flags, const FusedPack &pack = FusedPack{});
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles);
+hipError_t launch_copy_matrix(Handle &h, hipStream_t s, const int *numneigh, const int *neighbors,
+                              long stride, int num_rows);
+hipError_t launch_iota(hipStream_t s, int *p, int n);
 hipError_t launch_edge_force(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
                              double scale, double *f, const double *x, bool from_list);
 
@@ -185,6 +198,7 @@ hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, in
 hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,
                                 int nall, const int *ilist, const int *numneigh,
                                 const int *neighbors, long stride, int num_rows, int maxneighs,
-                                int nlocal, int nghost, int flags, double scale, double *f);
+                                int nlocal, int nghost, int flags, double scale, double *f,
+                                bool matrix = false, bool atoms = true);
 
 }  // namespace lk

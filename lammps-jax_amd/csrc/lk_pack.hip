@@ -282,6 +282,72 @@ __global__ __launch_bounds__(W * 64) void k_pack_write(PackArgs a, const int *__
   }
 }
 
+// CopyNeighborMatrixFunctor (cpp/pair_jax_kokkos.cpp:120-155): flat = slot * rows + row, atom
+// fastest on both sides, so reads of the LayoutLeft list and writes of the matrix coalesce. Row i
+// is atom i. The step result's edge count takes the widest row, its overflow flag a row longer
+// than max_neighbors (that row is truncated).
+__global__ void k_matrix_counts_reset(StepResult *r)
+{
+  if (threadIdx.x == 0) {
+    r->edge_count = 0;
+    r->edge_overflow = 0;
+    r->ghost_sender = 0;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_copy_matrix(const int *__restrict__ numneigh,
+                                                     const int *__restrict__ neighbors,
+                                                     long stride, int num_rows, int rows,
+                                                     int max_atoms, int max_neighbors,
+                                                     int *__restrict__ matrix,
+                                                     int *__restrict__ num_out, StepResult *r)
+{
+  const long flat = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (flat >= static_cast<long>(rows) * max_neighbors) return;
+  const int slot = static_cast<int>(flat / rows);
+  const int i = static_cast<int>(flat % rows);
+  if (i >= num_rows) {
+    matrix[flat] = max_atoms;
+    if (slot == 0) num_out[i] = 0;
+    return;
+  }
+  const int n = numneigh[i];
+  if (slot == 0) {
+    atomicMax(&r->edge_count, n);
+    if (n > max_neighbors) r->edge_overflow = 1;
+    num_out[i] = n < max_neighbors ? n : max_neighbors;
+  }
+  int j = max_atoms;
+  if (slot < n) j = neighbors[static_cast<long>(slot) * stride + i] & kNeighMask;
+  matrix[flat] = j < max_atoms ? j : max_atoms;
+}
+
+hipError_t launch_copy_matrix(Handle &h, hipStream_t s, const int *numneigh, const int *neighbors,
+                              long stride, int num_rows)
+{
+  StageTimer timer(h, s, "copy_matrix");
+  hipLaunchKernelGGL(k_matrix_counts_reset, dim3(1), dim3(64), 0, s, h.d_result);
+  const long flat = static_cast<long>(h.matrix_rows) * h.contract.max_neighbors;
+  const long blocks = (flat + 255) / 256;
+  hipLaunchKernelGGL(k_copy_matrix, dim3(static_cast<unsigned>(blocks > 0 ? blocks : 1)),
+                     dim3(256), 0, s, numneigh, neighbors, stride, num_rows, h.matrix_rows,
+                     h.contract.max_atoms, h.contract.max_neighbors, h.d_matrix,
+                     h.d_num_neighbors, h.d_result);
+  return hipGetLastError();
+}
+
+__global__ void k_iota(int *p, int n)
+{
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = i;
+}
+
+hipError_t launch_iota(hipStream_t s, int *p, int n)
+{
+  hipLaunchKernelGGL(k_iota, dim3((n + 255) / 256 > 0 ? (n + 255) / 256 : 1), dim3(256), 0, s, p, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles)
 {
   hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(1024), 0, s, h.d_tile_count, tile_flags, ntiles,

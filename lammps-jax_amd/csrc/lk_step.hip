@@ -58,7 +58,10 @@ constexpr int kStepMaxWords = 8;   // validity words kept in LDS for the write (
 
 // K1. Block-uniform control flow around every barrier: the group walk has the same trip count
 // for all threads of a block, and fill_window is entered by all of them.
-template <typename S, bool EAM>
+// MATRIX: the list is the neighbour matrix of a matrix bundle. No packer filter applies: an
+// entry counts when the model's mask does (r^2 < cutoff^2 at the contract precision,
+// eam_pallas.py list_pair), and only the internal receivers are written for the force sweep.
+template <typename S, bool EAM, bool MATRIX>
 __global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves_per_eu(8)))
 void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
 {
@@ -127,11 +130,11 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
           const double dx = xi0 - xj0, dy = xi1 - xj1, dz = xi2 - xj2;
           rsq = dx * dx + dy * dy + dz * dz;
         }
-        if (rsq > p.cutsq) continue;  // PackNeighborFunctor keeps rsq <= cutsq (cpp:91)
-        word |= 1u << (jj & 31);
-        ++cnt;
+        if constexpr (!MATRIX) {
+          if (rsq > p.cutsq) continue;  // PackNeighborFunctor keeps rsq <= cutsq (cpp:91)
+        }
+        S r2 = S(0);
         if constexpr (EAM) {
-          S r2;
           if constexpr (sizeof(S) == 8) {
             r2 = rsq;  // the model's (x_j - x_i)^2 sum is the same float64 value
           } else {
@@ -141,7 +144,14 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
             const S dz = static_cast<S>(xj2) - static_cast<S>(xi2);
             r2 = dx * dx + dy * dy + dz * dz;
           }
-          if (r2 < a.cutsq) {  // valid = mask & r_sq < cutoff_sq (eam.py:288)
+        }
+        if constexpr (MATRIX) {
+          if (!(r2 < a.cutsq)) continue;
+        }
+        word |= 1u << (jj & 31);
+        ++cnt;
+        if constexpr (EAM) {
+          if (MATRIX || r2 < a.cutsq) {  // valid = mask & r_sq < cutoff_sq (eam.py:288)
             const S rr = r2 * rsqrt_nr(r2);
             const Locator<S> L = locate_mul(rr, a.inv_dr, a.nr);
             rho += cvalue(rcoef(win, a, L.node, clamp_species(zj, a.n_el)), L.t);
@@ -237,9 +247,11 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
           const int j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
           const long e = base + cursor + lanes_below(M);
           if (e < p.max_edges) {  // past the capacity the count still reports the demand
-            p.senders[e] = i;
             p.receivers[e] = j;
-            p.mask[e] = 1;
+            if constexpr (!MATRIX) {
+              p.senders[e] = i;
+              p.mask[e] = 1;
+            }
           }
         }
         cursor += __popcll(M);
@@ -249,11 +261,17 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
   }
 }
 
-template <typename S, bool EAM>
+__global__ void k_clear_state(int *state)
+{
+  if (threadIdx.x < 2) state[threadIdx.x] = 0;
+}
+
+template <typename S, bool EAM, bool MATRIX>
 static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,
                                 int nall, const int *ilist, const int *numneigh,
                                 const int *neighbors, long stride, int num_rows, int maxneighs,
-                                int nlocal, int nghost, int flags, double scale, double *f)
+                                int nlocal, int nghost, int flags, double scale, double *f,
+                                bool atoms)
 {
   h.packed_rows = num_rows;
   EamArgs<S> a{};
@@ -289,18 +307,24 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   p.ghost_list = h.d_ghost_list;
   const int ntiles = (num_rows + kWave - 1) / kWave;
   const int ngroups = ntiles > 0 ? (ntiles + kStepTPB - 1) / kStepTPB : 1;
-  // K0: atom records and species; zeroes the demand counter and the ghost-sender flag
-  if (hipError_t e0 = launch_pack_atoms(h, s, x, type, nall, h.d_pack_state); e0 != hipSuccess)
-    return e0;
+  // K0: atom records and species; zeroes the demand counter and the ghost-sender flag (the
+  // records of a separate lk_pack_atoms call are reused when `atoms` is false)
+  if (atoms) {
+    if (hipError_t e0 = launch_pack_atoms(h, s, x, type, nall, h.d_pack_state); e0 != hipSuccess)
+      return e0;
+  } else {
+    hipLaunchKernelGGL(k_clear_state, dim3(1), dim3(64), 0, s, h.d_pack_state);
+  }
   if (ntiles > 0) {
     StageTimer timer(h, s, "step_pack");
     const int grid = persistent_grid(ngroups, 2, h.num_cus);
-    hipLaunchKernelGGL((k_step_pack<S, EAM>), dim3(grid), dim3(kStepW * kStepTPB * kWave), 0, s,
-                       p, a, ngroups);
+    hipLaunchKernelGGL((k_step_pack<S, EAM, MATRIX>), dim3(grid),
+                       dim3(kStepW * kStepTPB * kWave), 0, s, p, a, ngroups);
   }
   ++h.pack_serial;
   FusedPack fp;
-  fp.counter = h.d_pack_state;
+  // matrix bundles keep the copy's widest row and overflow flag as the step's counts
+  fp.counter = MATRIX ? nullptr : h.d_pack_state;
   fp.senders = h.d_senders;
   fp.receivers = h.d_receivers;
   fp.mask = h.d_mask;
@@ -318,21 +342,35 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
 hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,
                                 int nall, const int *ilist, const int *numneigh,
                                 const int *neighbors, long stride, int num_rows, int maxneighs,
-                                int nlocal, int nghost, int flags, double scale, double *f)
+                                int nlocal, int nghost, int flags, double scale, double *f,
+                                bool matrix, bool atoms)
 {
   const bool f64 = h.contract.precision == LK_FLOAT64;
   const bool eam = h.model == 1;
+  if (matrix) {  // the matrix bundles are EAM row models
+    if (f64)
+      return step_onesided<double, true, true>(h, s, x, type, nall, ilist, numneigh, neighbors,
+                                               stride, num_rows, maxneighs, nlocal, nghost, flags,
+                                               scale, f, atoms);
+    return step_onesided<float, true, true>(h, s, x, type, nall, ilist, numneigh, neighbors,
+                                            stride, num_rows, maxneighs, nlocal, nghost, flags,
+                                            scale, f, atoms);
+  }
   if (f64 && eam)
-    return step_onesided<double, true>(h, s, x, type, nall, ilist, numneigh, neighbors, stride,
-                                       num_rows, maxneighs, nlocal, nghost, flags, scale, f);
+    return step_onesided<double, true, false>(h, s, x, type, nall, ilist, numneigh, neighbors,
+                                              stride, num_rows, maxneighs, nlocal, nghost, flags,
+                                              scale, f, atoms);
   if (f64)
-    return step_onesided<double, false>(h, s, x, type, nall, ilist, numneigh, neighbors, stride,
-                                        num_rows, maxneighs, nlocal, nghost, flags, scale, f);
+    return step_onesided<double, false, false>(h, s, x, type, nall, ilist, numneigh, neighbors,
+                                               stride, num_rows, maxneighs, nlocal, nghost, flags,
+                                               scale, f, atoms);
   if (eam)
-    return step_onesided<float, true>(h, s, x, type, nall, ilist, numneigh, neighbors, stride,
-                                      num_rows, maxneighs, nlocal, nghost, flags, scale, f);
-  return step_onesided<float, false>(h, s, x, type, nall, ilist, numneigh, neighbors, stride,
-                                     num_rows, maxneighs, nlocal, nghost, flags, scale, f);
+    return step_onesided<float, true, false>(h, s, x, type, nall, ilist, numneigh, neighbors,
+                                             stride, num_rows, maxneighs, nlocal, nghost, flags,
+                                             scale, f, atoms);
+  return step_onesided<float, false, false>(h, s, x, type, nall, ilist, numneigh, neighbors,
+                                            stride, num_rows, maxneighs, nlocal, nghost, flags,
+                                            scale, f, atoms);
 }
 
 }  // namespace lk

@@ -754,7 +754,7 @@ static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost
 {
   EamArgs<S> m = eam_args<S>(h, nlocal, scale, f);
   TwoSided t = two_sided_args(h, nlocal, nghost, x);
-  if (from_list) t.inc_bit = h.d_inc_bit;
+  if (from_list && h.list_bits_filter) t.inc_bit = h.d_inc_bit;
   m.flags = flags;
   S *rho_part = static_cast<S *>(h.d_rho_part);
   S *epair = static_cast<S *>(h.d_epair);
@@ -797,7 +797,7 @@ static hipError_t lj_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost,
   m.flags = flags;
   m.mirror = h.d_host_result;
   TwoSided t = two_sided_args(h, nlocal, nghost, x);
-  if (from_list) t.inc_bit = h.d_inc_bit;
+  if (from_list && h.list_bits_filter) t.inc_bit = h.d_inc_bit;
   const int grid = grid_for(h, t.nblk > 0 ? t.nblk : 1, 1, 2);
   StageTimer timer(h, s, "lj_rows");
   if (flags & LK_VIRIAL)
@@ -1049,7 +1049,7 @@ static hipError_t eam_edge_force(Handle &h, hipStream_t s, int nlocal, int nghos
 {
   EamArgs<S> m = eam_args<S>(h, nlocal, scale, f);
   TwoSided t = two_sided_args(h, nlocal, nghost, x);
-  if (from_list) t.inc_bit = h.d_inc_bit;
+  if (from_list && h.list_bits_filter) t.inc_bit = h.d_inc_bit;
   m.flags = flags;
   S *rho_part = static_cast<S *>(h.d_rho_part);
   S *epair = static_cast<S *>(h.d_epair);

@@ -21,6 +21,7 @@ LK_ERR_UNSUPPORTED = 5
 LK_FLOAT32 = 4
 LK_FLOAT64 = 8
 LK_NEWTON_ANY, LK_NEWTON_ON, LK_NEWTON_OFF = 0, 1, 2
+LK_LAYOUT_SPARSE_EDGE, LK_LAYOUT_NEIGHBOR_MATRIX = 0, 1
 LK_PAIRING_FULL, LK_PAIRING_HALF, LK_PAIRING_HALF_UNIQUE = 0, 1, 2
 LK_ACCUM_PLAIN, LK_ACCUM_HALF, LK_ACCUM_ONESIDED = 0, 1, 2
 LK_ENERGY = 1
@@ -31,7 +32,8 @@ EXPORTED = (
     "lk_create", "lk_destroy", "lk_last_error", "lk_set_eam", "lk_set_lj",
     "lk_set_accumulation", "lk_set_list_epoch", "lk_set_ghost_map", "lk_pack_atoms", "lk_pack_edges", "lk_compute",
     "lk_pack_compute", "lk_step_result", "lk_timing_enable", "lk_timing_read", "lk_edge_buffers",
-    "lk_staging_buffers", "lk_model_buffers", "lk_edge_forces", "lk_bundle_load", "lk_bundle_free",
+    "lk_staging_buffers", "lk_model_buffers", "lk_edge_forces", "lk_neighbor_matrix",
+    "lk_bundle_load", "lk_bundle_free",
     "lk_bundle_contract", "lk_bundle_model", "lk_bundle_unit_style",
 )
 
@@ -51,6 +53,9 @@ class LkContract(ctypes.Structure):
         ("newton_pair", ctypes.c_int),
         ("half_list", ctypes.c_int),
         ("cutoff", ctypes.c_double),
+        ("input_layout", ctypes.c_int),
+        ("max_neighbors", ctypes.c_int),
+        ("max_owned", ctypes.c_int),
     ]
 
 
@@ -140,6 +145,8 @@ def load() -> ctypes.CDLL:
     lib.lk_model_buffers.restype = ip
     lib.lk_edge_forces.argtypes = [vp, pp(vp)]
     lib.lk_edge_forces.restype = ip
+    lib.lk_neighbor_matrix.argtypes = [vp, pp(vp), pp(vp)]
+    lib.lk_neighbor_matrix.restype = ip
     lib.lk_bundle_load.argtypes = [ctypes.c_char_p, pp(vp), ctypes.c_char_p, ip]
     lib.lk_bundle_load.restype = ip
     lib.lk_bundle_free.argtypes = [vp]

@@ -27,7 +27,8 @@ class StepInfo:
 
 def contract_for(*, max_atoms, max_edges, cutoff, precision=8, newton="on", pairing="full",
                  n_hops=1, pair_sum=False, comm=False, edge_force=False, n_species=0,
-                 newton_pair=True, half_list=False) -> N.LkContract:
+                 newton_pair=True, half_list=False, layout="sparse-edge", max_neighbors=0,
+                 max_owned=0) -> N.LkContract:
     """The bundle contract fields the hot path reads (lammps_jax_model.h:43-76)."""
     c = N.LkContract()
     c.max_atoms = int(max_atoms)
@@ -44,6 +45,10 @@ def contract_for(*, max_atoms, max_edges, cutoff, precision=8, newton="on", pair
     c.newton_pair = int(bool(newton_pair))
     c.half_list = int(bool(half_list))
     c.cutoff = float(cutoff)
+    c.input_layout = {"sparse-edge": N.LK_LAYOUT_SPARSE_EDGE,
+                      "neighbor-matrix": N.LK_LAYOUT_NEIGHBOR_MATRIX}[layout]
+    c.max_neighbors = int(max_neighbors)
+    c.max_owned = int(max_owned)
     return c
 
 
@@ -222,7 +227,7 @@ class PairJax:
     def __init__(self, system, model, *, precision=8, accumulation="onesided", n_hops=1,
                  max_atoms=None, edges_per_atom=128, max_edges=None, scale=1.0, device="cuda:0",
                  newton_pair=True, comm=None, pairing="full", pair_sum=False, fused=True,
-                 edge_force=False):
+                 edge_force=False, layout="sparse-edge", max_neighbors=None, max_owned=0):
         torch = _torch()
         self.torch = torch
         self.device = torch.device(device)
@@ -249,7 +254,10 @@ class PairJax:
                                 cutoff=cutoff, precision=precision, newton=newton,
                                 pairing=pairing, n_hops=n_hops, comm=comm,
                                 newton_pair=newton_pair, half_list=half_list, pair_sum=pair_sum,
-                                edge_force=edge_force)
+                                edge_force=edge_force, layout=layout,
+                                max_neighbors=(max_neighbors if max_neighbors is not None
+                                               else max(1, lst["maxneighs"])),
+                                max_owned=max_owned)
         self._setup(contract, accumulation)
 
     def _setup(self, contract: N.LkContract, accumulation) -> None:
@@ -388,6 +396,11 @@ class PairJax:
         self.enqueue(eflag, vflag, fused=fused)
         info = self.h.step_result(self.stream())
         if check_capacity and info.edge_overflow:
+            if self.contract.input_layout == N.LK_LAYOUT_NEIGHBOR_MATRIX:  # cpp:1069-1072
+                raise N.LammpsJaxError(
+                    N.LK_ERR_CAPACITY,
+                    f"LAMMPS-JAX neighbor capacity exceeded: global max {info.edge_count} "
+                    f"neighbors per atom, capacity {self.contract.max_neighbors}")
             raise N.LammpsJaxError(
                 N.LK_ERR_CAPACITY,
                 f"LAMMPS-JAX edge capacity exceeded: global max {info.edge_count} edges, "
@@ -406,6 +419,16 @@ class PairJax:
         dt = np.float64 if self.contract.precision == 8 else np.float32
         atoms = read_device(a_ptr, 4 * self.max_atoms, dt).reshape(self.max_atoms, 4)
         return atoms, read_device(sp_ptr, self.max_atoms, np.int32)
+
+    def neighbor_matrix(self):
+        """The device neighbour matrix [max_neighbors, rows] and per-row counts of a matrix
+        contract."""
+        nb, num = ctypes.c_void_p(), ctypes.c_void_p()
+        self.h.check(self.h.lib.lk_neighbor_matrix(self.h.ptr, ctypes.byref(nb), ctypes.byref(num)))
+        c = self.contract
+        rows = c.max_owned if c.max_owned > 0 else c.max_atoms
+        m = read_device(nb.value, c.max_neighbors * rows, np.int32).reshape(c.max_neighbors, rows)
+        return m, read_device(num.value, rows, np.int32)
 
     def edge_forces(self) -> np.ndarray:
         """The per-edge model forces of an edge-force contract, [max_edges, 3]."""

@@ -24,6 +24,7 @@
 //   python/lammps_jax/eam.py:336-409   make_setfl_edge_force        -> or_eam_edge_forces
 //   examples/export_model.py:52-74     make_lj_edge_force           -> or_lj_edge_forces
 //   cpp/pair_jax_kokkos.cpp:194-225    AddEdgeForcesFunctor         -> or_add_edge_forces
+//   cpp/pair_jax_kokkos.cpp:120-155    CopyNeighborMatrixFunctor    -> or_copy_neighbor_matrix
 //
 // Forces are the closed-form gradient of the restated energy (the reference takes them by
 // autodiff); tests pin them by finite differences of or_eam_compute's energy, by the dense
@@ -482,6 +483,31 @@ void or_lj_edge_forces(double epsilon, double sigma, double cutoff, int precisio
   else
     lj_edge_forces<double>(epsilon, sigma, cutoff, positions, max_atoms, senders, receivers,
                            mask, n_edges, edge_forces);
+}
+
+// cpp/pair_jax_kokkos.cpp:120-155 (CopyNeighborMatrixFunctor) and 824-842: column i of the
+// [max_neighbors][rows] matrix is atom i's list (row i is atom i; ilist is not read), unused slots
+// hold max_atoms; rows past num_rows are empty; the widest row and the overflow flag (a row longer
+// than max_neighbors, truncated) are reported.
+void or_copy_neighbor_matrix(const int *numneigh, const int *neighbors, long stride, int num_rows,
+                             int rows, int max_atoms, int max_neighbors, int *matrix,
+                             int *num_neighbors, int *widest, int *overflow)
+{
+  *widest = 0;
+  *overflow = 0;
+  for (int i = 0; i < rows; ++i) {
+    const int n = i < num_rows ? numneigh[i] : 0;
+    if (i < num_rows) {
+      *widest = std::max(*widest, n);
+      if (n > max_neighbors) *overflow = 1;
+    }
+    num_neighbors[i] = std::min(n, max_neighbors);
+    for (int s = 0; s < max_neighbors; ++s) {
+      int j = max_atoms;
+      if (s < n) j = neighbors[static_cast<long>(s) * stride + i] & kNeighMask;
+      matrix[static_cast<long>(s) * rows + i] = j < max_atoms ? j : max_atoms;
+    }
+  }
 }
 
 // cpp/pair_jax_kokkos.cpp:194-225 and 963-970 — over [0, count): f(i) += scale * F_e, and with

@@ -66,6 +66,8 @@ def _load():
     lib.or_lj_edge_forces.restype = None
     lib.or_add_edge_forces.argtypes = [vp, vp, vp, vp, lp, ip, dp]
     lib.or_add_edge_forces.restype = None
+    lib.or_copy_neighbor_matrix.argtypes = [vp, vp, lp, ip, ip, ip, ip, vp, vp, vp, vp]
+    lib.or_copy_neighbor_matrix.restype = None
     lib.or_num_threads.argtypes = []
     lib.or_num_threads.restype = ip
     _lib = lib
@@ -212,6 +214,35 @@ def add_edge_forces(f, edge_forces, senders, receivers, count, newton_pair=True,
     _load().or_add_edge_forces(f.ctypes.data, ef.ctypes.data, s.ctypes.data, r.ctypes.data,
                                int(count), int(bool(newton_pair)), float(scale))
     return f
+
+
+def copy_neighbor_matrix(lst, *, rows, max_atoms, max_neighbors, n_hops=1):
+    """CopyNeighborMatrixFunctor (cpp:120-155) over the list's first rows (inum, + gnum with
+    n_hops > 1, clamped to max_atoms). Returns (matrix [max_neighbors, rows], num_neighbors
+    [rows], widest row, overflow)."""
+    numneigh = _c(lst["numneigh"], np.int32)
+    neighbors = _c(lst["neighbors"], np.int32)
+    num_rows = min(lst["inum"] + (lst["gnum"] if n_hops > 1 else 0), max_atoms, rows)
+    matrix = np.zeros((max_neighbors, rows), np.int32)
+    num = np.zeros(rows, np.int32)
+    widest, ovf = ctypes.c_int(0), ctypes.c_int(0)
+    _load().or_copy_neighbor_matrix(numneigh.ctypes.data, neighbors.ctypes.data,
+                                    int(lst["stride"]), int(num_rows), int(rows), int(max_atoms),
+                                    int(max_neighbors), matrix.ctypes.data, num.ctypes.data,
+                                    ctypes.byref(widest), ctypes.byref(ovf))
+    return matrix, num, int(widest.value), int(ovf.value)
+
+
+def matrix_edges(matrix, num_neighbors, max_atoms):
+    """The matrix slots as (row -> neighbour) edges in slot-major order, mask set on the slots a
+    row model reads (s < num_neighbors, neighbour < max_atoms); the model applies its cutoff."""
+    max_neighbors, rows = matrix.shape
+    s_idx = np.arange(max_neighbors)[:, None]
+    live = (s_idx < num_neighbors[None, :]) & (matrix < max_atoms)
+    ss, ii = np.nonzero(live)
+    senders = ii.astype(np.int32)
+    receivers = matrix[ss, ii].astype(np.int32)
+    return senders, receivers, np.ones(len(senders), np.uint8)
 
 
 def add_forces(f, model_forces, rows, scale=1.0):

@@ -43,7 +43,7 @@ def test_library_is_built_for_gfx950():
 
 def test_struct_layout_matches_header():
     # lk_contract: 12 ints then a double -> 56 bytes with the double 8-aligned
-    assert ctypes.sizeof(N.LkContract) == 56
+    assert ctypes.sizeof(N.LkContract) == 72  # 12 ints, a double, 3 ints, padding
     assert ctypes.sizeof(N.LkStepInfo) == 8 + 48 + 8
     assert ctypes.sizeof(N.LkEamTables) == 12 + 4 + 24 + 24
 

@@ -295,13 +295,15 @@ def test_list_kind_follows_pair_half_list(tmp_path, edits, newton_pair, half_lis
     assert Bundle(path).contract(newton_pair=newton_pair).half_list == half_list
 
 
-def test_matrix_layout_loads_but_is_not_run(tmp_path):
+def test_matrix_layout_contract(tmp_path):
+    """A neighbor-matrix bundle: max_neighbors is its capacity, max_owned its row count when
+    set (cpp/pair_jax_kokkos.cpp:438-441), and it always takes a full list unless it pairs
+    half with a communication schedule."""
     path = _edit(_lj_bundle(tmp_path), input_layout="neighbor-matrix", max_neighbors=16,
-                 max_edges=None)
-    b = Bundle(path)
-    with pytest.raises(N.LammpsJaxError) as info:
-        b.contract()
-    assert info.value.code == N.LK_ERR_UNSUPPORTED
+                 max_edges=None, max_owned=40)
+    c = Bundle(path).contract()
+    assert (c.input_layout, c.max_neighbors, c.max_owned, c.half_list) == (
+        N.LK_LAYOUT_NEIGHBOR_MATRIX, 16, 40, 0)
 
 
 def test_writer_rejects_incomplete_models(tmp_path):

@@ -1,0 +1,135 @@
+"""GPU parity of the neighbour-matrix layout (input_layout = neighbor-matrix) against the oracle.
+
+The pair style copies the LAMMPS list into the [max_neighbors][rows] matrix on list rebuilds
+(CopyNeighborMatrixFunctor, cpp/pair_jax_kokkos.cpp:120-155, 824-842, 1011-1012) and the row
+models read it (eam_pallas.py:181-249, 313-343): a full list runs the one-sided rows (rows
+complete, F' of ghosts from their owners), a half list the half scheme (neighbours take their
+share, ghost densities fold into their owners). Every matrix slot below the row's count is
+masked by the model's cutoff alone. The copy is compared bit for bit; energies, forces and
+virials at float64 1e-10 and float32 1e-5 relative."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from lk_testutil import rel_err
+from lammps_jax_amd import _native as N
+from lammps_jax_amd import harness, systems
+from lammps_jax_amd.pair import PairJax
+
+pytestmark = pytest.mark.gpu
+
+TOL = {8: 1e-10, 4: 1e-5}
+
+
+def _case(kind, cells, seed, precision=8, max_neighbors=None, newton_pair=True, max_owned=0):
+    wl = systems.make_workload("eam_alloy_8k", cells=cells, seed=seed)
+    sysm = systems.System(wl.x, wl.types, wl.box, wl.cutoff + wl.skin)
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=kind)
+    accum = "half" if kind == harness.LIST_HALF else "onesided"
+    pj = PairJax(sysm, ("eam", wl.tables), precision=precision, accumulation=accum,
+                 layout="neighbor-matrix", max_neighbors=max_neighbors, newton_pair=newton_pair,
+                 max_owned=max_owned)
+    print(f"matrix case kind={kind} precision={precision} nall={sysm.nall} "
+          f"max_neighbors={pj.contract.max_neighbors}", flush=True)
+    return wl, sysm, lst, pj
+
+
+def _oracle(wl, sysm, pj, matrix, num, mode, precision):
+    pos, sp = O.pack_atoms(sysm.x, sysm.type, sysm.nall, pj.max_atoms, precision)
+    s, r, m = O.matrix_edges(matrix, num, pj.max_atoms)
+    return O.eam_compute(wl.tables, pos, sp, nlocal=sysm.nlocal, nghost=sysm.nghost, senders=s,
+                         receivers=r, mask=m, mode=mode, precision=precision,
+                         ghost_owner=sysm.ghost_owner)
+
+
+def test_matrix_copy_is_the_reference_copy(gpu):
+    wl, sysm, lst, pj = _case(harness.LIST_FULL, (3, 3, 3), seed=21)
+    info = pj.pack()
+    matrix, num = pj.neighbor_matrix()
+    rows = pj.max_atoms
+    ref_m, ref_num, widest, ovf = O.copy_neighbor_matrix(lst, rows=rows, max_atoms=pj.max_atoms,
+                                                         max_neighbors=pj.contract.max_neighbors)
+    np.testing.assert_array_equal(matrix, ref_m)
+    np.testing.assert_array_equal(num, ref_num)
+    assert (info.edge_count, info.edge_overflow) == (widest, ovf) == (int(lst["numneigh"][:sysm.nlocal].max()), 0)
+
+
+def test_matrix_overflow_truncates_and_reports(gpu):
+    wl, sysm, lst, pj = _case(harness.LIST_FULL, (3, 3, 3), seed=22, max_neighbors=40)
+    info = pj.pack()
+    matrix, num = pj.neighbor_matrix()
+    ref_m, ref_num, widest, ovf = O.copy_neighbor_matrix(lst, rows=pj.max_atoms,
+                                                         max_atoms=pj.max_atoms, max_neighbors=40)
+    np.testing.assert_array_equal(matrix, ref_m)
+    np.testing.assert_array_equal(num, ref_num)
+    assert ovf == 1 and info.edge_overflow == 1 and info.edge_count == widest
+    with pytest.raises(N.LammpsJaxError, match="neighbor capacity exceeded"):
+        pj.compute()
+
+
+@pytest.mark.parametrize("precision", [8, 4])
+def test_matrix_full_list_rows_match_oracle(gpu, precision):
+    wl, sysm, lst, pj = _case(harness.LIST_FULL, (4, 4, 4), seed=23, precision=precision)
+    info = pj.compute()
+    f = pj.forces()
+    matrix, num = pj.neighbor_matrix()
+    ref = _oracle(wl, sysm, pj, matrix, num, O.ONESIDED, precision)
+    nl, tol = sysm.nlocal, TOL[precision]
+    assert info.energy == pytest.approx(ref["energy"], rel=tol)
+    assert rel_err(f[:nl], ref["forces"][:nl]) < tol
+    assert np.all(f[nl:sysm.nall] == 0.0)
+    assert rel_err(info.virial, ref["virial"]) < tol
+    rho, _ = pj.model_rows()
+    assert rel_err(rho[:nl], ref["rho"][:nl]) < tol
+
+
+@pytest.mark.parametrize("precision", [8, 4])
+def test_matrix_half_list_rows_match_oracle(gpu, precision):
+    wl, sysm, lst, pj = _case(harness.LIST_HALF, (4, 4, 4), seed=24, precision=precision)
+    info = pj.compute()
+    f = pj.forces()
+    matrix, num = pj.neighbor_matrix()
+    ref = _oracle(wl, sysm, pj, matrix, num, O.HALF, precision)
+    nall, tol = sysm.nall, TOL[precision]
+    assert info.energy == pytest.approx(ref["energy"], rel=tol)
+    assert rel_err(f[:nall], ref["forces"][:nall]) < tol
+    assert rel_err(info.virial, O.virial_fdotr(ref["forces"][:nall], sysm.x, nall)) < tol
+
+
+def test_matrix_owned_rows_and_newton_off(gpu):
+    """max_owned rows (owned atoms only) with newton off: the forces of the owned rows, no pair
+    virial; a step with more owned atoms than max_owned is refused."""
+    wl, sysm, lst, pj = _case(harness.LIST_FULL, (4, 4, 4), seed=25, newton_pair=False,
+                              max_owned=4 * 4 * 4 * 4)
+    assert pj.contract.max_owned == sysm.nlocal
+    info = pj.compute()
+    f = pj.forces()
+    matrix, num = pj.neighbor_matrix()
+    assert matrix.shape[1] == sysm.nlocal
+    ref = _oracle(wl, sysm, pj, matrix, num, O.ONESIDED, 8)
+    nl = sysm.nlocal
+    assert info.energy == pytest.approx(ref["energy"], rel=1e-10)
+    assert rel_err(f[:nl], ref["forces"][:nl]) < 1e-10
+
+
+def test_matrix_copied_only_on_list_rebuilds(gpu):
+    """lk_pack_compute copies the list when its epoch changes; within an epoch the matrix (and
+    so the step) does not see changes to the engine's list."""
+    import torch
+
+    wl, sysm, lst, pj = _case(harness.LIST_FULL, (3, 3, 3), seed=26)
+    first = pj.compute()
+    f0 = pj.forces().copy()
+    pj.numneigh.zero_()  # the engine's list changes without a rebuild signal
+    torch.cuda.synchronize()
+    same = pj.compute()
+    assert same.energy == first.energy
+    np.testing.assert_array_equal(pj.forces(), f0)
+    pj.list_epoch += 1
+    pj.h.set_list_epoch(pj.list_epoch)
+    empty = pj.compute()
+    assert empty.edge_count == 0
+    assert empty.energy != first.energy
