@@ -30,12 +30,13 @@ HBM_PEAK_GBS = 8000.0
 
 
 def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: int,
-                words: int, two_sided: bool = False) -> float:
+                words: int, two_sided: bool = False, matrix: bool = False) -> float:
     """Algorithmic (compulsory, unique) HBM bytes of one launch of a stage.
 
     R list rows, A = owned + ghost atoms, N owned, E packed edges, entries = list entries read,
     S bytes per model scalar, words = validity words per row; two_sided: the plain / half
-    schemes (incidence lists, 2E incident entries)."""
+    schemes (incidence lists, 2E incident entries); matrix: the neighbour-matrix row models
+    (E = slots inside the cutoff; only the internal receivers are written)."""
     rec = 4 * S  # atom record: x, y, z, species
     if two_sided:
         if stage == "inc_count":
@@ -72,7 +73,7 @@ def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: 
         # list + row data, gathered atom records, validity bits and row counts, F' (owned +
         # ghost images) and rho out, the packed arrays out
         return (8 * R + 4 * entries + (rec + 4) * A + 4 * R * words + 8 * R + S * A + S * N
-                + 9 * E)
+                + (4 if matrix else 9) * E)
     if stage == "step_count":
         # list + row data, x and type of every atom once, atom records and species out,
         # validity bits, row counts, F' (owned + ghost images) and rho out
@@ -145,6 +146,23 @@ def pmc_traffic(kernel: str, workload: str):
     return None
 
 
+def slots_inside_cutoff(sysm, lst, cutoff: float) -> int:
+    """List slots of the list rows whose pair lies inside the cutoff (float64): the slots a
+    neighbour-matrix row model keeps, for the byte accounting of that layout."""
+    import numpy as np
+
+    rows = lst["ilist"][: lst["inum"]]
+    nn = lst["numneigh"][rows]
+    x = np.asarray(sysm.x)
+    kept = 0
+    for jj in range(int(nn.max()) if len(nn) else 0):
+        live = rows[nn > jj]
+        j = lst["neighbors"][jj * lst["stride"] + live] & 0x3FFFFFFF
+        d = x[j] - x[live]
+        kept += int(np.count_nonzero((d * d).sum(1) < cutoff * cutoff))
+    return kept
+
+
 def lean_step(pj, eflag: bool = True, vflag: bool = True):
     """One engine step as a C++ caller makes it: lk_pack_compute then lk_step_result, with the
     argument list bound once (ctypes calls, no torch dispatch). The forces add into f without a
@@ -183,6 +201,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="eam_alloy_131k")
+    ap.add_argument("--layout", default="sparse-edge", choices=("sparse-edge", "neighbor-matrix"),
+                    help="bundle input layout; neighbor-matrix times the steps between list "
+                         "rebuilds (the matrix is copied on rebuilds only)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--split-steps", type=int, default=20,
@@ -219,7 +240,7 @@ def main() -> int:
     max_atoms = ((nall * 21 // 20) + 1023) // 1024 * 1024  # 5% headroom, like an exported bundle
     pj = PairJax(sysm, model, precision=wl.precision, accumulation=wl.accumulation,
                  n_hops=wl.n_hops, max_atoms=max_atoms, edges_per_atom=wl.edges_per_atom,
-                 device="cuda:0")
+                 device="cuda:0", layout=args.layout)
     setup_s = time.perf_counter() - t_setup
     print(f"[bench] {wl.name}: N={sysm.nlocal} ghosts={sysm.nghost} list entries={lst['entries']} "
           f"max_atoms={max_atoms} max_edges={pj.max_edges} setup {setup_s:.1f}s", file=sys.stderr,
@@ -283,7 +304,11 @@ def main() -> int:
     stage_us = {k: 1e3 * tot / cnt for k, (tot, cnt) in stages.items()}
     device_us = sum(stage_us.values())
     two = wl.accumulation != "onesided"
-    sb_kw = dict(R=R, A=A, N=N, E=E, entries=lst["entries"], S=S, words=words, two_sided=two)
+    matrix = args.layout == "neighbor-matrix"
+    if matrix:  # the count reports the widest row; the rows keep the slots inside the cutoff
+        E = slots_inside_cutoff(sysm, lst, wl.cutoff)
+    sb_kw = dict(R=R, A=A, N=N, E=E, entries=lst["entries"], S=S, words=words, two_sided=two,
+                 matrix=matrix)
     kernel_stages = {k: v for k, v in stage_us.items() if stage_bytes(k, **sb_kw) > 0}
     dom = max(kernel_stages, key=kernel_stages.get)
     dom_bytes = stage_bytes(dom, **sb_kw)
@@ -293,7 +318,8 @@ def main() -> int:
 
     max_edges = pj.max_edges
     nve = None
-    if args.nve > 0 and wl.model == "eam" and wl.accumulation == "onesided":
+    if (args.nve > 0 and wl.model == "eam" and wl.accumulation == "onesided"
+            and args.layout == "sparse-edge"):
         from lammps_jax_amd.md import Nve
 
         del pj
@@ -328,6 +354,7 @@ def main() -> int:
             "edges": E,
             "edge_capacity_per_atom": wl.edges_per_atom,
             "accumulation": wl.accumulation,
+            "layout": args.layout,
             "step": "pack_atoms + pack_edges + model E/F/virial + f add + host readback "
                     "(lk_pack_compute + lk_step_result; f cleared by the engine, not timed)",
         },
@@ -338,7 +365,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": pmc_traffic(dom, wl.name),
+            "traffic": pmc_traffic(dom, wl.name if not matrix else f"{wl.name}_matrix"),
         },
         "cpu_baseline": cpu,
         "nve": nve,

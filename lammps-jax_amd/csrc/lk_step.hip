@@ -113,8 +113,11 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
         double xj0, xj1, xj2;
         int zj = 0;
         if constexpr (sizeof(S) == 8) {
-          // float64 records hold the engine's x exactly: one 32-byte gather brings x and species
+          // float64 records hold the engine's x exactly: one 32-byte gather (two 16-byte loads)
+          // brings x and species. The empty asm takes the species where it arrives, so the
+          // compiler cannot defer it into an 8-byte gather of its own behind the filter.
           const Atom4<double> rj = reinterpret_cast<const Atom4<double> *>(a.atoms)[j];
+          asm volatile("" ::"v"(rj.w));
           xj0 = rj.x;
           xj1 = rj.y;
           xj2 = rj.z;
