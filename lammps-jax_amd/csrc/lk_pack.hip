@@ -44,54 +44,6 @@ __global__ __launch_bounds__(256) void k_pack_atoms(const double *__restrict__ x
   species[i] = sp;
 }
 
-// The same copy four atoms per thread: 96 bytes of x and 16 bytes of type in 16-byte loads, the
-// four records and species in 16-byte stores (x and type 16-byte aligned; the launcher checks).
-template <typename S>
-__global__ __launch_bounds__(256) void k_pack_atoms4(const double *__restrict__ x,
-                                                      const int *__restrict__ type, int span,
-                                                      Atom4<S> *__restrict__ atoms,
-                                                      int *__restrict__ species,
-                                                      int *__restrict__ clear)
-{
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (clear && t < 2) clear[t] = 0;
-  const int i0 = 4 * t;
-  if (i0 >= span) return;
-  if (i0 + 4 <= span) {
-    const double2 *xv = reinterpret_cast<const double2 *>(x + 3L * i0);
-    double c[12];
-#pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      const double2 v = xv[k];
-      c[2 * k] = v.x;
-      c[2 * k + 1] = v.y;
-    }
-    const int4 ty = *reinterpret_cast<const int4 *>(type + i0);
-    const int sp[4] = {ty.x - 1, ty.y - 1, ty.z - 1, ty.w - 1};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      Atom4<S> a;
-      a.x = static_cast<S>(c[3 * q + 0]);
-      a.y = static_cast<S>(c[3 * q + 1]);
-      a.z = static_cast<S>(c[3 * q + 2]);
-      a.w = static_cast<S>(sp[q]);
-      atoms[i0 + q] = a;
-    }
-    *reinterpret_cast<int4 *>(species + i0) = make_int4(sp[0], sp[1], sp[2], sp[3]);
-    return;
-  }
-  for (int i = i0; i < span; ++i) {
-    const int sp = type[i] - 1;
-    Atom4<S> a;
-    a.x = static_cast<S>(x[3L * i + 0]);
-    a.y = static_cast<S>(x[3L * i + 1]);
-    a.z = static_cast<S>(x[3L * i + 2]);
-    a.w = static_cast<S>(sp);
-    atoms[i] = a;
-    species[i] = sp;
-  }
-}
-
 // Pass 1: one lane per list row, W waves per 64-row tile. Wave w takes the 32-slot words
 // w, w + W, ... of every row: it reads those list slots (coalesced across the rows), applies the
 // filter and stores the validity word (LayoutLeft words). The per-wave kept counts meet in LDS.
@@ -360,21 +312,8 @@ hipError_t launch_pack_atoms(Handle &h, hipStream_t s, const double *x, const in
 {
   const int span = nall < h.contract.max_atoms ? nall : h.contract.max_atoms;
   if (span <= 0 && !clear) return hipSuccess;
-  StageTimer timer(h, s, "pack_atoms");
-  const bool aligned = (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
-                       (reinterpret_cast<uintptr_t>(type) % 16 == 0);
-  if (aligned) {
-    const int threads = (span + 3) / 4;
-    const int blocks4 = threads > 0 ? (threads + 255) / 256 : 1;
-    if (h.contract.precision == LK_FLOAT64)
-      hipLaunchKernelGGL(k_pack_atoms4<double>, dim3(blocks4), dim3(256), 0, s, x, type, span,
-                         static_cast<Atom4<double> *>(h.d_atoms), h.d_species, clear);
-    else
-      hipLaunchKernelGGL(k_pack_atoms4<float>, dim3(blocks4), dim3(256), 0, s, x, type, span,
-                         static_cast<Atom4<float> *>(h.d_atoms), h.d_species, clear);
-    return hipGetLastError();
-  }
   const int blocks = span > 0 ? (span + 255) / 256 : 1;
+  StageTimer timer(h, s, "pack_atoms");
   if (h.contract.precision == LK_FLOAT64)
     hipLaunchKernelGGL(k_pack_atoms<double>, dim3(blocks), dim3(256), 0, s, x, type, span,
                        static_cast<Atom4<double> *>(h.d_atoms), h.d_species, clear);
