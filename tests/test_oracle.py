@@ -524,3 +524,42 @@ def test_lj_edge_force_is_the_pair_energy_gradient():
     far = np.array([[0.0, 0, 0], [3.0, 0, 0]])
     assert np.all(O.lj_edge_forces(LJ, far, senders=s, receivers=r, mask=m) == 0.0)
     assert np.all(O.lj_edge_forces(LJ, x, senders=s, receivers=r, mask=np.zeros(1, np.uint8)) == 0.0)
+
+
+# --------------------------------------------------------------------------------------------
+# neighbour-matrix copy (cpp/pair_jax_kokkos.cpp:120-155)
+# --------------------------------------------------------------------------------------------
+
+def test_copy_neighbor_matrix_known_answer():
+    """Three rows of a LayoutLeft list (stride 4): row 1 carries special-bond bits, row 2 is
+    longer than max_neighbors = 2 and is truncated; rows past the list (row 3) are empty."""
+    stride, max_atoms = 4, 10
+    nb = np.zeros(3 * stride, np.int32)
+    entries = {0: [5], 1: [2 | (1 << 30), 7], 2: [0, 1, 3]}
+    for i, js in entries.items():
+        for s, j in enumerate(js):
+            nb[s * stride + i] = j
+    lst = dict(numneigh=np.array([1, 2, 3, 0], np.int32), neighbors=nb, stride=stride, inum=3,
+               gnum=0)
+    m, num, widest, ovf = O.copy_neighbor_matrix(lst, rows=4, max_atoms=max_atoms, max_neighbors=2)
+    np.testing.assert_array_equal(m, [[5, 2, 0, 10], [10, 7, 1, 10]])
+    np.testing.assert_array_equal(num, [1, 2, 2, 0])
+    assert (widest, ovf) == (3, 1)
+    s, r, mask = O.matrix_edges(m, num, max_atoms)
+    assert sorted(zip(s.tolist(), r.tolist())) == [(0, 5), (1, 2), (1, 7), (2, 0), (2, 1)]
+
+
+def test_copy_neighbor_matrix_holds_the_list():
+    """On a real periodic list with room for every row, the matrix holds exactly the list's
+    (row, neighbour) pairs and the widest row is numneigh's maximum."""
+    wl = systems.make_workload("eam_alloy_131k", cells=(3, 3, 3), seed=31)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin)
+    rows = sysm.nall
+    m, num, widest, ovf = O.copy_neighbor_matrix(lst, rows=rows, max_atoms=rows,
+                                                 max_neighbors=lst["maxneighs"])
+    assert ovf == 0 and widest == int(lst["numneigh"][: sysm.nlocal].max())
+    s, r, _ = O.matrix_edges(m, num, rows)
+    got = set(zip(s.tolist(), r.tolist()))
+    want = set(map(tuple, list_pairs(lst, sysm.x, 1.0e9, lst["inum"]).tolist()))  # every entry
+    assert got == want
