@@ -55,6 +55,10 @@ def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: 
             return 8 * E + rec * A + S * A + 72 * A
         if stage == "lj_rows":
             return 8 * E + rec * A + 72 * A
+        if stage == "step_pack":
+            # the pack alone: list + row data, positions (float64 records, or x for float32),
+            # validity bits and row counts, the packed arrays out
+            return 8 * R + 4 * entries + (rec if S == 8 else 24) * A + 4 * R * words + 8 * R + 9 * E
     if stage == "pack_atoms":
         return A * (24 + 4) + A * (rec + 4)
     if stage == "pack_count":

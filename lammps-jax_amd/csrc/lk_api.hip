@@ -661,6 +661,63 @@ int lk_pack_compute(lk_handle *w, void *stream, const double *x, const int *type
     if (rc == LK_OK) rc = lk_compute(w, stream, nlocal, nghost, flags, scale, f);
     return rc;
   }
+  if (h.accum != LK_ACCUM_ONESIDED && !h.contract.edge_force && !h.contract.pair_sum) {
+    // Two-sided schemes whose incidence lists come from the list slots (no half filter, no
+    // unique boundary): the pack runs as one launch after the atom records (tile slots claimed
+    // with one atomic add, as the one-sided step does) instead of count + scan + write. The
+    // sweeps read the list and the validity bits, not the packed order, so results match the
+    // three entry points bit for bit.
+    const lk_contract &c = h.contract;
+    const bool multi_hop = c.n_hops > 1;
+    const bool half_edges = c.pairing != LK_PAIRING_FULL;
+    const bool full_list = !c.half_list;
+    long rows = static_cast<long>(inum) + (multi_hop ? gnum : 0);
+    if (rows > c.max_atoms) rows = c.max_atoms;
+    const int mnb = maxneighs > 1 ? maxneighs : 1;
+    const long bit_words = static_cast<long>((mnb + 31) / 32) * c.max_atoms;
+    if (!(half_edges && full_list) && bit_words < (1L << 27) && inum >= 0 && gnum >= 0 &&
+        nlocal >= 0 && nghost >= 0 && nall >= 0 && f) {
+      if (static_cast<long>(nlocal) + nghost > c.max_atoms)
+        return fail(h, LK_ERR_CAPACITY, "LAMMPS-JAX atom capacity exceeded");
+      if (rows * mnb > static_cast<long>(INT_MAX))
+        return fail(h, LK_ERR_CAPACITY,
+                    "LAMMPS-JAX neighbor pack index overflows int; reduce the bundle max_atoms or "
+                    "the neigh_modify one setting");
+      if ((rows > 0 || nall > 0) && (!x || !type || !ilist || !numneigh || !neighbors))
+        return fail(h, LK_ERR_ARGUMENT, "invalid atom or neighbor list arrays");
+      if (rows > 0 && nb_stride < 1) return fail(h, LK_ERR_ARGUMENT, "invalid neighbor stride");
+      if (h.accum == LK_ACCUM_HALF && h.model != 1)
+        return fail(h, LK_ERR_UNSUPPORTED,
+                    "half accumulation is defined for EAM; LJ on half lists uses plain accumulation");
+      if (h.accum == LK_ACCUM_HALF && nghost > 0 &&
+          (h.ghost_n != nghost || h.ghost_nlocal != nlocal))
+        return fail(h, LK_ERR_STATE,
+                    "half accumulation needs the ghost map of this step (lk_set_ghost_map) for the "
+                    "density fold");
+      if (int rc = ensure_bits(h, mnb)) return rc;
+      h.x_last = x;
+      h.type_last = type;
+      h.list_ilist = ilist;
+      h.list_numneigh = numneigh;
+      h.list_neighbors = neighbors;
+      h.list_stride = nb_stride;
+      h.list_rows = static_cast<int>(rows);
+      h.list_maxneighs = mnb;
+      h.list_half_filter = 0;
+      h.list_unique = 0;
+      h.list_duplicate = 0;
+      if (int rc = ensure_incidence(h, 2L * rows * mnb)) return rc;
+      hipStream_t s = as_stream(stream);
+      lk::FusedPack fp;
+      hipError_t e = lk::launch_pack_fused(h, s, x, type, nall, ilist, numneigh, neighbors,
+                                           nb_stride, static_cast<int>(rows), mnb, nlocal, &fp);
+      if (e == hipSuccess)
+        e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, x, true, fp);
+      if (e != hipSuccess) return hip_fail(h, e, "fused two-sided step");
+      h.result_mirrored = true;
+      return LK_OK;
+    }
+  }
   if (h.accum != LK_ACCUM_ONESIDED || h.contract.pair_sum) {
     // schemes without a fused form run the three entry points in order
     int rc = lk_pack_atoms(w, stream, x, type, nall);

@@ -193,8 +193,16 @@ hipError_t launch_edge_force(Handle &h, hipStream_t s, int nlocal, int nghost, i
                              double scale, double *f, const double *x, bool from_list);
 
 hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
-                            double scale, double *f, const double *x, bool from_list);
+                            double scale, double *f, const double *x, bool from_list,
+                            const FusedPack &pack = FusedPack{});
 
+// The one-sided step's first two launches alone (atom records, then the pack without a model):
+// the pack of the two-sided schemes whose incidence lists come from the list slots. `out`
+// receives what the sweeps need to finish it (tail reset, counts).
+hipError_t launch_pack_fused(Handle &h, hipStream_t s, const double *x, const int *type, int nall,
+                             const int *ilist, const int *numneigh, const int *neighbors,
+                             long stride, int num_rows, int maxneighs, int nlocal,
+                             FusedPack *out);
 hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,
                                 int nall, const int *ilist, const int *numneigh,
                                 const int *neighbors, long stride, int num_rows, int maxneighs,

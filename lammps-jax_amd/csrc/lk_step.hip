@@ -61,6 +61,17 @@ constexpr int kStepMaxWords = 8;   // validity words kept in LDS for the write (
 // MATRIX: the list is the neighbour matrix of a matrix bundle. No packer filter applies: an
 // entry counts when the model's mask does (r^2 < cutoff^2 at the contract precision,
 // eam_pallas.py list_pair), and only the internal receivers are written for the force sweep.
+// Grid of K1. With the EAM table window to fill, blocks stay resident and walk several groups
+// (two per CU), so the fill is paid once per block. Without it there is nothing to amortise: one
+// group per block lets the dispatcher hand out groups as CUs free up, instead of a static share
+// per block whose last round runs on a fraction of the blocks.
+template <bool EAM>
+static int step_pack_grid(int ngroups, int num_cus)
+{
+  if constexpr (EAM) return persistent_grid(ngroups, 2, num_cus);
+  return ((ngroups + kXcds - 1) / kXcds) * kXcds;
+}
+
 template <typename S, bool EAM, bool MATRIX>
 __global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves_per_eu(8)))
 void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
@@ -320,7 +331,7 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   }
   if (ntiles > 0) {
     StageTimer timer(h, s, "step_pack");
-    const int grid = persistent_grid(ngroups, 2, h.num_cus);
+    const int grid = step_pack_grid<EAM>(ngroups, h.num_cus);
     hipLaunchKernelGGL((k_step_pack<S, EAM, MATRIX>), dim3(grid),
                        dim3(kStepW * kStepTPB * kWave), 0, s, p, a, ngroups);
   }
@@ -340,6 +351,73 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
     return launch_eam_force(h, s, a, flags);
   }
   return launch_lj_onesided(h, s, nlocal, nghost, scale, f, flags, fp);
+}
+
+template <typename S>
+static hipError_t pack_fused(Handle &h, hipStream_t s, const double *x, const int *type, int nall,
+                             const int *ilist, const int *numneigh, const int *neighbors,
+                             long stride, int num_rows, int maxneighs, int nlocal, FusedPack *out)
+{
+  h.packed_rows = num_rows;
+  EamArgs<S> a{};
+  a.atoms = static_cast<const Atom4<S> *>(h.d_atoms);
+  a.partials = h.d_partials;
+  a.nlocal = nlocal;
+  StepPack p{};
+  p.x = x;
+  p.type = type;
+  p.ilist = ilist;
+  p.numneigh = numneigh;
+  p.neighbors = neighbors;
+  p.stride = stride;
+  p.num_rows = num_rows;
+  p.maxneighs = maxneighs;
+  p.max_atoms = h.contract.max_atoms;
+  p.max_edges = h.contract.max_edges;
+  p.cutsq = h.contract.cutoff * h.contract.cutoff;
+  p.pitch = h.contract.max_atoms;
+  p.bits = h.d_bits;
+  p.row_count = h.d_row_count;
+  p.row_atom = h.d_row_atom;
+  p.tile_base = h.d_tile_off;
+  p.state = h.d_pack_state;
+  p.senders = h.d_senders;
+  p.receivers = h.d_receivers;
+  p.mask = h.d_mask;
+  p.ghost_off = nullptr;  // no model: nothing to forward
+  p.ghost_list = nullptr;
+  const int ntiles = (num_rows + kWave - 1) / kWave;
+  const int ngroups = ntiles > 0 ? (ntiles + kStepTPB - 1) / kStepTPB : 1;
+  if (hipError_t e0 = launch_pack_atoms(h, s, x, type, nall, h.d_pack_state); e0 != hipSuccess)
+    return e0;
+  if (ntiles > 0) {
+    StageTimer timer(h, s, "step_pack");
+    const int grid = step_pack_grid<false>(ngroups, h.num_cus);
+    hipLaunchKernelGGL((k_step_pack<S, false, false>), dim3(grid),
+                       dim3(kStepW * kStepTPB * kWave), 0, s, p, a, ngroups);
+  }
+  ++h.pack_serial;
+  out->counter = h.d_pack_state;
+  out->senders = h.d_senders;
+  out->receivers = h.d_receivers;
+  out->mask = h.d_mask;
+  out->max_edges = h.contract.max_edges;
+  out->pad = h.contract.max_atoms;
+  out->reset_end = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
+                                                              : h.contract.max_edges;
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_fused(Handle &h, hipStream_t s, const double *x, const int *type, int nall,
+                             const int *ilist, const int *numneigh, const int *neighbors,
+                             long stride, int num_rows, int maxneighs, int nlocal,
+                             FusedPack *out)
+{
+  if (h.contract.precision == LK_FLOAT64)
+    return pack_fused<double>(h, s, x, type, nall, ilist, numneigh, neighbors, stride, num_rows,
+                              maxneighs, nlocal, out);
+  return pack_fused<float>(h, s, x, type, nall, ilist, numneigh, neighbors, stride, num_rows,
+                           maxneighs, nlocal, out);
 }
 
 hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,

@@ -329,6 +329,8 @@ struct TwoSided {
   int nblk;             // 64-atom tiles over nall
   const uint32_t *inc_bit;  // list-built entries: address of the slot's validity bit
   const uint32_t *bits;     // the pack's validity bits of this step
+  const int *ghost_flag;    // 1 when a packed edge starts on a ghost row (the pack's flag)
+  FusedPack pack;           // a fused pack of this step: tail reset and counts (else unused)
 };
 
 // The pack kept this entry's list slot this step (lists built from packed edges: always).
@@ -340,10 +342,10 @@ __device__ __forceinline__ bool slot_kept(const TwoSided &t, int q)
 }
 
 // Rows whose energy counts (export.py:183-194).
-__device__ __forceinline__ int energy_rows(const TwoSided &t, const StepResult *r, bool half)
+__device__ __forceinline__ int energy_rows(const TwoSided &t, bool half)
 {
   if (half || t.owned_rows_only) return t.nlocal;
-  return r->ghost_sender ? t.nall : t.nlocal;
+  return *t.ghost_flag ? t.nall : t.nlocal;
 }
 
 template <typename S>
@@ -363,6 +365,7 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
                                                                S *__restrict__ epair)
 {
   __shared__ LdsEntry<S> lds[kIncLds];
+  fused_tail_reset(t.pack);
   const Window<S> win = fill_window<S>(lds, kIncLds, m, m.n_rtab);
   const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
   for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
@@ -412,7 +415,7 @@ __global__ __launch_bounds__(kWave) void k_eam_embed_inc(EamArgs<S> m, TwoSided 
 {
   const int tile = blockIdx.x;
   const int a = tile * kWave + threadIdx.x;
-  const int erows = energy_rows(t, m.result, HALF);
+  const int erows = energy_rows(t, HALF);
   double e_row = 0.0;
   if (HALF) {
     if (a < t.nlocal) {
@@ -503,7 +506,7 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
   __shared__ double vt[6][kRowAtoms];
   const Window<S> win = fill_window<S>(lds, kIncLds, m, m.n_rtab);
   const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
-  const int erows = energy_rows(t, m.result, HALF);
+  const int erows = energy_rows(t, HALF);
   for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
     const int a = blk * kRowAtoms + g;
     S fx = S(0), fy = S(0), fz = S(0);
@@ -563,7 +566,7 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
     __syncthreads();
   }
   finalize_last_block(m.partials, t.nblk, m.scale, 1.0, m.flags, m.result, m.done,
-                      reinterpret_cast<double *>(lds), FusedPack{}, m.mirror);
+                      reinterpret_cast<double *>(lds), t.pack, m.mirror);
 }
 
 template <typename S>
@@ -587,8 +590,9 @@ __global__ __launch_bounds__(kRowBlock) void k_lj_inc(LjModel<S> m, TwoSided t)
   __shared__ double vt[6][kRowAtoms];
   __shared__ double et[kRowAtoms];
   __shared__ double scratch[7 * kRowBlock];
+  fused_tail_reset(t.pack);
   const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
-  const int erows = energy_rows(t, m.result, false);
+  const int erows = energy_rows(t, false);
   const S tiny = static_cast<S>(1.0e-12);
   for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
     const int a = blk * kRowAtoms + g;
@@ -635,7 +639,7 @@ __global__ __launch_bounds__(kRowBlock) void k_lj_inc(LjModel<S> m, TwoSided t)
     __syncthreads();
   }
   finalize_last_block(m.partials, t.nblk, m.scale, 1.0, m.flags, m.result, m.done, scratch,
-                      FusedPack{}, m.mirror);
+                      t.pack, m.mirror);
 }
 
 static int grid_for(const Handle &h, long work, int per_block, int blocks_per_cu)
@@ -745,15 +749,28 @@ static TwoSided two_sided_args(Handle &h, int nlocal, int nghost, const double *
   t.nblk = (t.nall + kRowAtoms - 1) / kRowAtoms;
   t.inc_bit = nullptr;
   t.bits = h.d_bits;
+  t.ghost_flag = &h.d_result->ghost_sender;
+  t.pack = FusedPack{};
   return t;
+}
+
+// A fused pack (`pack.counter` set) leaves the demand count and the ghost-sender flag in its
+// state words and the previous step's tail to reset; the sweeps take both from there.
+static void use_pack(TwoSided &t, const FusedPack &pack)
+{
+  if (!pack.counter) return;
+  t.pack = pack;
+  t.ghost_flag = pack.counter + 1;
 }
 
 template <typename S, bool HALF>
 static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
-                                double scale, double *f, const double *x, bool from_list)
+                                double scale, double *f, const double *x, bool from_list,
+                                const FusedPack &pack)
 {
   EamArgs<S> m = eam_args<S>(h, nlocal, scale, f);
   TwoSided t = two_sided_args(h, nlocal, nghost, x);
+  use_pack(t, pack);
   if (from_list && h.list_bits_filter) t.inc_bit = h.d_inc_bit;
   m.flags = flags;
   S *rho_part = static_cast<S *>(h.d_rho_part);
@@ -781,7 +798,8 @@ static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost
 
 template <typename S>
 static hipError_t lj_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
-                               double scale, double *f, const double *x, bool from_list)
+                               double scale, double *f, const double *x, bool from_list,
+                               const FusedPack &pack)
 {
   LjModel<S> m;
   m.atoms = static_cast<const Atom4<S> *>(h.d_atoms);
@@ -797,6 +815,7 @@ static hipError_t lj_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost,
   m.flags = flags;
   m.mirror = h.d_host_result;
   TwoSided t = two_sided_args(h, nlocal, nghost, x);
+  use_pack(t, pack);
   if (from_list && h.list_bits_filter) t.inc_bit = h.d_inc_bit;
   const int grid = grid_for(h, t.nblk > 0 ? t.nblk : 1, 1, 2);
   StageTimer timer(h, s, "lj_rows");
@@ -1134,7 +1153,8 @@ hipError_t launch_edge_force(Handle &h, hipStream_t s, int nlocal, int nghost, i
 }
 
 hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
-                            double scale, double *f, const double *x, bool from_list)
+                            double scale, double *f, const double *x, bool from_list,
+                            const FusedPack &pack)
 {
   hipError_t e = hipSuccess;
   if (from_list) {
@@ -1160,13 +1180,13 @@ hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, in
   const bool half = h.accum == LK_ACCUM_HALF;
   if (h.model == 1) {
     if (f64)
-      return half ? eam_two_sided<double, true>(h, s, nlocal, nghost, flags, scale, f, x, from_list)
-                  : eam_two_sided<double, false>(h, s, nlocal, nghost, flags, scale, f, x, from_list);
-    return half ? eam_two_sided<float, true>(h, s, nlocal, nghost, flags, scale, f, x, from_list)
-                : eam_two_sided<float, false>(h, s, nlocal, nghost, flags, scale, f, x, from_list);
+      return half ? eam_two_sided<double, true>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack)
+                  : eam_two_sided<double, false>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack);
+    return half ? eam_two_sided<float, true>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack)
+                : eam_two_sided<float, false>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack);
   }
-  if (f64) return lj_two_sided<double>(h, s, nlocal, nghost, flags, scale, f, x, from_list);
-  return lj_two_sided<float>(h, s, nlocal, nghost, flags, scale, f, x, from_list);
+  if (f64) return lj_two_sided<double>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack);
+  return lj_two_sided<float>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack);
 }
 
 }  // namespace lk

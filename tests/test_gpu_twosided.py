@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lk_testutil import fold_ghosts, rel_err
+from lk_testutil import canonical, fold_ghosts, rel_err
 from lammps_jax_amd import harness, systems
 from lammps_jax_amd.pair import PairJax
 
@@ -179,3 +179,56 @@ def test_half_unique_boundary_bundle_on_full_list(gpu):
                         receivers=r, mask=m, mode=O.HALF, ghost_owner=sysm.ghost_owner,
                         owned_rows_only=True)
     _check(pj, sysm, ref, 8)
+
+
+@pytest.mark.parametrize("name,kind,accum,precision", [
+    ("eam_alloy_8k", harness.LIST_HALF, "half", 4),
+    ("lj_fcc_1k", harness.LIST_FULL, "plain", 8),
+    ("lj_ghost_262k", harness.LIST_FULL_GHOST, "plain", 4),
+])
+def test_fused_pack_of_two_sided_steps(gpu, name, kind, accum, precision):
+    """lk_pack_compute packs list-built two-sided steps in one launch: the same packed edges
+    (canonical order), padding past the count, results bitwise equal to the three entry points,
+    the previous step's tail reset, and the demand count on overflow."""
+    import torch
+
+    from lammps_jax_amd._native import LammpsJaxError
+
+    n_hops = 2 if kind == harness.LIST_FULL_GHOST else 1
+    wl, sysm, lst, pj = _case(name, (4, 4, 4), precision, accum, kind, n_hops=n_hops, seed=12,
+                              fused=True)
+    a, fa = pj.compute(), pj.forces().copy()
+    b, fb = pj.compute(fused=False), pj.forces().copy()
+    assert (a.edge_count, a.edge_overflow) == (b.edge_count, b.edge_overflow) == (a.edge_count, 0)
+    s2, r2, m2 = (v.copy() for v in pj.edges())
+    pj.compute()
+    s, r, m = pj.edges()
+    np.testing.assert_array_equal(canonical(s, r, m), canonical(s2, r2, m2))
+    c = a.edge_count
+    assert np.all(m[:c] == 1) and not m[c:].any()
+    assert np.all(s[c:] == pj.max_atoms) and np.all(r[c:] == pj.max_atoms)
+    np.testing.assert_array_equal(fa, fb)
+    assert a.energy == b.energy
+    np.testing.assert_array_equal(a.virial, b.virial)
+    # spread atoms (same list): fewer pairs; the first step's slots past the new count reset
+    center = sysm.x.mean(0)
+    spread = np.ascontiguousarray(center + 1.03 * (sysm.x - center))
+    pj.x = torch.from_numpy(spread).to(pj.device)
+    second = pj.compute()
+    f2 = pj.forces().copy()
+    c2 = second.edge_count
+    assert c2 < c
+    s, r, m = pj.edges()
+    assert np.all(m[:c2] == 1) and not m[c2:].any()
+    assert np.all(s[c2:] == pj.max_atoms) and np.all(r[c2:] == pj.max_atoms)
+    split = pj.compute(fused=False)
+    assert split.edge_count == c2 and split.energy == second.energy
+    np.testing.assert_array_equal(pj.forces(), f2)
+    # an edge capacity below the demand: the count reports demand and the step errors
+    small = PairJax(sysm, (pj.kind, pj.model), precision=precision, accumulation=accum,
+                    n_hops=n_hops, max_edges=1000, fused=True)
+    with pytest.raises(LammpsJaxError, match="edge capacity exceeded"):
+        small.compute()
+    info = small.compute(check_capacity=False)
+    assert info.edge_overflow == 1 and info.edge_count == c
+    assert int(small.edges()[2].sum()) == 1000
