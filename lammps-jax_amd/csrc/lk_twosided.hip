@@ -34,6 +34,7 @@ constexpr int kGroup = 16;                     // lanes per atom in the row swee
 constexpr int kRowBlock = 1024;                // threads per row-sweep block
 constexpr int kRowAtoms = kRowBlock / kGroup;  // 64 atoms per block = one partial tile
 constexpr int kIncLds = 7680;                  // 120 KB table window
+constexpr int kIncDensLds = 4096;              // 64 KB density-table window (two blocks per CU)
 
 struct IncArgs {
   const int *senders;
@@ -358,15 +359,18 @@ __device__ __forceinline__ S geometry(const Atom4<S> &xa, const Atom4<S> &xo, S 
   return dx * dx + dy * dy + dz * dz;
 }
 
-// Density and pair energy per row (eam.py:298-314).
-template <typename S, bool HALF>
+// Density per row (eam.py:298-314); PAIR: also the row's pair energy (the edge-force path, whose
+// edge sweep keeps no per-row energy). Without it the window holds the density tables only, so
+// two blocks fit on a CU; the force sweep then sums the pair energy.
+template <typename S, bool HALF, bool PAIR>
 __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, TwoSided t,
                                                                S *__restrict__ rho_part,
                                                                S *__restrict__ epair)
 {
-  __shared__ LdsEntry<S> lds[kIncLds];
+  constexpr int kLds = PAIR ? kIncLds : kIncDensLds;
+  __shared__ LdsEntry<S> lds[kLds];
   fused_tail_reset(t.pack);
-  const Window<S> win = fill_window<S>(lds, kIncLds, m, m.n_rtab);
+  const Window<S> win = fill_window<S>(lds, kLds, m, PAIR ? m.n_rtab : m.n_el);
   const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
   for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
     const int a = blk * kRowAtoms + g;
@@ -391,23 +395,24 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
         const Locator<S> L2 = locate_mul(rr, m.inv_dr, m.nr);
         const int zo = clamp_species(static_cast<int>(xo.w), m.n_el);
         rho += cvalue(rcoef(win, m, L2.node, zo), L2.t);
-        if (!in) {
+        if (PAIR && !in) {
           const S phi = cvalue(rcoef(win, m, L2.node, m.n_el + pair_row(za, zo)), L2.t) * rinv;
           ep += HALF ? phi : S(0.5) * phi;  // half: the sender carries both halves
         }
       }
     }
     rho = group_sum(rho);
-    ep = group_sum(ep);
+    if (PAIR) ep = group_sum(ep);
     if (gl == 0 && a < t.nall) {
       rho_part[a] = rho;
-      epair[a] = ep;
+      if (PAIR) epair[a] = ep;
     }
   }
 }
 
 // Embedding: F and F' per row (eam.py:319-321); half folds ghost densities into their owners
-// first and hands the owner's F' to its ghost images. Energy partial of the tile into slot 0.
+// first and hands the owner's F' to its ghost images. Energy partial of the tile into slot 0:
+// F, plus the row's pair energy when the density sweep kept it (epair not null).
 template <typename S, bool HALF>
 __global__ __launch_bounds__(kWave) void k_eam_embed_inc(EamArgs<S> m, TwoSided t,
                                                          const S *__restrict__ rho_part,
@@ -431,7 +436,7 @@ __global__ __launch_bounds__(kWave) void k_eam_embed_inc(EamArgs<S> m, TwoSided 
           m.fp[t.ghost_list[q]] = Fp;
           m.rho[t.ghost_list[q]] = S(0);
         }
-      e_row = static_cast<double>(epair[a] + F);
+      e_row = static_cast<double>(epair ? epair[a] + F : F);
     }
   } else if (a < t.nall) {
     const S rho = rho_part[a];
@@ -439,7 +444,7 @@ __global__ __launch_bounds__(kWave) void k_eam_embed_inc(EamArgs<S> m, TwoSided 
     embed(m, clamp_species(static_cast<int>(m.atoms[a].w), m.n_el), rho, F, Fp);
     m.fp[a] = Fp;
     m.rho[a] = rho;
-    if (a < erows) e_row = static_cast<double>(epair[a] + F);
+    if (a < erows) e_row = static_cast<double>(epair ? epair[a] + F : F);
   }
   const double esum = wave_sum(e_row);
   if (threadIdx.x == 0 && tile < t.nblk) m.partials[8L * tile] = esum;
@@ -482,7 +487,7 @@ __device__ __forceinline__ void add_row_force(double *f, const double *x, int a,
 template <bool VIRIAL>
 __device__ __forceinline__ void store_tile_virial(double *partials, int blk,
                                                   double (*vt)[kRowAtoms], double e_tile,
-                                                  bool write_energy)
+                                                  bool write_energy, double e_pair = 0.0)
 {
   // called by the first wave only, after a barrier
   const int lane = threadIdx.x;
@@ -493,23 +498,26 @@ __device__ __forceinline__ void store_tile_virial(double *partials, int blk,
     }
   }
   if (lane == 0) {
-    partials[8L * blk + 7] = 0.0;
+    partials[8L * blk + 7] = e_pair;
     if (write_energy) partials[8L * blk] = e_tile;
   }
 }
 
-// Force sweep (eam.py:336-409 closed form; export.py:197-204 autodiff convention).
+// Force sweep (eam.py:336-409 closed form; export.py:197-204 autodiff convention), and the pair
+// energy of the counted rows (eam.py:300-307) from the phi it evaluates anyway: on the sender,
+// both halves in the half scheme, half per directed edge in the plain one.
 template <typename S, bool HALF, bool VIRIAL>
 __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSided t)
 {
   __shared__ LdsEntry<S> lds[kIncLds];
   __shared__ double vt[6][kRowAtoms];
+  __shared__ double et[kRowAtoms];
   const Window<S> win = fill_window<S>(lds, kIncLds, m, m.n_rtab);
   const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
   const int erows = energy_rows(t, HALF);
   for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
     const int a = blk * kRowAtoms + g;
-    S fx = S(0), fy = S(0), fz = S(0);
+    S fx = S(0), fy = S(0), fz = S(0), ep = S(0);
     if (a < t.nall) {
       const Atom4<S> xa = m.atoms[a];
       const int za = clamp_species(static_cast<int>(xa.w), m.n_el);
@@ -537,6 +545,7 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
         const S rho_r_p = inside ? cslope_t(rcoef(win, m, L2.node, zr), L2.t) * m.inv_dr : S(0);
         const Coef<S> cp = rcoef(win, m, L2.node, m.n_el + pair_row(za, zo));
         const S phi = cvalue(cp, L2.t) * rinv;
+        if (!in) ep += HALF ? phi : S(0.5) * phi;
         const S z2p = inside ? cslope_t(cp, L2.t) * m.inv_dr : S(0);
         const S phip = (z2p - phi) * rinv;
         S coef;
@@ -556,13 +565,16 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
     fx = group_sum(fx);
     fy = group_sum(fy);
     fz = group_sum(fz);
-    if (gl == 0)
+    ep = group_sum(ep);
+    if (gl == 0) {
       add_row_force<VIRIAL>(m.f, t.x, a, t.nadd, t.nall, t.fdotr, m.scale,
                             static_cast<double>(fx), static_cast<double>(fy),
                             static_cast<double>(fz), vt, g);
+      et[g] = a < erows ? static_cast<double>(ep) : 0.0;
+    }
     __syncthreads();
     if (threadIdx.x < kWave && blk * kRowAtoms < t.nall)
-      store_tile_virial<VIRIAL>(m.partials, blk, vt, 0.0, false);
+      store_tile_virial<VIRIAL>(m.partials, blk, vt, 0.0, false, wave_sum(et[threadIdx.x]));
     __syncthreads();
   }
   finalize_last_block(m.partials, t.nblk, m.scale, 1.0, m.flags, m.result, m.done,
@@ -774,18 +786,17 @@ static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost
   if (from_list && h.list_bits_filter) t.inc_bit = h.d_inc_bit;
   m.flags = flags;
   S *rho_part = static_cast<S *>(h.d_rho_part);
-  S *epair = static_cast<S *>(h.d_epair);
   const int nblk = t.nblk > 0 ? t.nblk : 1;
   const int grid = grid_for(h, nblk, 1, 1);
   if (t.nblk > 0) {
     StageTimer timer(h, s, "eam_density");
-    hipLaunchKernelGGL((k_eam_density_inc<S, HALF>), dim3(grid), dim3(kRowBlock), 0, s, m, t,
-                       rho_part, epair);
+    hipLaunchKernelGGL((k_eam_density_inc<S, HALF, false>), dim3(grid_for(h, nblk, 1, 2)),
+                       dim3(kRowBlock), 0, s, m, t, rho_part, static_cast<S *>(nullptr));
   }
   if (t.nblk > 0) {
     StageTimer timer(h, s, "eam_embed");
     hipLaunchKernelGGL((k_eam_embed_inc<S, HALF>), dim3(t.nblk), dim3(kWave), 0, s, m, t,
-                       static_cast<const S *>(rho_part), static_cast<const S *>(epair));
+                       static_cast<const S *>(rho_part), static_cast<const S *>(nullptr));
   }
   // one launch even with no rows: its last block writes the step result
   StageTimer timer(h, s, "eam_force");
@@ -997,13 +1008,18 @@ __global__ __launch_bounds__(256) void k_fdotr_rows(const double *__restrict__ f
                                                     double escale, int flags, StepResult *result,
                                                     int *done, StepResult *mirror)
 {
+  constexpr int kWaves = 256 / kWave;
   __shared__ double scratch[7 * 256];
+  __shared__ double tp[kWaves][6];
   const int lane = threadIdx.x & (kWave - 1);
-  const int waves = static_cast<int>(gridDim.x) * (blockDim.x / kWave);
-  for (int t = blockIdx.x * (blockDim.x / kWave) + wave_in_block(); t < ntiles; t += waves) {
+  const int wave = wave_in_block();
+  // Each wave sums one tile; the first wave alone stores the block's tiles (finalize_last_block
+  // releases the first wave's stores only). The loop bounds are the block's, for the barriers.
+  for (int t0 = blockIdx.x * kWaves; t0 < ntiles; t0 += static_cast<int>(gridDim.x) * kWaves) {
+    const int t = t0 + wave;
     const int a = t * kWave + lane;
     double w[6] = {0, 0, 0, 0, 0, 0};
-    if (VIRIAL && fdotr && a < nall) {
+    if (VIRIAL && fdotr && t < ntiles && a < nall) {
       const double *fa = f + 3L * a;
       const double *xa = x + 3L * a;
       w[0] = fa[0] * xa[0];
@@ -1016,8 +1032,14 @@ __global__ __launch_bounds__(256) void k_fdotr_rows(const double *__restrict__ f
 #pragma unroll
     for (int c = 0; c < 6; ++c) {
       const double v = wave_sum(w[c]);
-      if (lane == 0) partials[8L * t + 1 + c] = v;
+      if (lane == 0) tp[wave][c] = v;
     }
+    __syncthreads();
+    if (threadIdx.x < kWaves * 6) {
+      const int q = threadIdx.x / 6, c = threadIdx.x % 6;
+      if (t0 + q < ntiles) partials[8L * (t0 + q) + 1 + c] = tp[q][c];
+    }
+    __syncthreads();
   }
   finalize_last_block(partials, ntiles, escale, 1.0, flags, result, done, scratch, FusedPack{},
                       mirror);
@@ -1074,7 +1096,7 @@ static hipError_t eam_edge_force(Handle &h, hipStream_t s, int nlocal, int nghos
   S *epair = static_cast<S *>(h.d_epair);
   if (t.nblk > 0) {
     StageTimer timer(h, s, "eam_density");
-    hipLaunchKernelGGL((k_eam_density_inc<S, true>), dim3(grid_for(h, t.nblk, 1, 1)),
+    hipLaunchKernelGGL((k_eam_density_inc<S, true, true>), dim3(grid_for(h, t.nblk, 1, 1)),
                        dim3(kRowBlock), 0, s, m, t, rho_part, epair);
   }
   if (t.nblk > 0) {
