@@ -334,12 +334,22 @@ struct TwoSided {
   FusedPack pack;           // a fused pack of this step: tail reset and counts (else unused)
 };
 
-// The pack kept this entry's list slot this step (lists built from packed edges: always).
-__device__ __forceinline__ bool slot_kept(const TwoSided &t, int q)
+// Whether the pack kept an entry's list slot this step (lists built from packed edges: always),
+// split in two so the sweeps can put each load in its round trip: the entry's bit address goes
+// out with the entry itself, the validity word with the neighbour's record.
+__device__ __forceinline__ uint32_t slot_bit_address(const TwoSided &t, int q)
 {
-  if (!t.inc_bit) return true;
-  const uint32_t ba = t.inc_bit[q];
-  return ((t.bits[ba >> 5] >> (ba & 31u)) & 1u) != 0;
+  return t.inc_bit ? t.inc_bit[q] : 0u;
+}
+
+__device__ __forceinline__ uint32_t slot_word(const TwoSided &t, uint32_t ba)
+{
+  return t.inc_bit ? t.bits[ba >> 5] : ~0u;
+}
+
+__device__ __forceinline__ bool word_has(uint32_t word, uint32_t ba)
+{
+  return ((word >> (ba & 31u)) & 1u) != 0;
 }
 
 // Rows whose energy counts (export.py:183-194).
@@ -382,11 +392,14 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
       const int L = inc_off(t.loc, t.part, a + 1) - b;
       for (int k = gl; k < L; k += kGroup) {
         const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
+        const uint32_t ba = slot_bit_address(t, b + k);
         const bool in = (v >> 31) != 0;
         if (!HALF && in) continue;  // plain: density and pair energy stay on the sender
-        if (!slot_kept(t, b + k)) continue;
         const int o = static_cast<int>(v & 0x7FFFFFFFu);
+        // The record gather goes out with the validity word's, not after it: two memory round
+        // trips per entry instead of three (a dropped slot's record is simply not used).
         const Atom4<S> xo = m.atoms[o];
+        if (!word_has(slot_word(t, ba), ba)) continue;
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
         if (!(r2 < m.cutsq)) continue;
@@ -526,11 +539,14 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
       const int L = inc_off(t.loc, t.part, a + 1) - b;
       for (int k = gl; k < L; k += kGroup) {
         const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
+        const uint32_t ba = slot_bit_address(t, b + k);
         const bool in = (v >> 31) != 0;
         const int o = static_cast<int>(v & 0x7FFFFFFFu);
         if (!HALF && (in ? o : a) >= erows) continue;  // uncounted senders carry no gradient
-        if (!slot_kept(t, b + k)) continue;
+        // record and F' gathers issued with the validity word's (two round trips, not three)
         const Atom4<S> xo = m.atoms[o];
+        const S fpo = HALF || in ? m.fp[o] : S(0);
+        if (!word_has(slot_word(t, ba), ba)) continue;
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
         if (!(r2 < m.cutsq)) continue;
@@ -541,7 +557,7 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
         // Past the table the non-extrapolated lookups saturate: slope 0 (eam.py:150).
         const bool inside = !(L2.t_raw > S(1));
         const int zs = in ? zo : za, zr = in ? za : zo;
-        const S fps = in ? m.fp[o] : fpa;
+        const S fps = in ? fpo : fpa;
         const S rho_r_p = inside ? cslope_t(rcoef(win, m, L2.node, zr), L2.t) * m.inv_dr : S(0);
         const Coef<S> cp = rcoef(win, m, L2.node, m.n_el + pair_row(za, zo));
         const S phi = cvalue(cp, L2.t) * rinv;
@@ -550,7 +566,7 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
         const S phip = (z2p - phi) * rinv;
         S coef;
         if (HALF) {
-          const S fpr = in ? fpa : m.fp[o];
+          const S fpr = in ? fpa : fpo;
           const S rho_s_p = inside ? cslope_t(rcoef(win, m, L2.node, zs), L2.t) * m.inv_dr : S(0);
           coef = (fps * rho_r_p + fpr * rho_s_p + phip) * rinv;
         } else {
@@ -615,11 +631,12 @@ __global__ __launch_bounds__(kRowBlock) void k_lj_inc(LjModel<S> m, TwoSided t)
       const int L = inc_off(t.loc, t.part, a + 1) - b;
       for (int k = gl; k < L; k += kGroup) {
         const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
+        const uint32_t ba = slot_bit_address(t, b + k);
         const bool in = (v >> 31) != 0;
         const int o = static_cast<int>(v & 0x7FFFFFFFu);
         if ((in ? o : a) >= erows) continue;
-        if (!slot_kept(t, b + k)) continue;
-        const Atom4<S> xo = m.atoms[o];
+        const Atom4<S> xo = m.atoms[o];  // issued with the validity word's gather
+        if (!word_has(slot_word(t, ba), ba)) continue;
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
         if (!(r2 > tiny && r2 < m.cutsq)) continue;  // export_model.py:22
