@@ -352,6 +352,49 @@ __device__ __forceinline__ bool word_has(uint32_t word, uint32_t ba)
   return ((word >> (ba & 31u)) & 1u) != 0;
 }
 
+// The same two loads with the filter as a template flag (BITS: t.inc_bit is set) rather than a
+// null test, which would put a branch around them, for the force sweep's prefetching walk.
+template <bool BITS>
+__device__ __forceinline__ uint32_t slot_bit_address_of(const TwoSided &t, int q)
+{
+  if constexpr (BITS) return t.inc_bit[q];
+  return 0u;
+}
+
+template <bool BITS>
+__device__ __forceinline__ uint32_t slot_word_of(const TwoSided &t, uint32_t ba)
+{
+  if constexpr (BITS) return t.bits[ba >> 5];
+  return ~0u;
+}
+
+// The force sweep's walk over its atom's incident entries k = gl, gl + 16, ... with the next
+// entry (and its bit address) in flight while the current one is computed. Per entry the sweep
+// issues, in this order: the neighbour's record and F', the validity word, then advance(): the
+// next entry's loads go out after this entry's gathers, so waiting for the gathers never waits
+// for them. A skipped entry gathers its own row's record instead (cached), so no branch surrounds
+// a load. (The density and LJ sweeps, with less arithmetic per entry to cover the latency,
+// measured faster without it.)
+template <bool BITS>
+struct IncCursor {
+  uint32_t v = 0, ba = 0;
+  int b, last;
+  __device__ __forceinline__ IncCursor(const TwoSided &t, int b_, int L, int gl) : b(b_), last(b_ + L - 1)
+  {
+    if (gl < L) load(t, b + gl);
+  }
+  __device__ __forceinline__ void load(const TwoSided &t, int q)
+  {
+    v = static_cast<uint32_t>(t.inc[q]);
+    ba = slot_bit_address_of<BITS>(t, q);
+  }
+  __device__ __forceinline__ void advance(const TwoSided &t, int k)
+  {
+    asm volatile("" ::: "memory");  // keep these loads behind the current entry's gathers
+    load(t, min(b + k + kGroup, last));
+  }
+};
+
 // Rows whose energy counts (export.py:183-194).
 __device__ __forceinline__ int energy_rows(const TwoSided &t, bool half)
 {
@@ -519,7 +562,7 @@ __device__ __forceinline__ void store_tile_virial(double *partials, int blk,
 // Force sweep (eam.py:336-409 closed form; export.py:197-204 autodiff convention), and the pair
 // energy of the counted rows (eam.py:300-307) from the phi it evaluates anyway: on the sender,
 // both halves in the half scheme, half per directed edge in the plain one.
-template <typename S, bool HALF, bool VIRIAL>
+template <typename S, bool HALF, bool VIRIAL, bool BITS>
 __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSided t)
 {
   __shared__ LdsEntry<S> lds[kIncLds];
@@ -537,16 +580,17 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
       const S fpa = m.fp[a];
       const int b = inc_off(t.loc, t.part, a);
       const int L = inc_off(t.loc, t.part, a + 1) - b;
+      IncCursor<BITS> cur(t, b, L, gl);
       for (int k = gl; k < L; k += kGroup) {
-        const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
-        const uint32_t ba = slot_bit_address(t, b + k);
+        const uint32_t v = cur.v, ba = cur.ba;
         const bool in = (v >> 31) != 0;
         const int o = static_cast<int>(v & 0x7FFFFFFFu);
-        if (!HALF && (in ? o : a) >= erows) continue;  // uncounted senders carry no gradient
-        // record and F' gathers issued with the validity word's (two round trips, not three)
-        const Atom4<S> xo = m.atoms[o];
-        const S fpo = HALF || in ? m.fp[o] : S(0);
-        if (!word_has(slot_word(t, ba), ba)) continue;
+        const bool skip = !HALF && (in ? o : a) >= erows;  // uncounted senders: no gradient
+        const Atom4<S> xo = m.atoms[skip ? a : o];
+        const S fpo = m.fp[(HALF || in) && !skip ? o : a];
+        const uint32_t word = slot_word_of<BITS>(t, ba);
+        cur.advance(t, k);
+        if (skip || !word_has(word, ba)) continue;
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
         if (!(r2 < m.cutsq)) continue;
@@ -817,10 +861,15 @@ static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost
   }
   // one launch even with no rows: its last block writes the step result
   StageTimer timer(h, s, "eam_force");
-  if (flags & LK_VIRIAL)
-    hipLaunchKernelGGL((k_eam_force_inc<S, HALF, true>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+  const bool vir = (flags & LK_VIRIAL) != 0;
+  if (vir && t.inc_bit)
+    hipLaunchKernelGGL((k_eam_force_inc<S, HALF, true, true>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+  else if (vir)
+    hipLaunchKernelGGL((k_eam_force_inc<S, HALF, true, false>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+  else if (t.inc_bit)
+    hipLaunchKernelGGL((k_eam_force_inc<S, HALF, false, true>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
   else
-    hipLaunchKernelGGL((k_eam_force_inc<S, HALF, false>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+    hipLaunchKernelGGL((k_eam_force_inc<S, HALF, false, false>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
   return hipGetLastError();
 }
 
