@@ -48,9 +48,9 @@ def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: 
         if stage == "inc_sort":
             return 8 * E + 8 * E + 8 * E
         if stage == "eam_density":
-            return 8 * E + rec * A + 2 * S * A
+            return 8 * E + rec * A + S * A
         if stage == "eam_embed":
-            return 6 * S * A
+            return 5 * S * A
         if stage == "eam_force":
             return 8 * E + rec * A + S * A + 72 * A
         if stage == "lj_rows":
