@@ -25,6 +25,9 @@
 //   examples/export_model.py:52-74     make_lj_edge_force           -> or_lj_edge_forces
 //   cpp/pair_jax_kokkos.cpp:194-225    AddEdgeForcesFunctor         -> or_add_edge_forces
 //   cpp/pair_jax_kokkos.cpp:120-155    CopyNeighborMatrixFunctor    -> or_copy_neighbor_matrix
+//   the one-sided step above, row-parallel (OpenMP), for the benchmark's CPU baseline
+//                                                                   -> or_onesided_step
+//   (pinned against or_pack_neighbors + or_eam_compute(onesided) by tests/test_oracle.py)
 //
 // Forces are the closed-form gradient of the restated energy (the reference takes them by
 // autodiff); tests pin them by finite differences of or_eam_compute's energy, by the dense
@@ -692,6 +695,131 @@ double or_lj_compute(double epsilon, double sigma, double cutoff, double edge_en
   return lj_compute<double>(epsilon, sigma, cutoff, edge_energy_scale, positions, max_atoms,
                             nlocal, nghost, senders, receivers, mask, n_edges, mode,
                             owned_rows_only, forces, virial);
+}
+
+// The one-sided float64 EAM step as a row-parallel OpenMP restatement: the CPU baseline of the
+// benchmark. Per row (cpp:54-118 filter chain, full list, no half-edge or unique-boundary rule):
+// the kept neighbours in slot order and the row's density; the packed arrays in row order; the
+// embedding and F' of the owned rows and F' copied to the ghost rows (one-rank forward comm);
+// then each owned row's whole force added into f (scale * F), the energy and the pair virial
+// (eam_pallas.py:181-249 one-sided scheme, cpp:175-192). The same numbers as or_pack_neighbors +
+// or_eam_compute(kOneSided) up to the order of the sums. `scratch` holds inum * maxneighs ints.
+double or_onesided_step(int n_el, int nrho, double drho, int nr, double dr, double cutoff,
+                        const double *emb, const double *dens, const double *pair,
+                        const double *x, const int *type, int nall, int nlocal,
+                        const int *ilist, const int *numneigh, const int *neighbors, long stride,
+                        int inum, int maxneighs, int max_atoms, int max_edges, double pack_cutsq,
+                        const int *ghost_owner, double scale, int *scratch, int *senders,
+                        int *receivers, unsigned char *mask, long *count, double *f,
+                        double *virial, int threads)
+{
+  const Tables<double> T = make_tables<double>(n_el, nrho, drho, nr, dr, cutoff, emb, dens, pair);
+  int nt = threads;
+#ifdef _OPENMP
+  if (nt <= 0) nt = omp_get_max_threads();
+#else
+  nt = 1;
+#endif
+  const long nr4 = 4L * T.nr, nrho4 = 4L * T.nrho;
+  const int span = std::min(nall, max_atoms);
+  std::vector<double> rho(span, 0.0), fp(span, 0.0);
+  std::vector<int> cnt(inum, 0);
+  std::vector<long> off(static_cast<size_t>(inum) + 1, 0);
+#pragma omp parallel for num_threads(nt) schedule(static, 64)
+  for (int ii = 0; ii < inum; ++ii) {
+    const int i = ilist[ii];
+    if (i >= max_atoms) continue;
+    const int nn = std::min(numneigh[i], maxneighs);
+    int *kept = scratch + static_cast<long>(ii) * maxneighs;
+    int c = 0;
+    double r = 0.0;
+    for (int jj = 0; jj < nn; ++jj) {
+      const int j = neighbors[static_cast<long>(jj) * stride + i] & kNeighMask;
+      if (j >= max_atoms) continue;
+      const double dx = x[3 * i + 0] - x[3 * j + 0];
+      const double dy = x[3 * i + 1] - x[3 * j + 1];
+      const double dz = x[3 * i + 2] - x[3 * j + 2];
+      const double rsq = dx * dx + dy * dy + dz * dz;
+      if (rsq > pack_cutsq) continue;
+      kept[c++] = j;
+      if (rsq < T.cutsq)
+        r += spline_value(T.dens.data() + (type[j] - 1) * nr4, T.nr, T.dr, std::sqrt(rsq), false);
+    }
+    cnt[ii] = c;
+    rho[i] = r;
+  }
+  for (int ii = 0; ii < inum; ++ii) off[ii + 1] = off[ii] + cnt[ii];
+  *count = off[inum];
+#pragma omp parallel for num_threads(nt) schedule(static, 64)
+  for (int ii = 0; ii < inum; ++ii) {
+    const int i = ilist[ii];
+    const int *kept = scratch + static_cast<long>(ii) * maxneighs;
+    for (int k = 0; k < cnt[ii]; ++k) {
+      const long e = off[ii] + k;
+      if (e >= max_edges) break;
+      senders[e] = i;
+      receivers[e] = kept[k];
+      mask[e] = 1;
+    }
+  }
+  double e_emb = 0.0;
+#pragma omp parallel for num_threads(nt) schedule(static) reduction(+ : e_emb)
+  for (int i = 0; i < std::min(nlocal, span); ++i) {
+    const double *c = T.emb.data() + (type[i] - 1) * nrho4;
+    e_emb += spline_value(c, T.nrho, T.drho, rho[i], true);
+    fp[i] = spline_slope(c, T.nrho, T.drho, rho[i], true);
+  }
+  if (ghost_owner)
+    for (int g = nlocal; g < span; ++g) fp[g] = fp[ghost_owner[g - nlocal]];
+  double e_pair = 0.0, w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
+#pragma omp parallel for num_threads(nt) schedule(static, 64) \
+    reduction(+ : e_pair, w0, w1, w2, w3, w4, w5)
+  for (int ii = 0; ii < inum; ++ii) {
+    const int i = ilist[ii];
+    if (i >= nlocal || i >= max_atoms) continue;  // one-sided: owned rows take the force
+    const int zi = type[i] - 1;
+    const int *kept = scratch + static_cast<long>(ii) * maxneighs;
+    double fx = 0.0, fy = 0.0, fz = 0.0;
+    for (int k = 0; k < cnt[ii]; ++k) {
+      const int j = kept[k];
+      const double d0 = x[3 * j + 0] - x[3 * i + 0];
+      const double d1 = x[3 * j + 1] - x[3 * i + 1];
+      const double d2 = x[3 * j + 2] - x[3 * i + 2];
+      const double r2 = d0 * d0 + d1 * d1 + d2 * d2;
+      if (!(r2 < T.cutsq)) continue;
+      const double rr = std::sqrt(r2);
+      const int zj = type[j] - 1;
+      const double *pt = T.pair.data() + pair_row(zi, zj) * nr4;
+      const double z2 = spline_value(pt, T.nr, T.dr, rr, false);
+      const double z2p = spline_slope(pt, T.nr, T.dr, rr, false);
+      const double phi = z2 / rr;
+      const double phip = (z2p - phi) / rr;
+      const double rhojp = spline_slope(T.dens.data() + zj * nr4, T.nr, T.dr, rr, false);
+      const double rhoip = spline_slope(T.dens.data() + zi * nr4, T.nr, T.dr, rr, false);
+      const double coef = (fp[i] * rhojp + fp[j] * rhoip + phip) / rr;
+      e_pair += 0.5 * phi;
+      fx += coef * d0;
+      fy += coef * d1;
+      fz += coef * d2;
+      const double c = 0.5 * coef;
+      w0 -= c * d0 * d0;
+      w1 -= c * d1 * d1;
+      w2 -= c * d2 * d2;
+      w3 -= c * d0 * d1;
+      w4 -= c * d0 * d2;
+      w5 -= c * d1 * d2;
+    }
+    f[3 * i + 0] += scale * fx;
+    f[3 * i + 1] += scale * fy;
+    f[3 * i + 2] += scale * fz;
+  }
+  virial[0] = scale * w0;
+  virial[1] = scale * w1;
+  virial[2] = scale * w2;
+  virial[3] = scale * w3;
+  virial[4] = scale * w4;
+  virial[5] = scale * w5;
+  return scale * (e_emb + e_pair);
 }
 
 int or_num_threads(void)

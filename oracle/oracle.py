@@ -68,6 +68,10 @@ def _load():
     lib.or_add_edge_forces.restype = None
     lib.or_copy_neighbor_matrix.argtypes = [vp, vp, lp, ip, ip, ip, ip, vp, vp, vp, vp]
     lib.or_copy_neighbor_matrix.restype = None
+    lib.or_onesided_step.argtypes = [ip, ip, dp, ip, dp, dp, vp, vp, vp, vp, vp, ip, ip, vp, vp,
+                                     vp, lp, ip, ip, ip, ip, dp, vp, dp, vp, vp, vp, vp, vp, vp,
+                                     vp, ip]
+    lib.or_onesided_step.restype = dp
     lib.or_num_threads.argtypes = []
     lib.or_num_threads.restype = ip
     _lib = lib
@@ -132,6 +136,54 @@ def pack_neighbors(x, lst, *, max_atoms, max_edges, nlocal, cutoff, n_hops=1, du
         int(unique_boundary), int(cached_count), s.ctypes.data, r.ctypes.data, m.ctypes.data,
         ctypes.byref(ovf))
     return s, r, m, int(count), int(ovf.value)
+
+
+class OneSidedStep:
+    """The one-sided float64 EAM step as a row-parallel OpenMP restatement (or_onesided_step):
+    pack, density, embedding, row forces added into f, energy and pair virial. The CPU baseline
+    of the benchmark; buffers are allocated once, like the device contract's."""
+
+    def __init__(self, tables, x, types, lst, *, nlocal, max_atoms, max_edges, cutoff,
+                 ghost_owner=None, threads=0):
+        self.tables = {k: _c(tables[k], np.float64) for k in ("embedding", "density", "pair")}
+        self.meta = (int(self.tables["embedding"].shape[0]), int(tables["nrho"]),
+                     float(tables["drho"]), int(tables["nr"]), float(tables["dr"]),
+                     float(tables["cutoff"]))
+        self.x = _c(x, np.float64)
+        self.types = _c(types, np.int32)
+        self.lst = {k: _c(lst[k], np.int32) for k in ("ilist", "numneigh", "neighbors")}
+        self.stride, self.inum = int(lst["stride"]), int(lst["inum"])
+        self.maxneighs = max(1, int(lst["maxneighs"]))
+        self.nlocal, self.max_atoms, self.max_edges = int(nlocal), int(max_atoms), int(max_edges)
+        self.cutsq = float(cutoff) * float(cutoff)
+        self.go = None if ghost_owner is None else _c(ghost_owner, np.int32)
+        self.threads = int(threads)
+        self.scratch = np.zeros(self.inum * self.maxneighs, np.int32)
+        self.senders = np.full(self.max_edges, self.max_atoms, np.int32)
+        self.receivers = np.full(self.max_edges, self.max_atoms, np.int32)
+        self.mask = np.zeros(self.max_edges, np.uint8)
+        self.f = np.zeros((len(self.x), 3))
+        self.virial = np.zeros(6)
+
+    @staticmethod
+    def threads_available() -> int:
+        return int(_load().or_num_threads())
+
+    def __call__(self, scale=1.0):
+        """One step; forces add into self.f. Returns (energy, count)."""
+        count = ctypes.c_long(0)
+        t = self.tables
+        e = _load().or_onesided_step(
+            *self.meta, t["embedding"].ctypes.data, t["density"].ctypes.data,
+            t["pair"].ctypes.data, self.x.ctypes.data, self.types.ctypes.data, len(self.x),
+            self.nlocal, self.lst["ilist"].ctypes.data, self.lst["numneigh"].ctypes.data,
+            self.lst["neighbors"].ctypes.data, self.stride, self.inum, self.maxneighs,
+            self.max_atoms, self.max_edges, self.cutsq,
+            None if self.go is None else self.go.ctypes.data, float(scale),
+            self.scratch.ctypes.data, self.senders.ctypes.data, self.receivers.ctypes.data,
+            self.mask.ctypes.data, ctypes.byref(count), self.f.ctypes.data,
+            self.virial.ctypes.data, self.threads)
+        return e, int(count.value)
 
 
 def eam_compute(tables, positions, species, *, nlocal, nghost, senders, receivers, mask,

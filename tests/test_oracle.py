@@ -17,7 +17,7 @@ import oracle as O
 from lk_testutil import GOLDEN, all_pairs_within, canonical, fold_ghosts, list_pairs, padded, \
     random_cluster, rel_err
 from lammps_jax_amd import setfl as setfl_mod
-from lammps_jax_amd import systems
+from lammps_jax_amd import harness, systems
 
 
 @pytest.fixture(scope="module")
@@ -563,3 +563,36 @@ def test_copy_neighbor_matrix_holds_the_list():
     got = set(zip(s.tolist(), r.tolist()))
     want = set(map(tuple, list_pairs(lst, sysm.x, 1.0e9, lst["inum"]).tolist()))  # every entry
     assert got == want
+
+
+def test_openmp_onesided_step_matches_the_serial_oracle():
+    """or_onesided_step (the benchmark's CPU baseline) against or_pack_neighbors +
+    or_eam_compute(one-sided): the same packed edges in row order, forces, energy and virial up to
+    the order of the sums, and the same results on 1 and 4 threads."""
+    wl = systems.make_workload("eam_alloy_131k", cells=(3, 3, 3), seed=21)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    nall, nl = sysm.nall, sysm.nlocal
+    ma, me = nall + 32, (nall + 32) * 128
+    pos, sp = O.pack_atoms(sysm.x, sysm.type, nall, ma, 8)
+    s, r, m, count, _ = O.pack_neighbors(sysm.x, lst, max_atoms=ma, max_edges=me, nlocal=nl,
+                                         cutoff=wl.cutoff)
+    ref = O.eam_compute(wl.tables, pos, sp, nlocal=nl, nghost=sysm.nghost, senders=s,
+                        receivers=r, mask=m, mode=O.ONESIDED, ghost_owner=sysm.ghost_owner)
+    runs = []
+    for threads in (1, 4):
+        step = O.OneSidedStep(wl.tables, sysm.x, sysm.type, lst, nlocal=nl, max_atoms=ma,
+                              max_edges=me, cutoff=wl.cutoff, ghost_owner=sysm.ghost_owner,
+                              threads=threads)
+        e, c = step(scale=0.5)
+        assert c == count
+        np.testing.assert_array_equal(canonical(step.senders, step.receivers, step.mask),
+                                      canonical(s, r, m))
+        assert e == pytest.approx(0.5 * ref["energy"], rel=1e-12)
+        assert rel_err(step.f[:nl], 0.5 * ref["forces"][:nl]) < 1e-12
+        assert np.all(step.f[nl:] == 0.0)  # one-sided: ghost rows take no force
+        assert rel_err(step.virial, 0.5 * ref["virial"]) < 1e-12
+        runs.append((e, step.f.copy(), step.senders[:c].copy()))
+    # rows are independent: the packed order and the row forces do not depend on the threads
+    np.testing.assert_array_equal(runs[0][2], runs[1][2])
+    np.testing.assert_array_equal(runs[0][1], runs[1][1])
