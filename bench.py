@@ -123,6 +123,27 @@ def cpu_baseline(wl, sysm, lst, max_atoms, max_edges, budget_s: float, max_steps
     }
 
 
+def copy_ceiling_gbs(mib: int = 1024, reps: int = 10) -> float:
+    """Measured device-copy bandwidth (read + write bytes / time), a STREAM-like ceiling for the
+    HBM roofline: `reps` copies of `mib` MiB timed with HIP events, after one warm copy."""
+    import torch
+
+    n = mib * (1 << 20) // 8
+    src = torch.ones(n, dtype=torch.float64, device="cuda:0")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    end.synchronize()
+    gbs = 2.0 * n * 8 * reps / (start.elapsed_time(end) * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return gbs
+
+
 def calibrate_copy(mib: int) -> int:
     """A plain copy of known size: FETCH_SIZE and WRITE_SIZE of its dispatches give the factor
     that turns the counters into bytes (expected bytes / counted bytes)."""
@@ -390,6 +411,7 @@ def main() -> int:
             "device_us": round(device_us, 2),
             "frac_of_hbm_peak": sb["total"] / (device_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
         },
+        "copy_ceiling_gbs": round(copy_ceiling_gbs(), 1),
     }
     print(json.dumps(line))
     return 0
