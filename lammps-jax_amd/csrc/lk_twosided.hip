@@ -56,6 +56,12 @@ __device__ __forceinline__ long live_edges(const StepResult *r, int max_edges)
   return c < max_edges ? c : max_edges;
 }
 
+__global__ __launch_bounds__(256) void k_clear_int(int *p, long n)
+{
+  const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
 __device__ __forceinline__ int inc_off(const int *loc, const int *part, int a)
 {
   return loc[a] + part[a / kScanChunk];
@@ -194,7 +200,9 @@ __global__ __launch_bounds__(256) void k_inc_sort(IncArgs a, int nsort)
       const uint32_t w = c1 + lane < L ? a.tmp[b + c1 + lane] : 0xFFFFFFFFu;
 #pragma unroll 16
       for (int m = 0; m < kWave; ++m) {
-        const uint32_t wm = static_cast<uint32_t>(__shfl(static_cast<int>(w), m, kWave));
+        // lane m's key broadcast through a scalar register (v_readlane), not the LDS crossbar
+        const uint32_t wm =
+            static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(w), m));
         rank += wm < v ? 1 : 0;
       }
     }
@@ -207,10 +215,13 @@ __global__ __launch_bounds__(256) void k_inc_sort(IncArgs a, int nsort)
   }
 }
 
-// Incidence lists from the neighbour-list slots (once per list). Slot f = jj * rows + ii (the
-// reference packer's flat order, cpp:77-83) passes the list's static filters of
-// PackNeighborFunctor (cpp:84-94: rows past max_atoms, jj >= numneigh, j >= max_atoms, the half
-// filter j < i); its distance filter is applied each step from the pack's validity bits.
+// Incidence lists from the neighbour-list slots (once per list). Slot (ii, jj) passes the
+// list's static filters of PackNeighborFunctor (cpp:84-94: rows past max_atoms, jj >= numneigh,
+// j >= max_atoms, the half filter j < i); its distance filter is applied each step from the
+// pack's validity bits. Atom a's list is its out-entries (the kept slots of its own row, in slot
+// order: other = j) followed by its in-entries (slots of other rows naming a: other = i, side
+// bit set) in ascending flat slot f = jj * rows + ii (the reference packer's flat order,
+// cpp:77-83). Only the in-entries need atomics and a sort; each row places its own out-entries.
 struct ListArgs {
   const int *ilist;
   const int *numneigh;
@@ -229,54 +240,88 @@ struct ListArgs {
   uint32_t *inc_bit;
 };
 
-__device__ __forceinline__ bool list_slot(const ListArgs &L, long f, int &i, int &j)
+// The row atom of list row ii and its slot count, or -1 when the row packs nothing.
+__device__ __forceinline__ int list_row(const ListArgs &L, int ii, int &nn)
 {
-  const int ii = static_cast<int>(f % L.rows);
-  const int jj = static_cast<int>(f / L.rows);
-  i = L.ilist[ii];
-  if (i < 0 || i >= L.max_atoms) return false;
-  const int nn = min(L.numneigh[i], L.maxneighs);
-  if (jj >= nn) return false;
+  const int i = L.ilist[ii];
+  nn = 0;
+  if (i < 0 || i >= L.max_atoms) return -1;
+  nn = min(L.numneigh[i], L.maxneighs);
+  return i;
+}
+
+__device__ __forceinline__ bool list_neighbor(const ListArgs &L, int i, int jj, int &j)
+{
   j = L.neighbors[static_cast<long>(jj) * L.stride + i] & kNeighMask;
   if (j >= L.max_atoms) return false;
   return !(L.half_filter && j < i);
 }
 
+// Validity-bit address of slot (ii, jj): word (jj >> 5) * pitch + ii, bit jj & 31.
+__device__ __forceinline__ uint32_t slot_bit(const ListArgs &L, int ii, int jj)
+{
+  return ((static_cast<uint32_t>(jj >> 5) * static_cast<uint32_t>(L.pitch) +
+           static_cast<uint32_t>(ii))
+          << 5) |
+         static_cast<uint32_t>(jj & 31);
+}
+
+// One thread per row: the row's kept slots count once on its own atom, and once on each
+// neighbour (deg was cleared before).
 __global__ __launch_bounds__(256) void k_inc_list_count(ListArgs L)
 {
-  const long n = static_cast<long>(L.rows) * L.maxneighs;
-  for (long f = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; f < n;
-       f += static_cast<long>(gridDim.x) * blockDim.x) {
-    int i, j;
-    if (!list_slot(L, f, i, j)) continue;
-    atomicAdd(&L.deg[i], 1);
+  const int ii = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ii >= L.rows) return;
+  int nn;
+  const int i = list_row(L, ii, nn);
+  if (i < 0) return;
+  int out = 0;
+  for (int jj = 0; jj < nn; ++jj) {
+    int j;
+    if (!list_neighbor(L, i, jj, j)) continue;
+    ++out;
     atomicAdd(&L.deg[j], 1);
   }
+  if (out) atomicAdd(&L.deg[i], out);
 }
 
+// One thread per row: out-entries in slot order at the front of the row atom's list; each
+// in-entry's key (f << 1 | 1) into the neighbour's in-part, counting its deg down (deg ends at
+// the out-count, which the sort reads).
 __global__ __launch_bounds__(256) void k_inc_list_fill(ListArgs L)
 {
-  const long n = static_cast<long>(L.rows) * L.maxneighs;
-  for (long f = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; f < n;
-       f += static_cast<long>(gridDim.x) * blockDim.x) {
-    int i, j;
-    if (!list_slot(L, f, i, j)) continue;
-    const uint32_t key = static_cast<uint32_t>(f) << 1;
-    const int pi = inc_off(L.loc, L.part, i) + atomicSub(&L.deg[i], 1) - 1;
-    L.tmp[pi] = key;
+  const int ii = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ii >= L.rows) return;
+  int nn;
+  const int i = list_row(L, ii, nn);
+  if (i < 0) return;
+  const int b = inc_off(L.loc, L.part, i);
+  int k = 0;
+  for (int jj = 0; jj < nn; ++jj) {
+    int j;
+    if (!list_neighbor(L, i, jj, j)) continue;
+    L.inc[b + k] = j;
+    L.inc_bit[b + k] = slot_bit(L, ii, jj);
+    ++k;
+    const uint32_t f = static_cast<uint32_t>(jj) * static_cast<uint32_t>(L.rows) +
+                       static_cast<uint32_t>(ii);
     const int pj = inc_off(L.loc, L.part, j) + atomicSub(&L.deg[j], 1) - 1;
-    L.tmp[pj] = key | 1u;
+    L.tmp[pj] = (f << 1) | 1u;
   }
 }
 
-// As k_inc_sort: rank by slot, then store the other atom (side in the top bit) and the address
-// of the slot's validity bit, word ((jj >> 5) * pitch + ii), bit jj & 31.
+// One wave per atom: rank sort of the in-part by slot key (keys are distinct), so its store
+// order is ascending f whatever order the fill left; then the other atom (side bit set) and the
+// slot's validity-bit address.
 __global__ __launch_bounds__(256) void k_inc_list_sort(ListArgs L, int nsort)
 {
   const int atom = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   if (atom >= nsort) return;  // whole wave
-  const int b = inc_off(L.loc, L.part, atom);
+  const int b0 = inc_off(L.loc, L.part, atom);
+  const int out = L.deg[atom];
+  if (lane == 0) L.deg[atom] = 0;  // read by the whole wave above; zero again between builds
+  const int b = b0 + out;
   const int len = inc_off(L.loc, L.part, atom + 1) - b;
   for (int c0 = 0; c0 < len; c0 += kWave) {
     const bool mine = c0 + lane < len;
@@ -286,22 +331,19 @@ __global__ __launch_bounds__(256) void k_inc_list_sort(ListArgs L, int nsort)
       const uint32_t w = c1 + lane < len ? L.tmp[b + c1 + lane] : 0xFFFFFFFFu;
 #pragma unroll 16
       for (int m = 0; m < kWave; ++m) {
-        const uint32_t wm = static_cast<uint32_t>(__shfl(static_cast<int>(w), m, kWave));
+        // lane m's key broadcast through a scalar register (v_readlane), not the LDS crossbar
+        const uint32_t wm =
+            static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(w), m));
         rank += wm < v ? 1 : 0;
       }
     }
     if (mine) {
-      const long f = v >> 1;
-      const uint32_t side = v & 1u;
-      const int ii = static_cast<int>(f % L.rows);
-      const int jj = static_cast<int>(f / L.rows);
+      const uint32_t f = v >> 1;
+      const int ii = static_cast<int>(f % static_cast<uint32_t>(L.rows));
+      const int jj = static_cast<int>(f / static_cast<uint32_t>(L.rows));
       const int i = L.ilist[ii];
-      const int other =
-          side ? i : (L.neighbors[static_cast<long>(jj) * L.stride + i] & kNeighMask);
-      L.inc[b + rank] = static_cast<int>(static_cast<uint32_t>(other) | (side << 31));
-      L.inc_bit[b + rank] =
-          ((static_cast<uint32_t>(jj >> 5) * static_cast<uint32_t>(L.pitch) + static_cast<uint32_t>(ii))
-           << 5) | static_cast<uint32_t>(jj & 31);
+      L.inc[b + rank] = static_cast<int>(static_cast<uint32_t>(i) | (1u << 31));
+      L.inc_bit[b + rank] = slot_bit(L, ii, jj);
     }
   }
 }
@@ -741,6 +783,11 @@ static hipError_t build_incidence(Handle &h, hipStream_t s, int nall)
   const int egrid = grid_for(h, h.contract.max_edges, 256, 16);
   {
     StageTimer timer(h, s, "inc_count");
+    // the counts start from zero whatever the previous build left (a list-built build keeps
+    // out-counts in deg until its sort clears them)
+    const long n = static_cast<long>(h.contract.max_atoms) + 1;
+    hipLaunchKernelGGL(k_clear_int, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                       h.d_deg, n);
     hipLaunchKernelGGL(k_inc_count, dim3(egrid), dim3(256), 0, s, ia);
   }
   {
@@ -781,10 +828,14 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall)
   L.inc = h.d_inc;
   L.inc_bit = h.d_inc_bit;
   const long slots = static_cast<long>(L.rows) * L.maxneighs;
-  const int grid = grid_for(h, slots > 0 ? slots : 1, 256, 16);
-  if (slots > 0) {
+  const int row_blocks = (L.rows + 255) / 256;
+  {
     StageTimer timer(h, s, "inc_count");
-    hipLaunchKernelGGL(k_inc_list_count, dim3(grid), dim3(256), 0, s, L);
+    const long n = static_cast<long>(h.contract.max_atoms) + 1;
+    hipLaunchKernelGGL(k_clear_int, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                       h.d_deg, n);
+    if (slots > 0)
+      hipLaunchKernelGGL(k_inc_list_count, dim3(row_blocks), dim3(256), 0, s, L);
   }
   {
     StageTimer timer(h, s, "inc_scan");
@@ -796,7 +847,7 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall)
   }
   if (slots > 0) {
     StageTimer timer(h, s, "inc_fill");
-    hipLaunchKernelGGL(k_inc_list_fill, dim3(grid), dim3(256), 0, s, L);
+    hipLaunchKernelGGL(k_inc_list_fill, dim3(row_blocks), dim3(256), 0, s, L);
   }
   if (nall > 0) {
     StageTimer timer(h, s, "inc_sort");
