@@ -112,72 +112,97 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
     const bool lds_bits = nwords <= kStepMaxWords;
     int cnt = 0;
     S rho = S(0);
-    for (int w = wave; w < nwords; w += W) {
-      uint32_t word = 0;
-      const int jj0 = w * 32;
-      const int jj1 = min(jj0 + 32, nn_max);
-      for (int jj = jj0; jj < jj1; ++jj) {
-        if (jj >= nn) continue;
-        const int j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
-        if (j >= p.max_atoms) continue;
-        double rsq;
-        double xj0, xj1, xj2;
-        int zj = 0;
+    // One list slot of this lane's row: the filter chain, and the density of a kept pair.
+    auto visit = [&](int jj) -> bool {
+      if (jj >= nn) return false;
+      const int j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
+      if (j >= p.max_atoms) return false;
+      double rsq;
+      double xj0, xj1, xj2;
+      int zj = 0;
+      if constexpr (sizeof(S) == 8) {
+        // float64 records hold the engine's x exactly: one 32-byte gather (two 16-byte loads)
+        // brings x and species. The empty asm takes the species where it arrives, so the
+        // compiler cannot defer it into an 8-byte gather of its own behind the filter.
+        const Atom4<double> rj = reinterpret_cast<const Atom4<double> *>(a.atoms)[j];
+        asm volatile("" ::"v"(rj.w));
+        xj0 = rj.x;
+        xj1 = rj.y;
+        xj2 = rj.z;
+        zj = static_cast<int>(rj.w);
+      } else {
+        xj0 = p.x[3L * j + 0];
+        xj1 = p.x[3L * j + 1];
+        xj2 = p.x[3L * j + 2];
+        if constexpr (EAM) zj = p.type[j] - 1;
+      }
+      {
+#pragma clang fp contract(off)
+        const double dx = xi0 - xj0, dy = xi1 - xj1, dz = xi2 - xj2;
+        rsq = dx * dx + dy * dy + dz * dz;
+      }
+      if constexpr (!MATRIX) {
+        if (rsq > p.cutsq) return false;  // PackNeighborFunctor keeps rsq <= cutsq (cpp:91)
+      }
+      S r2 = S(0);
+      if constexpr (EAM) {
         if constexpr (sizeof(S) == 8) {
-          // float64 records hold the engine's x exactly: one 32-byte gather (two 16-byte loads)
-          // brings x and species. The empty asm takes the species where it arrives, so the
-          // compiler cannot defer it into an 8-byte gather of its own behind the filter.
-          const Atom4<double> rj = reinterpret_cast<const Atom4<double> *>(a.atoms)[j];
-          asm volatile("" ::"v"(rj.w));
-          xj0 = rj.x;
-          xj1 = rj.y;
-          xj2 = rj.z;
-          zj = static_cast<int>(rj.w);
+          r2 = rsq;  // the model's (x_j - x_i)^2 sum is the same float64 value
         } else {
-          xj0 = p.x[3L * j + 0];
-          xj1 = p.x[3L * j + 1];
-          xj2 = p.x[3L * j + 2];
-          if constexpr (EAM) zj = p.type[j] - 1;
-        }
-        {
 #pragma clang fp contract(off)
-          const double dx = xi0 - xj0, dy = xi1 - xj1, dz = xi2 - xj2;
-          rsq = dx * dx + dy * dy + dz * dz;
-        }
-        if constexpr (!MATRIX) {
-          if (rsq > p.cutsq) continue;  // PackNeighborFunctor keeps rsq <= cutsq (cpp:91)
-        }
-        S r2 = S(0);
-        if constexpr (EAM) {
-          if constexpr (sizeof(S) == 8) {
-            r2 = rsq;  // the model's (x_j - x_i)^2 sum is the same float64 value
-          } else {
-#pragma clang fp contract(off)
-            const S dx = static_cast<S>(xj0) - static_cast<S>(xi0);
-            const S dy = static_cast<S>(xj1) - static_cast<S>(xi1);
-            const S dz = static_cast<S>(xj2) - static_cast<S>(xi2);
-            r2 = dx * dx + dy * dy + dz * dz;
-          }
-        }
-        if constexpr (MATRIX) {
-          if (!(r2 < a.cutsq)) continue;
-        }
-        word |= 1u << (jj & 31);
-        ++cnt;
-        if constexpr (EAM) {
-          if (MATRIX || r2 < a.cutsq) {  // valid = mask & r_sq < cutoff_sq (eam.py:288)
-            const S rr = r2 * rsqrt_nr(r2);
-            const Locator<S> L = locate_mul(rr, a.inv_dr, a.nr);
-            rho += cvalue(rcoef(win, a, L.node, clamp_species(zj, a.n_el)), L.t);
-          }
+          const S dx = static_cast<S>(xj0) - static_cast<S>(xi0);
+          const S dy = static_cast<S>(xj1) - static_cast<S>(xi1);
+          const S dz = static_cast<S>(xj2) - static_cast<S>(xi2);
+          r2 = dx * dx + dy * dy + dz * dz;
         }
       }
-      if (row) p.bits[static_cast<long>(w) * p.pitch + ii] = word;
-      if (lds_bits) sbits[sub][w][lane] = word;
+      if constexpr (MATRIX) {
+        if (!(r2 < a.cutsq)) return false;
+      }
+      ++cnt;
+      if constexpr (EAM) {
+        if (MATRIX || r2 < a.cutsq) {  // valid = mask & r_sq < cutoff_sq (eam.py:288)
+          const S rr = r2 * rsqrt_nr(r2);
+          const Locator<S> L = locate_mul(rr, a.inv_dr, a.nr);
+          rho += cvalue(rcoef(win, a, L.node, clamp_species(zj, a.n_el)), L.t);
+        }
+      }
+      return true;
+    };
+    // Rows of fewer than W words (half lists) would leave waves idle under one word per wave:
+    // there each wave takes every W-th slot and ORs its bits into the tile's LDS words, which
+    // the first barrier below completes (the global words are stored after it).
+    const bool strided = nwords < W;
+    if (strided && wave == 0)
+      for (int w = 0; w < nwords; ++w) sbits[sub][w][lane] = 0u;
+    __syncthreads();
+    if (strided) {
+      for (int w = 0; w < nwords; ++w) {
+        uint32_t part = 0;
+        for (int k = wave; k < 32; k += W) {
+          const int jj = w * 32 + k;
+          if (jj >= nn_max) break;
+          if (visit(jj)) part |= 1u << k;
+        }
+        if (part) atomicOr(&sbits[sub][w][lane], part);
+      }
+    } else {
+      for (int w = wave; w < nwords; w += W) {
+        uint32_t word = 0;
+        const int jj0 = w * 32;
+        const int jj1 = min(jj0 + 32, nn_max);
+        for (int jj = jj0; jj < jj1; ++jj)
+          if (visit(jj)) word |= 1u << (jj & 31);
+        if (row) p.bits[static_cast<long>(w) * p.pitch + ii] = word;
+        if (lds_bits) sbits[sub][w][lane] = word;
+      }
     }
     cpart[sub][wave][lane] = cnt;
     if constexpr (EAM) rpart[sub][wave][lane] = rho;
     __syncthreads();
+    if (strided && row)
+      for (int w = wave; w < nwords; w += W)
+        p.bits[static_cast<long>(w) * p.pitch + ii] = sbits[sub][w][lane];
     if (wave == 0) {
       cnt = cpart[sub][0][lane];
       if constexpr (EAM) rho = rpart[sub][0][lane];
