@@ -155,3 +155,33 @@ def test_fused_step_tail_reset_and_overflow(gpu):
     info = small.compute(check_capacity=False)
     assert info.edge_overflow == 1 and info.edge_count == first.edge_count
     assert int(small.edges()[2].sum()) == 3000
+
+
+@pytest.mark.parametrize("accum,fused", [("onesided", True), ("onesided", False), ("plain", True)])
+def test_rows_longer_than_the_lds_bit_words(gpu, accum, fused):
+    """LJ with a 4.4 sigma cutoff: about 370 list slots per row, more than the 256 whose validity
+    words the tile pack keeps in LDS, so its compacted write (and the plain scheme's incidence
+    filter) read the words back from the global bits."""
+    wl = systems.make_workload("lj_fcc_1k", cells=(6, 6, 6), seed=31)
+    lj = dict(wl.lj, cutoff=4.4)
+    sysm = systems.System(wl.x, wl.types, wl.box, lj["cutoff"] + wl.skin)
+    lst = sysm.build_list(lj["cutoff"] + wl.skin, kind=harness.LIST_FULL)
+    assert lst["maxneighs"] > 256
+    pj = PairJax(sysm, ("lj", lj), precision=8, accumulation=accum, fused=fused,
+                 edges_per_atom=400)
+    print(f"long-row case {accum} fused={fused} nall={sysm.nall} maxneighs={lst['maxneighs']}",
+          flush=True)
+    info = pj.compute()
+    f = pj.forces()
+    nl, nall = sysm.nlocal, sysm.nall
+    pos, _ = O.pack_atoms(sysm.x, sysm.type, nall, pj.max_atoms, 8)
+    s, r, m, count, _ = O.pack_neighbors(sysm.x, lst, max_atoms=pj.max_atoms,
+                                         max_edges=pj.max_edges, nlocal=nl, cutoff=lj["cutoff"])
+    mode = O.ONESIDED if accum == "onesided" else O.PLAIN
+    ref = O.lj_compute(lj, pos, nlocal=nl, nghost=sysm.nghost, senders=s, receivers=r, mask=m,
+                       mode=mode)
+    assert info.edge_count == count and info.edge_overflow == 0
+    np.testing.assert_array_equal(canonical(*pj.edges()), canonical(s, r, m))
+    assert info.energy == pytest.approx(ref["energy"], rel=1e-10)
+    rows = nl if accum == "onesided" else nall
+    assert rel_err(f[:rows], ref["forces"][:rows]) < 1e-10
