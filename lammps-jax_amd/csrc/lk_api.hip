@@ -56,7 +56,7 @@ void free_all(Handle &h)
                   h.d_result,    h.d_ghost_owner, h.d_ghost_off, h.d_ghost_list, h.d_done,
                   h.d_deg,       h.d_inc_loc,   h.d_inc_part,    h.d_inc_tmp,   h.d_inc,
                   h.d_rho_part,  h.d_epair,     h.d_pack_state,  h.d_inc_bit,   h.d_edge_f,
-                  h.d_matrix,    h.d_num_neighbors, h.d_identity};
+                  h.d_matrix,    h.d_num_neighbors, h.d_identity, h.d_inc_len};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -95,6 +95,7 @@ int ensure_incidence(Handle &h, long entries = 0)
     if ((e = dalloc(&h.d_deg, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence counts)");
     if ((e = dalloc(&h.d_inc_loc, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence offsets)");
     if ((e = dalloc(&h.d_inc_part, chunks)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence chunks)");
+    if ((e = dalloc(&h.d_inc_len, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence lengths)");
     if ((e = hipMalloc(&h.d_rho_part, A * h.scalar_bytes())) != hipSuccess) return hip_fail(h, e, "hipMalloc(rho partials)");
     if ((e = hipMalloc(&h.d_epair, A * h.scalar_bytes())) != hipSuccess) return hip_fail(h, e, "hipMalloc(pair energy)");
     if ((e = hipMemset(h.d_deg, 0, sizeof(int) * (A + 1))) != hipSuccess) return hip_fail(h, e, "hipMemset(incidence counts)");

@@ -11,6 +11,13 @@ constexpr int kWave = 64;
 // LAMMPS NEIGHMASK: the two top bits of a neighbour entry carry special-bond flags.
 constexpr int kNeighMask = 0x3FFFFFFF;
 
+// Eight waves per SIMD (two 1024-thread blocks per CU) run on gfx950 only while a wave holds at
+// most 80 SGPRs, VCC and the other reserved ones included: the compiler counts 96 as fitting,
+// but a two-sided LJ sweep built at 82 ran one block per CU, half the resident waves and 1.4x
+// the time. Kernels launched for eight waves per SIMD carry this cap (the compiler keeps within
+// it, moving a few values to VGPR lanes).
+#define LK_EIGHT_WAVES __attribute__((amdgpu_num_sgpr(80)))
+
 // ----------------------------------------------------------------------------------------------
 // Wave64 primitives
 // ----------------------------------------------------------------------------------------------

@@ -32,7 +32,7 @@ constexpr int kForceW = 4, kForceTPB = 4, kForceLds = 7680;  // 120 KB table win
 // Density sweep (one-sided): rho_i over the row's own edges, then F(rho_i), F'(rho_i). Owned rows
 // add F(rho_i) to the tile's energy partial.
 template <typename S, int W, int TPB>
-__global__ __launch_bounds__(W * TPB * 64) void k_eam_density_rows(EamArgs<S> a, int ngroups)
+__global__ __launch_bounds__(W * TPB * 64) LK_EIGHT_WAVES void k_eam_density_rows(EamArgs<S> a, int ngroups)
 {
   __shared__ LdsEntry<S> lds[kDensLds];
   __shared__ S part[TPB][W][kWave];

@@ -110,6 +110,7 @@ struct Handle {
   int *d_inc_part = nullptr;    // [chunks] chunk offsets
   uint32_t *d_inc_tmp = nullptr;  // [2 max_edges] (edge << 1 | side), unsorted
   int *d_inc = nullptr;         // [2 max_edges] other atom | side << 31, ascending edge order
+  int *d_inc_len = nullptr;     // [max_atoms + 1] entries of each atom's list (after folding)
   void *d_rho_part = nullptr;   // [max_atoms] per-row density before the ghost fold
   void *d_epair = nullptr;      // [max_atoms] per-row pair energy
   const double *x_last = nullptr;  // engine positions of the last pack (f.r virial)
@@ -138,11 +139,12 @@ struct Handle {
     long epoch = -2;
     const int *ilist = nullptr, *neighbors = nullptr;
     long stride = 0;
-    int rows = 0, maxneighs = 0, half_filter = 0;
+    int rows = 0, maxneighs = 0, half_filter = 0, fold = 0;
     bool operator==(const IncKey &o) const
     {
       return epoch == o.epoch && ilist == o.ilist && neighbors == o.neighbors && stride == o.stride &&
-             rows == o.rows && maxneighs == o.maxneighs && half_filter == o.half_filter;
+             rows == o.rows && maxneighs == o.maxneighs && half_filter == o.half_filter &&
+             fold == o.fold;
     }
   } inc_key;
 

@@ -73,7 +73,7 @@ static int step_pack_grid(int ngroups, int num_cus)
 }
 
 template <typename S, bool EAM, bool MATRIX>
-__global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves_per_eu(8)))
+__global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves_per_eu(8))) LK_EIGHT_WAVES
 void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
 {
   constexpr int W = kStepW, TPB = kStepTPB;

@@ -48,6 +48,7 @@ struct IncArgs {
   int *part;  // [chunks] exclusive chunk offsets
   uint32_t *tmp;
   int *inc;
+  int *len;   // [nrows + 1] entries of each atom's list
 };
 
 __device__ __forceinline__ long live_edges(const StepResult *r, int max_edges)
@@ -192,6 +193,7 @@ __global__ __launch_bounds__(256) void k_inc_sort(IncArgs a, int nsort)
   if (atom >= nsort) return;  // whole wave
   const int b = inc_off(a.loc, a.part, atom);
   const int L = inc_off(a.loc, a.part, atom + 1) - b;
+  if (lane == 0) a.len[atom] = L;
   for (int c0 = 0; c0 < L; c0 += kWave) {
     const bool mine = c0 + lane < L;
     const uint32_t v = mine ? a.tmp[b + c0 + lane] : 0xFFFFFFFFu;
@@ -238,6 +240,8 @@ struct ListArgs {
   uint32_t *tmp;
   int *inc;
   uint32_t *inc_bit;
+  int *len;
+  int fold;  // plain scheme: fold in-entries into the reverse out-entry (below)
 };
 
 // The row atom of list row ii and its slot count, or -1 when the row packs nothing.
@@ -310,9 +314,53 @@ __global__ __launch_bounds__(256) void k_inc_list_fill(ListArgs L)
   }
 }
 
+// Plain scheme only, one wave per atom, between fill and sort. An in-entry (row i names atom a)
+// whose reverse slot is one of a's out-entries (a's row names i) gives a the same pair force:
+// the two slots pass the pack's distance filter together (r^2 is the same sum of the negated
+// differences), and a's plain-scheme share of edge i -> a, -g = coef (x_i - x_a), equals that of
+// a -> i (coef depends on r only). Such an in-entry is dropped (its key set to all ones, which
+// the sort leaves out) and the out-entry marked (bit 30), and the sweeps weigh the out-entry by
+// the ends whose rows count. Each owned pair is then evaluated once per end instead of twice.
+constexpr uint32_t kIncPaired = 1u << 30;
+constexpr uint32_t kIncAtom = 0x3FFFFFFFu;
+
+__global__ __launch_bounds__(256) void k_inc_list_fold(ListArgs L, int nsort)
+{
+  const int atom = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (atom >= nsort) return;  // whole wave
+  const int b0 = inc_off(L.loc, L.part, atom);
+  const int out = L.deg[atom];
+  const int b = b0 + out;
+  const int len = inc_off(L.loc, L.part, atom + 1) - b;
+  if (out == 0 || len == 0) return;
+  for (int c0 = 0; c0 < len; c0 += kWave) {
+    const bool mine = c0 + lane < len;
+    int row_atom = -1;
+    if (mine) {
+      const uint32_t f = L.tmp[b + c0 + lane] >> 1;
+      row_atom = L.ilist[static_cast<int>(f % static_cast<uint32_t>(L.rows))];
+    }
+    int hit = -1;
+    for (int c1 = 0; c1 < out; c1 += kWave) {
+      const int w = c1 + lane < out ? static_cast<int>(L.inc[b0 + c1 + lane] & kIncAtom) : -1;
+      const int n = min(kWave, out - c1);
+      for (int m = 0; m < n; ++m) {
+        const int wm = __builtin_amdgcn_readlane(w, m);
+        if (hit < 0 && wm == row_atom) hit = c1 + m;
+      }
+    }
+    if (hit >= 0) {
+      L.inc[b0 + hit] = static_cast<int>(static_cast<uint32_t>(row_atom) | kIncPaired);
+      L.tmp[b + c0 + lane] = 0xFFFFFFFFu;
+    }
+  }
+}
+
 // One wave per atom: rank sort of the in-part by slot key (keys are distinct), so its store
 // order is ascending f whatever order the fill left; then the other atom (side bit set) and the
-// slot's validity-bit address.
+// slot's validity-bit address. Entries the fold dropped (key all ones) are left out; the list's
+// length goes to len.
 __global__ __launch_bounds__(256) void k_inc_list_sort(ListArgs L, int nsort)
 {
   const int atom = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
@@ -320,9 +368,17 @@ __global__ __launch_bounds__(256) void k_inc_list_sort(ListArgs L, int nsort)
   if (atom >= nsort) return;  // whole wave
   const int b0 = inc_off(L.loc, L.part, atom);
   const int out = L.deg[atom];
-  if (lane == 0) L.deg[atom] = 0;  // read by the whole wave above; zero again between builds
   const int b = b0 + out;
   const int len = inc_off(L.loc, L.part, atom + 1) - b;
+  int kept = 0;  // in-entries the fold left (all of them without folding)
+  for (int c0 = 0; c0 < len; c0 += kWave) {
+    const uint32_t v = c0 + lane < len ? L.tmp[b + c0 + lane] : 0xFFFFFFFFu;
+    kept += __popcll(wave_ballot(v != 0xFFFFFFFFu));
+  }
+  if (lane == 0) {
+    L.deg[atom] = 0;  // read by the whole wave above; zero again between builds
+    L.len[atom] = out + kept;
+  }
   for (int c0 = 0; c0 < len; c0 += kWave) {
     const bool mine = c0 + lane < len;
     const uint32_t v = mine ? L.tmp[b + c0 + lane] : 0xFFFFFFFFu;
@@ -337,7 +393,7 @@ __global__ __launch_bounds__(256) void k_inc_list_sort(ListArgs L, int nsort)
         rank += wm < v ? 1 : 0;
       }
     }
-    if (mine) {
+    if (mine && v != 0xFFFFFFFFu) {
       const uint32_t f = v >> 1;
       const int ii = static_cast<int>(f % static_cast<uint32_t>(L.rows));
       const int jj = static_cast<int>(f / static_cast<uint32_t>(L.rows));
@@ -361,6 +417,7 @@ struct TwoSided {
   const int *loc;
   const int *part;
   const int *inc;
+  const int *len;  // entries of each atom's list when the build folded pairs, else null
   int nall;
   int nlocal;
   int nadd;             // rows that take the force add: nall with newton on, else nlocal
@@ -375,6 +432,12 @@ struct TwoSided {
   const int *ghost_flag;    // 1 when a packed edge starts on a ghost row (the pack's flag)
   FusedPack pack;           // a fused pack of this step: tail reset and counts (else unused)
 };
+
+// Entries of atom a's list starting at b: all of its range, less the in-entries a fold dropped.
+__device__ __forceinline__ int inc_len(const TwoSided &t, int a, int b)
+{
+  return t.len ? t.len[a] : inc_off(t.loc, t.part, a + 1) - b;
+}
 
 // Whether the pack kept an entry's list slot this step (lists built from packed edges: always),
 // split in two so the sweeps can put each load in its round trip: the entry's bit address goes
@@ -474,13 +537,13 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
       const Atom4<S> xa = m.atoms[a];
       const int za = clamp_species(static_cast<int>(xa.w), m.n_el);
       const int b = inc_off(t.loc, t.part, a);
-      const int L = inc_off(t.loc, t.part, a + 1) - b;
+      const int L = HALF ? inc_off(t.loc, t.part, a + 1) - b : inc_len(t, a, b);  // half: no folds
       for (int k = gl; k < L; k += kGroup) {
         const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
         const uint32_t ba = slot_bit_address(t, b + k);
         const bool in = (v >> 31) != 0;
         if (!HALF && in) continue;  // plain: density and pair energy stay on the sender
-        const int o = static_cast<int>(v & 0x7FFFFFFFu);
+        const int o = static_cast<int>(v & kIncAtom);
         // The record gather goes out with the validity word's, not after it: two memory round
         // trips per entry instead of three (a dropped slot's record is simply not used).
         const Atom4<S> xo = m.atoms[o];
@@ -621,15 +684,18 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
       const int za = clamp_species(static_cast<int>(xa.w), m.n_el);
       const S fpa = m.fp[a];
       const int b = inc_off(t.loc, t.part, a);
-      const int L = inc_off(t.loc, t.part, a + 1) - b;
+      const int L = HALF ? inc_off(t.loc, t.part, a + 1) - b : inc_len(t, a, b);  // half: no folds
       IncCursor<BITS> cur(t, b, L, gl);
       for (int k = gl; k < L; k += kGroup) {
         const uint32_t v = cur.v, ba = cur.ba;
         const bool in = (v >> 31) != 0;
-        const int o = static_cast<int>(v & 0x7FFFFFFFu);
-        const bool skip = !HALF && (in ? o : a) >= erows;  // uncounted senders: no gradient
+        const int o = static_cast<int>(v & kIncAtom);
+        // plain: an uncounted sender gives no gradient; a folded pair counts each counted end
+        const bool paired = !HALF && (v & kIncPaired) != 0;
+        const bool ca = a < erows, co = o < erows;
+        const bool skip = !HALF && (paired ? !(ca || co) : !(in ? co : ca));
         const Atom4<S> xo = m.atoms[skip ? a : o];
-        const S fpo = m.fp[(HALF || in) && !skip ? o : a];
+        const S fpo = m.fp[(HALF || in || paired) && !skip ? o : a];
         const uint32_t word = slot_word_of<BITS>(t, ba);
         cur.advance(t, k);
         if (skip || !word_has(word, ba)) continue;
@@ -655,6 +721,12 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSi
           const S fpr = in ? fpa : fpo;
           const S rho_s_p = inside ? cslope_t(rcoef(win, m, L2.node, zs), L2.t) * m.inv_dr : S(0);
           coef = (fps * rho_r_p + fpr * rho_s_p + phip) * rinv;
+        } else if (paired) {
+          // both directed edges: a -> o on a's counted row, o -> a on o's
+          const S rho_a_p = inside ? cslope_t(rcoef(win, m, L2.node, za), L2.t) * m.inv_dr : S(0);
+          const S ga = ca ? fpa * rho_r_p + S(0.5) * phip : S(0);
+          const S go = co ? fpo * rho_a_p + S(0.5) * phip : S(0);
+          coef = (ga + go) * rinv;
         } else {
           coef = (fps * rho_r_p + S(0.5) * phip) * rinv;
         }
@@ -699,7 +771,7 @@ struct LjModel {
 // LJ 12-6 plain (examples/export_model.py:16-50): e per edge on the sender row, g = 2 de/d(r^2) d
 // (times edge_energy_scale) to the sender and minus it to the receiver.
 template <typename S, bool VIRIAL>
-__global__ __launch_bounds__(kRowBlock) void k_lj_inc(LjModel<S> m, TwoSided t)
+__global__ __launch_bounds__(kRowBlock) LK_EIGHT_WAVES void k_lj_inc(LjModel<S> m, TwoSided t)
 {
   __shared__ double vt[6][kRowAtoms];
   __shared__ double et[kRowAtoms];
@@ -714,13 +786,17 @@ __global__ __launch_bounds__(kRowBlock) void k_lj_inc(LjModel<S> m, TwoSided t)
     if (a < t.nall) {
       const Atom4<S> xa = m.atoms[a];
       const int b = inc_off(t.loc, t.part, a);
-      const int L = inc_off(t.loc, t.part, a + 1) - b;
+      const int L = inc_len(t, a, b);
       for (int k = gl; k < L; k += kGroup) {
         const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
         const uint32_t ba = slot_bit_address(t, b + k);
         const bool in = (v >> 31) != 0;
-        const int o = static_cast<int>(v & 0x7FFFFFFFu);
-        if ((in ? o : a) >= erows) continue;
+        const int o = static_cast<int>(v & kIncAtom);
+        // counted ends of the entry: its sender's row, or both rows of a folded pair (the pair
+        // force on a is the same from either directed edge)
+        const int co = o < erows ? 1 : 0;
+        const int w = (in ? 0 : (a < erows ? 1 : 0)) + ((in || (v & kIncPaired)) ? co : 0);
+        if (w == 0) continue;
         const Atom4<S> xo = m.atoms[o];  // issued with the validity word's gather
         if (!word_has(slot_word(t, ba), ba)) continue;
         S dx, dy, dz;
@@ -730,7 +806,7 @@ __global__ __launch_bounds__(kRowBlock) void k_lj_inc(LjModel<S> m, TwoSided t)
         const S inv_r6 = inv_r2 * inv_r2 * inv_r2;
         if (!in) en += m.edge_scale * (m.four_eps * (inv_r6 * inv_r6 - inv_r6));
         const S dedr2 = -m.four_eps * (S(6) * inv_r6 * inv_r6 - S(3) * inv_r6) / r2;
-        const S coef = m.edge_scale * S(2) * dedr2;
+        const S coef = static_cast<S>(w) * (m.edge_scale * S(2) * dedr2);
         fx += coef * dx;
         fy += coef * dy;
         fz += coef * dz;
@@ -780,6 +856,7 @@ static hipError_t build_incidence(Handle &h, hipStream_t s, int nall)
   ia.part = h.d_inc_part;
   ia.tmp = h.d_inc_tmp;
   ia.inc = h.d_inc;
+  ia.len = h.d_inc_len;
   const int egrid = grid_for(h, h.contract.max_edges, 256, 16);
   {
     StageTimer timer(h, s, "inc_count");
@@ -809,7 +886,7 @@ static hipError_t build_incidence(Handle &h, hipStream_t s, int nall)
   return hipGetLastError();
 }
 
-static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall)
+static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall, bool fold)
 {
   ListArgs L;
   L.ilist = h.list_ilist;
@@ -826,6 +903,8 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall)
   L.part = h.d_inc_part;
   L.tmp = h.d_inc_tmp;
   L.inc = h.d_inc;
+  L.len = h.d_inc_len;
+  L.fold = fold ? 1 : 0;
   L.inc_bit = h.d_inc_bit;
   const long slots = static_cast<long>(L.rows) * L.maxneighs;
   const int row_blocks = (L.rows + 255) / 256;
@@ -851,6 +930,8 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall)
   }
   if (nall > 0) {
     StageTimer timer(h, s, "inc_sort");
+    if (L.fold)
+      hipLaunchKernelGGL(k_inc_list_fold, dim3((nall + 3) / 4), dim3(256), 0, s, L, nall);
     hipLaunchKernelGGL(k_inc_list_sort, dim3((nall + 3) / 4), dim3(256), 0, s, L, nall);
   }
   return hipGetLastError();
@@ -862,6 +943,7 @@ static TwoSided two_sided_args(Handle &h, int nlocal, int nghost, const double *
   t.loc = h.d_inc_loc;
   t.part = h.d_inc_part;
   t.inc = h.d_inc;
+  t.len = h.inc_key.fold ? h.d_inc_len : nullptr;  // set by the list build that folded
   t.nall = nlocal + nghost;
   t.nlocal = nlocal;
   t.nadd = h.contract.newton_pair ? t.nall : nlocal;
@@ -1278,8 +1360,9 @@ hipError_t launch_edge_force(Handle &h, hipStream_t s, int nlocal, int nghost, i
     key.rows = h.list_rows;
     key.maxneighs = h.list_maxneighs;
     key.half_filter = h.list_half_filter;
+    key.fold = 0;  // the edge-force sweeps walk whole lists
     if (h.list_epoch < 0 || !(key == h.inc_key)) {
-      e = build_incidence_from_list(h, s, nlocal + nghost);
+      e = build_incidence_from_list(h, s, nlocal + nghost, false);
       h.inc_key = key;
     }
   } else {
@@ -1306,8 +1389,9 @@ hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, in
     key.rows = h.list_rows;
     key.maxneighs = h.list_maxneighs;
     key.half_filter = h.list_half_filter;
+    key.fold = h.accum == LK_ACCUM_PLAIN ? 1 : 0;
     if (h.list_epoch < 0 || !(key == h.inc_key)) {
-      e = build_incidence_from_list(h, s, nlocal + nghost);
+      e = build_incidence_from_list(h, s, nlocal + nghost, key.fold != 0);
       h.inc_key = key;
     }
   } else {
