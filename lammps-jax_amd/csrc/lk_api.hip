@@ -101,6 +101,11 @@ int ensure_incidence(Handle &h, long entries = 0)
     if ((e = hipMemset(h.d_deg, 0, sizeof(int) * (A + 1))) != hipSuccess) return hip_fail(h, e, "hipMemset(incidence counts)");
   }
   const long need = entries > 2L * h.contract.max_edges ? entries : 2L * h.contract.max_edges;
+  // an incidence entry keeps the other atom in 30 bits (side and pair flags above it)
+  if (h.contract.max_atoms > (1 << 30))
+    return fail(h, LK_ERR_CAPACITY,
+                "LAMMPS-JAX atom capacity too large for two-sided accumulation (at most 2^30 "
+                "atoms)");
   if (need > static_cast<long>(INT_MAX))
     return fail(h, LK_ERR_CAPACITY,
                 "LAMMPS-JAX capacity too large for two-sided accumulation (incidence entries must "
