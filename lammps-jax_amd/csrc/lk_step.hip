@@ -255,46 +255,70 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
       const int per = (kmax + W - 1) / W;
       const int k0 = min(wave * per, kmax);
       const int k1 = min(k0 + per, kmax);
-      long cursor = wave_sum(min(c, k0));
-      int wd = 0;
-      uint32_t word = 0;
-      if (k0 < c) {
-        word = lds_bits ? sbits[sub][0][lane] : p.bits[ii];
-        int skip = k0;
-        while (skip > 0) {
-          const int pc = __popc(word);
-          if (pc <= skip) {  // the k0-th entry lies in a later word
-            skip -= pc;
-            ++wd;
-            word = lds_bits ? sbits[sub][wd][lane] : p.bits[static_cast<long>(wd) * p.pitch + ii];
-          } else {
-            for (; skip > 0; --skip) word &= word - 1u;
-          }
-        }
-      }
-      for (int k = k0; k < k1; ++k) {
-        const bool active = k < c;
-        const uint64_t M = wave_ballot(active);
-        if (active) {
-          while (word == 0) {
-            ++wd;
-            word = lds_bits ? sbits[sub][wd][lane] : p.bits[static_cast<long>(wd) * p.pitch + ii];
-          }
-          const int b = __builtin_ctz(word);
-          word &= word - 1u;
-          const int jj = wd * 32 + b;
-          const int j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
-          const long e = base + cursor + lanes_below(M);
-          if (e < p.max_edges) {  // past the capacity the count still reports the demand
-            p.receivers[e] = j;
-            if constexpr (!MATRIX) {
-              p.senders[e] = i;
-              p.mask[e] = 1;
+      const long cursor0 = wave_sum(min(c, k0));
+      // Writes ordinals [k0, k1), B at a time: the slot positions of a batch come from the
+      // validity words alone (read(wd): word wd of this lane's row), so its list re-reads are
+      // all in flight before its stores. The words come from LDS for rows of up to 256 slots
+      // (batches of 4) and from memory past that (one ordinal at a time: a word loaded inside
+      // the batch would make every re-read wait for it).
+      auto write_ordinals = [&](auto read, auto batch) {
+        constexpr int B = decltype(batch)::value;
+        long cursor = cursor0;
+        int wd = 0;
+        uint32_t word = 0;
+        if (k0 < c) {
+          word = read(0);
+          int skip = k0;
+          while (skip > 0) {
+            const int pc = __popc(word);
+            if (pc <= skip) {  // the k0-th entry lies in a later word
+              skip -= pc;
+              word = read(++wd);
+            } else {
+              for (; skip > 0; --skip) word &= word - 1u;
             }
           }
         }
-        cursor += __popcll(M);
-      }
+        for (int k = k0; k < k1; k += B) {
+          int jv[B];
+          long ev[B];
+          bool act[B];
+#pragma unroll
+          for (int q = 0; q < B; ++q) {
+            const bool active = k + q < k1 && k + q < c;
+            const uint64_t M = wave_ballot(active);
+            int jj = 0;
+            if (active) {
+              while (word == 0) word = read(++wd);
+              jj = wd * 32 + __builtin_ctz(word);
+              word &= word - 1u;
+            }
+            act[q] = active;
+            ev[q] = base + cursor + lanes_below(M);
+            cursor += __popcll(M);
+            jv[q] = active ? p.neighbors[static_cast<long>(jj) * p.stride + i] : 0;
+          }
+#pragma unroll
+          for (int q = 0; q < B; ++q) {
+            // the empty asm keeps the neighbour mask here, after the batch's loads have all gone
+            // out (folded into each load's branch it would wait for each load in turn)
+            int jr = jv[q];
+            asm volatile("" : "+v"(jr));
+            if (act[q] && ev[q] < p.max_edges) {  // past the capacity the count reports the demand
+              p.receivers[ev[q]] = jr & kNeighMask;
+              if constexpr (!MATRIX) {
+                p.senders[ev[q]] = i;
+                p.mask[ev[q]] = 1;
+              }
+            }
+          }
+        }
+      };
+      if (lds_bits)
+        write_ordinals([&](int w) { return sbits[sub][w][lane]; }, std::integral_constant<int, 4>{});
+      else
+        write_ordinals([&](int w) { return p.bits[static_cast<long>(w) * p.pitch + ii]; },
+                       std::integral_constant<int, 1>{});
     }
     __syncthreads();
   }
