@@ -77,6 +77,10 @@ __global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves
 void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
 {
   constexpr int W = kStepW, TPB = kStepTPB;
+  // List entries one slot ahead in the pack-only kernels (C4 pack 369 -> 362 us, C5 230 -> 223);
+  // with the density in the loop it measured slower (C3 94 -> 100), so there each slot loads its
+  // entry first.
+  constexpr bool kPrefetch = !EAM;
   __shared__ LdsEntry<S> lds[EAM ? kStepLds : 1];
   __shared__ int cpart[TPB][W][kWave];
   __shared__ S rpart[TPB][W][kWave];
@@ -112,29 +116,50 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
     const bool lds_bits = nwords <= kStepMaxWords;
     int cnt = 0;
     S rho = S(0);
-    // One list slot of this lane's row: the filter chain, and the density of a kept pair.
-    auto visit = [&](int jj) -> bool {
-      if (jj >= nn) return false;
-      const int j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
-      if (j >= p.max_atoms) return false;
+    // The list entry of slot jj of this lane's row; past the row it reads element 0 (which
+    // exists: the loops below only run when some row of the wave has a slot) and is unused.
+    // The load is unconditional, so the compiler can count it exactly and wait for an earlier
+    // load without waiting for this one.
+    auto slot_entry = [&](int jj) -> int {
+      return p.neighbors[jj < nn ? static_cast<long>(jj) * p.stride + i : 0L];
+    };
+    // One list slot of this lane's row (entry: its list entry, loaded one slot ahead): the filter
+    // chain, and the density of a kept pair. next() loads the following slot's entry; it is
+    // called once the neighbour's gather has gone out, so the entry's load overlaps this slot's
+    // gather and arithmetic instead of heading the next slot's chain.
+    auto visit = [&](int jj, int entry, auto &&next) -> bool {
+      asm volatile("" : "+v"(entry));
+      const int j = entry & kNeighMask;
+      const bool ok = jj < nn && j < p.max_atoms;
       double rsq;
-      double xj0, xj1, xj2;
+      double xj0 = 0.0, xj1 = 0.0, xj2 = 0.0;
       int zj = 0;
       if constexpr (sizeof(S) == 8) {
         // float64 records hold the engine's x exactly: one 32-byte gather (two 16-byte loads)
-        // brings x and species. The empty asm takes the species where it arrives, so the
-        // compiler cannot defer it into an 8-byte gather of its own behind the filter.
-        const Atom4<double> rj = reinterpret_cast<const Atom4<double> *>(a.atoms)[j];
-        asm volatile("" ::"v"(rj.w));
+        // brings x and species. The empty asm takes the species before the filter, so the
+        // compiler cannot defer it into an 8-byte gather of its own behind the filter; it comes
+        // after next(), so the next entry's load goes out first.
+        Atom4<double> rj = {0.0, 0.0, 0.0, 0.0};
+        if (ok) {
+          rj = reinterpret_cast<const Atom4<double> *>(a.atoms)[j];
+          if constexpr (!kPrefetch) asm volatile("" ::"v"(rj.w));
+        }
+        next();
+        if constexpr (kPrefetch) asm volatile("" ::"v"(rj.w));
+        if (!ok) return false;
         xj0 = rj.x;
         xj1 = rj.y;
         xj2 = rj.z;
         zj = static_cast<int>(rj.w);
       } else {
-        xj0 = p.x[3L * j + 0];
-        xj1 = p.x[3L * j + 1];
-        xj2 = p.x[3L * j + 2];
-        if constexpr (EAM) zj = p.type[j] - 1;
+        if (ok) {
+          xj0 = p.x[3L * j + 0];
+          xj1 = p.x[3L * j + 1];
+          xj2 = p.x[3L * j + 2];
+          if constexpr (EAM) zj = p.type[j] - 1;
+        }
+        next();
+        if (!ok) return false;
       }
       {
 #pragma clang fp contract(off)
@@ -179,10 +204,15 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
     if (strided) {
       for (int w = 0; w < nwords; ++w) {
         uint32_t part = 0;
+        int entry = kPrefetch ? slot_entry(w * 32 + wave) : 0;
         for (int k = wave; k < 32; k += W) {
           const int jj = w * 32 + k;
           if (jj >= nn_max) break;
-          if (visit(jj)) part |= 1u << k;
+          const int cur = kPrefetch ? entry : slot_entry(jj);
+          if (visit(jj, cur, [&] {
+                if constexpr (kPrefetch) entry = slot_entry(jj + W);
+              }))
+            part |= 1u << k;
         }
         if (part) atomicOr(&sbits[sub][w][lane], part);
       }
@@ -191,8 +221,14 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
         uint32_t word = 0;
         const int jj0 = w * 32;
         const int jj1 = min(jj0 + 32, nn_max);
-        for (int jj = jj0; jj < jj1; ++jj)
-          if (visit(jj)) word |= 1u << (jj & 31);
+        int entry = kPrefetch ? slot_entry(jj0) : 0;
+        for (int jj = jj0; jj < jj1; ++jj) {
+          const int cur = kPrefetch ? entry : slot_entry(jj);
+          if (visit(jj, cur, [&] {
+                if constexpr (kPrefetch) entry = slot_entry(jj + 1);
+              }))
+            word |= 1u << (jj & 31);
+        }
         if (row) p.bits[static_cast<long>(w) * p.pitch + ii] = word;
         if (lds_bits) sbits[sub][w][lane] = word;
       }
