@@ -482,7 +482,8 @@ __device__ __forceinline__ uint32_t slot_word_of(const TwoSided &t, uint32_t ba)
 // next entry's loads go out after this entry's gathers, so waiting for the gathers never waits
 // for them. A skipped entry gathers its own row's record instead (cached), so no branch surrounds
 // a load. (The density and LJ sweeps, with less arithmetic per entry to cover the latency,
-// measured faster without it.)
+// measured faster without it, also at eight waves per SIMD: C4 density 404 -> 464 us with it,
+// C5 LJ 181 -> 183 us.)
 template <bool BITS>
 struct IncCursor {
   uint32_t v = 0, ba = 0;
