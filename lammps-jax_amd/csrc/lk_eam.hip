@@ -172,22 +172,38 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
           const Locator<S> L = locate_mul(rr, a.inv_dr, a.nr);
           const int zj = clamp_species(static_cast<int>(r.at.w), a.n_el);
           const int tp = a.n_el + pair_row(zi, zj);
-          Coef<S> cj, ci, cp;
-          if (wave_ballot(L.node < win.lo) == 0) {  // every active lane reads the LDS window
-            cj = rcoef_lds(win, L.node, zj);
-            ci = rcoef_lds(win, L.node, zi);
-            cp = rcoef_lds(win, L.node, tp);
+          S sj, si, z2, z2s;  // slopes in t of rho_j, rho_i and z2r, and z2r itself
+          if (sizeof(S) == 8 && wave_ballot(L.node < win.lo) == 0) {
+            // every active lane reads the LDS window: float64 in the Hermite basis
+            if constexpr (sizeof(S) == 8) {
+              const HermBasis hb = herm_basis(L.t);
+              sj = herm_slope_t(herm_lds(win, L.node, zj), hb);
+              si = herm_slope_t(herm_lds(win, L.node, zi), hb);
+              const Herm hp = herm_lds(win, L.node, tp);
+              z2 = herm_value(hp, hb);
+              z2s = herm_slope_t(hp, hb);
+            }
           } else {
-            cj = rcoef(win, a, L.node, zj);
-            ci = rcoef(win, a, L.node, zi);
-            cp = rcoef(win, a, L.node, tp);
+            Coef<S> cj, ci, cp;
+            if (wave_ballot(L.node < win.lo) == 0) {
+              cj = rcoef_lds(win, L.node, zj);
+              ci = rcoef_lds(win, L.node, zi);
+              cp = rcoef_lds(win, L.node, tp);
+            } else {
+              cj = rcoef(win, a, L.node, zj);
+              ci = rcoef(win, a, L.node, zi);
+              cp = rcoef(win, a, L.node, tp);
+            }
+            sj = cslope_t(cj, L.t);
+            si = cslope_t(ci, L.t);
+            z2 = cvalue(cp, L.t);
+            z2s = cslope_t(cp, L.t);
           }
           // Past the table the non-extrapolated lookups saturate: autodiff slope 0 (eam.py:150).
           const bool inside = !(L.t_raw > S(1));
-          const S rhojp = inside ? cslope_t(cj, L.t) * a.inv_dr : S(0);
-          const S rhoip = inside ? cslope_t(ci, L.t) * a.inv_dr : S(0);
-          const S z2 = cvalue(cp, L.t);
-          const S z2p = inside ? cslope_t(cp, L.t) * a.inv_dr : S(0);
+          const S rhojp = inside ? sj * a.inv_dr : S(0);
+          const S rhoip = inside ? si * a.inv_dr : S(0);
+          const S z2p = inside ? z2s * a.inv_dr : S(0);
           const S phi = z2 * rinv;
           const S phip = (z2p - phi) * rinv;
           const S psip = fpi * rhojp + r.fp * rhoip + phip;

@@ -139,6 +139,49 @@ __device__ __forceinline__ Coef<S> rcoef_lds(const Window<S> &w, int m, int tab)
   }
 }
 
+// float64 intervals in the Hermite basis: the window holds (f, d) per node, so an interval is
+// f0, s = f1 - f0, d0, d1 and value(t) = f0 + s hs + d0 h0 + d1 h1, slope_t = s gs + d0 g0 + d1 g1
+// with basis functions of t alone, shared by every table an edge reads (the same cubic as
+// c0 + t (c1 + t (c2 + t c3)) of coef_from, fewer operations per table).
+struct HermBasis {
+  double hs, h0, h1, gs, g0, g1;
+};
+
+__device__ __forceinline__ HermBasis herm_basis(double t)
+{
+  const double u = 1.0 - t, tt = t * t;
+  HermBasis b;
+  b.hs = tt * (3.0 - 2.0 * t);
+  b.h0 = t * u * u;
+  b.h1 = -tt * u;
+  b.gs = 6.0 * t * u;
+  b.g0 = u * (1.0 - 3.0 * t);
+  b.g1 = t * (3.0 * t - 2.0);
+  return b;
+}
+
+struct Herm {
+  double f0, s, d0, d1;
+};
+
+// LDS-only (node m in the window).
+__device__ __forceinline__ Herm herm_lds(const Window<double> &w, int m, int tab)
+{
+  const int q = (m - w.lo) * w.T + tab;
+  const double2 e0 = w.lds[q], e1 = w.lds[q + w.T];
+  return Herm{e0.x, e1.x - e0.x, e0.y, e1.y};
+}
+
+__device__ __forceinline__ double herm_value(const Herm &h, const HermBasis &b)
+{
+  return h.f0 + h.s * b.hs + h.d0 * b.h0 + h.d1 * b.h1;
+}
+
+__device__ __forceinline__ double herm_slope_t(const Herm &h, const HermBasis &b)
+{
+  return h.s * b.gs + h.d0 * b.g0 + h.d1 * b.g1;
+}
+
 template <typename S>
 __device__ __forceinline__ S cvalue(const Coef<S> &c, S t)
 {
