@@ -181,34 +181,64 @@ __device__ __forceinline__ void pack_write_tile(const PackArgs &a, int tile,
   int w = 0;
   uint32_t word = cnt > 0 ? a.bits[ii] : 0u;
   long cursor = 0;
-  for (int k = 0;; ++k) {
-    const bool active = k < cnt;
-    const uint64_t M = wave_ballot(active);
-    if (M == 0) break;
-    if (active) {
-      while (word == 0) {
-        ++w;
-        word = a.bits[static_cast<long>(w) * a.pitch + ii];
-      }
-      const int b = __builtin_ctz(word);
-      word &= word - 1u;
-      if ((k % W) == wave) {
-        const int jj = w * 32 + b;
-        const int j = a.neighbors[static_cast<long>(jj) * a.stride + i] & kNeighMask;
-        const long e = base + (cursor + lanes_below(M)) * mult;
-        if (e + mult <= a.max_edges) {
-          senders[e] = i;
-          receivers[e] = j;
-          mask[e] = 1;
-          if (mult == 2) {
-            senders[e + 1] = j;
-            receivers[e + 1] = i;
-            mask[e + 1] = 1;
+  // Every wave pops the bits of every ordinal k (the slot positions need the counts of all of
+  // them) and writes the ordinals with k % W == wave, B of its own at a time: a batch's list
+  // re-reads all go out before its stores, after the batch's bit words have been read.
+  constexpr int B = 4;
+  for (int k0 = 0;; k0 += B * W) {
+    int jv[B];
+    long ev[B];
+    bool act[B];
+    bool more = true;
+#pragma unroll
+    for (int q = 0; q < B; ++q) {
+      act[q] = false;
+      jv[q] = 0;
+      ev[q] = 0;
+#pragma unroll
+      for (int r = 0; r < W; ++r) {
+        const int k = k0 + q * W + r;
+        const bool active = more && k < cnt;
+        const uint64_t M = wave_ballot(active);
+        if (M == 0) more = false;
+        int jj = 0;
+        if (active) {
+          while (word == 0) {
+            ++w;
+            word = a.bits[static_cast<long>(w) * a.pitch + ii];
           }
+          jj = w * 32 + __builtin_ctz(word);
+          word &= word - 1u;
+        }
+        if (r == wave) {
+          act[q] = active;
+          ev[q] = base + (cursor + lanes_below(M)) * mult;
+          jv[q] = jj;
+        }
+        cursor += __popcll(M);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < B; ++q)
+      jv[q] = act[q] ? a.neighbors[static_cast<long>(jv[q]) * a.stride + i] : 0;
+#pragma unroll
+    for (int q = 0; q < B; ++q) {
+      int jr = jv[q];
+      asm volatile("" : "+v"(jr));  // the mask after the batch's loads, not inside each branch
+      const int j = jr & kNeighMask;
+      const long e = ev[q];
+      if (act[q] && e + mult <= a.max_edges) {
+        senders[e] = i;
+        receivers[e] = j;
+        mask[e] = 1;
+        if (mult == 2) {
+          senders[e + 1] = j;
+          receivers[e + 1] = i;
+          mask[e + 1] = 1;
         }
       }
     }
-    cursor += __popcll(M);
+    if (!more) break;
   }
 }
 
