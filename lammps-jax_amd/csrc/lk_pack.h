@@ -34,14 +34,11 @@ struct PackArgs {
 // The filter chain of PackNeighborFunctor::operator() (cpp:84-101) for list entry (i, jj).
 // r^2 is formed without FMA contraction, in double, from the engine's x, so the keep/drop
 // decision at r^2 == rc^2 matches the reference bit for bit.
+// The neighbour's position (xj0, xj1, xj2) is gathered by the caller.
 __device__ __forceinline__ bool keep_entry(const PackArgs &a, int i, double xi0, double xi1,
-                                           double xi2, int j)
+                                           double xi2, int j, double xj0, double xj1, double xj2)
 {
 #pragma clang fp contract(off)
-  if (j >= a.max_atoms) return false;
-  const double xj0 = a.x[3L * j + 0];
-  const double xj1 = a.x[3L * j + 1];
-  const double xj2 = a.x[3L * j + 2];
   const double dx = xi0 - xj0;
   const double dy = xi1 - xj1;
   const double dz = xi2 - xj2;

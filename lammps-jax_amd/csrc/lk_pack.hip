@@ -76,16 +76,30 @@ __global__ __launch_bounds__(W * 64) void k_pack_count(PackArgs a)
   const int nn_max = wave_max_int(nn);
   const int nwords = (nn_max + 31) >> 5;
   int cnt = 0;
+  // The list entry of slot jj (past the row: element 0, which exists since some row of the wave
+  // has a slot when the loop runs, and is unused), loaded one slot ahead behind the previous
+  // neighbour's position gather; unconditional, so waiting for the gather never waits for it.
+  auto slot_entry = [&](int jj) -> int {
+    return a.neighbors[jj < nn ? static_cast<long>(jj) * a.stride + i : 0L];
+  };
   for (int w = wave; w < nwords; w += W) {
     uint32_t word = 0;
     const int jj0 = w * 32;
     const int jj1 = min(jj0 + 32, nn_max);
+    int entry = slot_entry(jj0);
     for (int jj = jj0; jj < jj1; ++jj) {
-      bool keep = false;
-      if (jj < nn) {
-        const int j = a.neighbors[static_cast<long>(jj) * a.stride + i] & kNeighMask;
-        keep = keep_entry(a, i, xi0, xi1, xi2, j);
+      int cur = entry;
+      asm volatile("" : "+v"(cur));
+      const int j = cur & kNeighMask;
+      const bool ok = jj < nn && j < a.max_atoms;
+      double xj0 = 0.0, xj1 = 0.0, xj2 = 0.0;
+      if (ok) {
+        xj0 = a.x[3L * j + 0];
+        xj1 = a.x[3L * j + 1];
+        xj2 = a.x[3L * j + 2];
       }
+      entry = slot_entry(jj + 1);
+      const bool keep = ok && keep_entry(a, i, xi0, xi1, xi2, j, xj0, xj1, xj2);
       if (keep) {
         word |= 1u << (jj & 31);
         ++cnt;
