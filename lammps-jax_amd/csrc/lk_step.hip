@@ -77,10 +77,6 @@ __global__ __launch_bounds__(kStepW * kStepTPB * 64) __attribute__((amdgpu_waves
 void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
 {
   constexpr int W = kStepW, TPB = kStepTPB;
-  // List entries one slot ahead in the pack-only kernels (C4 pack 369 -> 362 us, C5 230 -> 223);
-  // with the density in the loop it measured slower (C3 94 -> 100), so there each slot loads its
-  // entry first.
-  constexpr bool kPrefetch = !EAM;
   __shared__ LdsEntry<S> lds[EAM ? kStepLds : 1];
   __shared__ int cpart[TPB][W][kWave];
   __shared__ S rpart[TPB][W][kWave];
@@ -123,43 +119,29 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
     auto slot_entry = [&](int jj) -> int {
       return p.neighbors[jj < nn ? static_cast<long>(jj) * p.stride + i : 0L];
     };
-    // One list slot of this lane's row (entry: its list entry, loaded one slot ahead): the filter
-    // chain, and the density of a kept pair. next() loads the following slot's entry; it is
-    // called once the neighbour's gather has gone out, so the entry's load overlaps this slot's
-    // gather and arithmetic instead of heading the next slot's chain.
-    auto visit = [&](int jj, int entry, auto &&next) -> bool {
-      asm volatile("" : "+v"(entry));
+    // One list slot of this lane's row (entry: its list entry): the filter chain, and the density
+    // of a kept pair (the model kernels).
+    auto visit = [&](int jj, int entry) -> bool {
       const int j = entry & kNeighMask;
-      const bool ok = jj < nn && j < p.max_atoms;
+      if (!(jj < nn && j < p.max_atoms)) return false;
       double rsq;
-      double xj0 = 0.0, xj1 = 0.0, xj2 = 0.0;
+      double xj0, xj1, xj2;
       int zj = 0;
       if constexpr (sizeof(S) == 8) {
         // float64 records hold the engine's x exactly: one 32-byte gather (two 16-byte loads)
-        // brings x and species. The empty asm takes the species before the filter, so the
-        // compiler cannot defer it into an 8-byte gather of its own behind the filter; it comes
-        // after next(), so the next entry's load goes out first.
-        Atom4<double> rj = {0.0, 0.0, 0.0, 0.0};
-        if (ok) {
-          rj = reinterpret_cast<const Atom4<double> *>(a.atoms)[j];
-          if constexpr (!kPrefetch) asm volatile("" ::"v"(rj.w));
-        }
-        next();
-        if constexpr (kPrefetch) asm volatile("" ::"v"(rj.w));
-        if (!ok) return false;
+        // brings x and species. The empty asm takes the species where it arrives, so the
+        // compiler cannot defer it into an 8-byte gather of its own behind the filter.
+        const Atom4<double> rj = reinterpret_cast<const Atom4<double> *>(a.atoms)[j];
+        asm volatile("" ::"v"(rj.w));
         xj0 = rj.x;
         xj1 = rj.y;
         xj2 = rj.z;
         zj = static_cast<int>(rj.w);
       } else {
-        if (ok) {
-          xj0 = p.x[3L * j + 0];
-          xj1 = p.x[3L * j + 1];
-          xj2 = p.x[3L * j + 2];
-          if constexpr (EAM) zj = p.type[j] - 1;
-        }
-        next();
-        if (!ok) return false;
+        xj0 = p.x[3L * j + 0];
+        xj1 = p.x[3L * j + 1];
+        xj2 = p.x[3L * j + 2];
+        if constexpr (EAM) zj = p.type[j] - 1;
       }
       {
 #pragma clang fp contract(off)
@@ -194,6 +176,54 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
       }
       return true;
     };
+    // Pack-only kernels (no model in the loop, registers to spare) walk the slots jj0,
+    // jj0 + step, ... < jj1 two at a time: both entries are loaded one pair ahead, then both
+    // neighbour positions gathered together, so a pair costs one memory round trip. Every load
+    // is unconditional (slots past the row read element 0 of the list and the record or position
+    // of atom 0, which exist whenever the loop runs, and are unused), so the compiler counts
+    // them exactly and waits for the gathers without waiting for the next pair's entries.
+    auto walk = [&](int jj0, int jj1, int step, auto &&kept) {
+      auto gather = [&](int jj, int entry, double &x0, double &x1, double &x2) {
+        const int j = entry & kNeighMask;
+        const long q = (jj < nn && j < p.max_atoms) ? j : 0;
+        if constexpr (sizeof(S) == 8) {
+          const double2 h = reinterpret_cast<const double2 *>(a.atoms)[2 * q];
+          x0 = h.x;
+          x1 = h.y;
+          x2 = reinterpret_cast<const double *>(a.atoms)[4 * q + 2];
+        } else {
+          x0 = p.x[3 * q + 0];
+          x1 = p.x[3 * q + 1];
+          x2 = p.x[3 * q + 2];
+        }
+      };
+      auto test = [&](int jj, int entry, double x0, double x1, double x2) {
+        const int j = entry & kNeighMask;
+        double rsq;
+        {
+#pragma clang fp contract(off)
+          const double dx = xi0 - x0, dy = xi1 - x1, dz = xi2 - x2;
+          rsq = dx * dx + dy * dy + dz * dz;
+        }
+        // PackNeighborFunctor keeps rsq <= cutsq (cpp:84-101)
+        if (jj < nn && j < p.max_atoms && !(rsq > p.cutsq)) {
+          ++cnt;
+          kept(jj);
+        }
+      };
+      int ea = slot_entry(jj0), eb = slot_entry(jj0 + step);
+      for (int jj = jj0; jj < jj1; jj += 2 * step) {
+        const int jb = jj + step;
+        double a0, a1, a2, b0, b1, b2;
+        gather(jj, ea, a0, a1, a2);
+        gather(jb, eb, b0, b1, b2);
+        const int na = slot_entry(jj + 2 * step), nb = slot_entry(jj + 3 * step);
+        test(jj, ea, a0, a1, a2);
+        if (jb < jj1) test(jb, eb, b0, b1, b2);
+        ea = na;
+        eb = nb;
+      }
+    };
     // Rows of fewer than W words (half lists) would leave waves idle under one word per wave:
     // there each wave takes every W-th slot and ORs its bits into the tile's LDS words, which
     // the first barrier below completes (the global words are stored after it).
@@ -204,15 +234,15 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
     if (strided) {
       for (int w = 0; w < nwords; ++w) {
         uint32_t part = 0;
-        int entry = kPrefetch ? slot_entry(w * 32 + wave) : 0;
-        for (int k = wave; k < 32; k += W) {
-          const int jj = w * 32 + k;
-          if (jj >= nn_max) break;
-          const int cur = kPrefetch ? entry : slot_entry(jj);
-          if (visit(jj, cur, [&] {
-                if constexpr (kPrefetch) entry = slot_entry(jj + W);
-              }))
-            part |= 1u << k;
+        if constexpr (EAM) {
+          for (int k = wave; k < 32; k += W) {
+            const int jj = w * 32 + k;
+            if (jj >= nn_max) break;
+            if (visit(jj, slot_entry(jj))) part |= 1u << k;
+          }
+        } else {
+          walk(w * 32 + wave, min(w * 32 + 32, nn_max), W,
+               [&](int jj) { part |= 1u << (jj & 31); });
         }
         if (part) atomicOr(&sbits[sub][w][lane], part);
       }
@@ -221,13 +251,11 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
         uint32_t word = 0;
         const int jj0 = w * 32;
         const int jj1 = min(jj0 + 32, nn_max);
-        int entry = kPrefetch ? slot_entry(jj0) : 0;
-        for (int jj = jj0; jj < jj1; ++jj) {
-          const int cur = kPrefetch ? entry : slot_entry(jj);
-          if (visit(jj, cur, [&] {
-                if constexpr (kPrefetch) entry = slot_entry(jj + 1);
-              }))
-            word |= 1u << (jj & 31);
+        if constexpr (EAM) {
+          for (int jj = jj0; jj < jj1; ++jj)
+            if (visit(jj, slot_entry(jj))) word |= 1u << (jj & 31);
+        } else {
+          walk(jj0, jj1, 1, [&](int jj) { word |= 1u << (jj & 31); });
         }
         if (row) p.bits[static_cast<long>(w) * p.pitch + ii] = word;
         if (lds_bits) sbits[sub][w][lane] = word;
