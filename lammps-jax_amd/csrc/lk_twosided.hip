@@ -542,19 +542,17 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
       const int za = clamp_species(static_cast<int>(xa.w), m.n_el);
       const int b = inc_off(t.loc, t.part, a);
       const int L = HALF ? inc_off(t.loc, t.part, a + 1) - b : inc_len(t, a, b);  // half: no folds
-      for (int k = gl; k < L; k += kGroup) {
-        const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
-        const uint32_t ba = slot_bit_address(t, b + k);
+      // Two entries per lane at a time (k and k + 16): both entries load together, then both
+      // records with their validity words, so a pair of entries costs two memory round trips.
+      // The record gather goes out with the validity word's, not after it (a dropped slot's
+      // record is simply not used); a skipped or missing entry gathers the row's own record.
+      auto dens = [&](uint32_t v, uint32_t ba, const Atom4<S> &xo, uint32_t word) {
         const bool in = (v >> 31) != 0;
-        if (!HALF && in) continue;  // plain: density and pair energy stay on the sender
-        const int o = static_cast<int>(v & kIncAtom);
-        // The record gather goes out with the validity word's, not after it: two memory round
-        // trips per entry instead of three (a dropped slot's record is simply not used).
-        const Atom4<S> xo = m.atoms[o];
-        if (!word_has(slot_word(t, ba), ba)) continue;
+        if (!HALF && in) return;  // plain: density and pair energy stay on the sender
+        if (!word_has(word, ba)) return;
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
-        if (!(r2 < m.cutsq)) continue;
+        if (!(r2 < m.cutsq)) return;
         const S rinv = rsqrt_nr(r2);
         const S rr = r2 * rinv;
         const Locator<S> L2 = locate_mul(rr, m.inv_dr, m.nr);
@@ -564,6 +562,19 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
           const S phi = cvalue(rcoef(win, m, L2.node, m.n_el + pair_row(za, zo)), L2.t) * rinv;
           ep += HALF ? phi : S(0.5) * phi;  // half: the sender carries both halves
         }
+      };
+      for (int k = gl; k < L; k += 2 * kGroup) {
+        const bool two = k + kGroup < L;
+        const int q1 = b + k, q2 = b + (two ? k + kGroup : k);
+        const uint32_t v1 = static_cast<uint32_t>(t.inc[q1]);
+        const uint32_t v2 = static_cast<uint32_t>(t.inc[q2]);
+        const uint32_t ba1 = slot_bit_address(t, q1), ba2 = slot_bit_address(t, q2);
+        const bool s1 = !HALF && (v1 >> 31) != 0, s2 = !two || (!HALF && (v2 >> 31) != 0);
+        const Atom4<S> x1 = m.atoms[s1 ? a : static_cast<int>(v1 & kIncAtom)];
+        const Atom4<S> x2 = m.atoms[s2 ? a : static_cast<int>(v2 & kIncAtom)];
+        const uint32_t w1 = slot_word(t, ba1), w2 = slot_word(t, ba2);
+        dens(v1, ba1, x1, w1);
+        if (two) dens(v2, ba2, x2, w2);
       }
     }
     rho = group_sum(rho);
@@ -794,7 +805,8 @@ struct LjModel {
 // LJ 12-6 plain (examples/export_model.py:16-50): e per edge on the sender row, g = 2 de/d(r^2) d
 // (times edge_energy_scale) to the sender and minus it to the receiver.
 template <typename S, bool VIRIAL>
-__global__ __launch_bounds__(kRowBlock) LK_EIGHT_WAVES void k_lj_inc(LjModel<S> m, TwoSided t)
+__global__ __launch_bounds__(kRowBlock) __attribute__((amdgpu_waves_per_eu(8))) LK_EIGHT_WAVES
+void k_lj_inc(LjModel<S> m, TwoSided t)
 {
   __shared__ double vt[6][kRowAtoms];
   __shared__ double et[kRowAtoms];
@@ -810,29 +822,42 @@ __global__ __launch_bounds__(kRowBlock) LK_EIGHT_WAVES void k_lj_inc(LjModel<S> 
       const Atom4<S> xa = m.atoms[a];
       const int b = inc_off(t.loc, t.part, a);
       const int L = inc_len(t, a, b);
-      for (int k = gl; k < L; k += kGroup) {
-        const uint32_t v = static_cast<uint32_t>(t.inc[b + k]);
-        const uint32_t ba = slot_bit_address(t, b + k);
+      // counted ends of an entry: its sender's row, or both rows of a folded pair (the pair
+      // force on a is the same from either directed edge)
+      auto ends = [&](uint32_t v) -> int {
         const bool in = (v >> 31) != 0;
-        const int o = static_cast<int>(v & kIncAtom);
-        // counted ends of the entry: its sender's row, or both rows of a folded pair (the pair
-        // force on a is the same from either directed edge)
-        const int co = o < erows ? 1 : 0;
-        const int w = (in ? 0 : (a < erows ? 1 : 0)) + ((in || (v & kIncPaired)) ? co : 0);
-        if (w == 0) continue;
-        const Atom4<S> xo = m.atoms[o];  // issued with the validity word's gather
-        if (!word_has(slot_word(t, ba), ba)) continue;
+        const int co = static_cast<int>(v & kIncAtom) < erows ? 1 : 0;
+        return (in ? 0 : (a < erows ? 1 : 0)) + ((in || (v & kIncPaired)) ? co : 0);
+      };
+      auto pair = [&](uint32_t v, uint32_t ba, int w, const Atom4<S> &xo, uint32_t word) {
+        if (w == 0 || !word_has(word, ba)) return;
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
-        if (!(r2 > tiny && r2 < m.cutsq)) continue;  // export_model.py:22
+        if (!(r2 > tiny && r2 < m.cutsq)) return;  // export_model.py:22
         const S inv_r2 = m.sigsq / r2;
         const S inv_r6 = inv_r2 * inv_r2 * inv_r2;
-        if (!in) en += m.edge_scale * (m.four_eps * (inv_r6 * inv_r6 - inv_r6));
+        if (!(v >> 31)) en += m.edge_scale * (m.four_eps * (inv_r6 * inv_r6 - inv_r6));
         const S dedr2 = -m.four_eps * (S(6) * inv_r6 * inv_r6 - S(3) * inv_r6) / r2;
         const S coef = static_cast<S>(w) * (m.edge_scale * S(2) * dedr2);
         fx += coef * dx;
         fy += coef * dy;
         fz += coef * dz;
+      };
+      // Two entries per lane at a time (k and k + 16), as in the density sweep: both entries,
+      // then both records with their validity words (an uncounted or missing entry gathers the
+      // row's own record).
+      for (int k = gl; k < L; k += 2 * kGroup) {
+        const bool two = k + kGroup < L;
+        const int q1 = b + k, q2 = b + (two ? k + kGroup : k);
+        const uint32_t v1 = static_cast<uint32_t>(t.inc[q1]);
+        const uint32_t v2 = static_cast<uint32_t>(t.inc[q2]);
+        const uint32_t ba1 = slot_bit_address(t, q1), ba2 = slot_bit_address(t, q2);
+        const int w1 = ends(v1), w2 = two ? ends(v2) : 0;
+        const Atom4<S> x1 = m.atoms[w1 ? static_cast<int>(v1 & kIncAtom) : a];
+        const Atom4<S> x2 = m.atoms[w2 ? static_cast<int>(v2 & kIncAtom) : a];
+        const uint32_t wd1 = slot_word(t, ba1), wd2 = slot_word(t, ba2);
+        pair(v1, ba1, w1, x1, wd1);
+        pair(v2, ba2, w2, x2, wd2);
       }
     }
     en = group_sum(en);
