@@ -77,33 +77,40 @@ __global__ __launch_bounds__(W * 64) void k_pack_count(PackArgs a)
   const int nwords = (nn_max + 31) >> 5;
   int cnt = 0;
   // The list entry of slot jj (past the row: element 0, which exists since some row of the wave
-  // has a slot when the loop runs, and is unused), loaded one slot ahead behind the previous
-  // neighbour's position gather; unconditional, so waiting for the gather never waits for it.
+  // has a slot when the loop runs, and is unused). Slots go two at a time: both entries load one
+  // pair ahead, then both positions are gathered together (a slot past the row or the capacity
+  // gathers atom 0's, unused), so a pair costs one memory round trip; every load is
+  // unconditional, so waiting for the gathers never waits for the next pair's entries.
   auto slot_entry = [&](int jj) -> int {
     return a.neighbors[jj < nn ? static_cast<long>(jj) * a.stride + i : 0L];
+  };
+  auto keep_slot = [&](int jj, int entry, const double *xs) -> bool {
+    const int j = entry & kNeighMask;
+    return jj < nn && j < a.max_atoms && keep_entry(a, i, xi0, xi1, xi2, j, xs[0], xs[1], xs[2]);
   };
   for (int w = wave; w < nwords; w += W) {
     uint32_t word = 0;
     const int jj0 = w * 32;
     const int jj1 = min(jj0 + 32, nn_max);
-    int entry = slot_entry(jj0);
-    for (int jj = jj0; jj < jj1; ++jj) {
-      int cur = entry;
-      asm volatile("" : "+v"(cur));
-      const int j = cur & kNeighMask;
-      const bool ok = jj < nn && j < a.max_atoms;
-      double xj0 = 0.0, xj1 = 0.0, xj2 = 0.0;
-      if (ok) {
-        xj0 = a.x[3L * j + 0];
-        xj1 = a.x[3L * j + 1];
-        xj2 = a.x[3L * j + 2];
-      }
-      entry = slot_entry(jj + 1);
-      const bool keep = ok && keep_entry(a, i, xi0, xi1, xi2, j, xj0, xj1, xj2);
-      if (keep) {
+    int ea = slot_entry(jj0), eb = slot_entry(jj0 + 1);
+    for (int jj = jj0; jj < jj1; jj += 2) {
+      double xa[3], xb[3];
+      const int ja = ea & kNeighMask, jb = eb & kNeighMask;
+      const long qa = (jj < nn && ja < a.max_atoms) ? ja : 0;
+      const long qb = (jj + 1 < nn && jb < a.max_atoms) ? jb : 0;
+      for (int c = 0; c < 3; ++c) xa[c] = a.x[3 * qa + c];
+      for (int c = 0; c < 3; ++c) xb[c] = a.x[3 * qb + c];
+      const int na = slot_entry(jj + 2), nb = slot_entry(jj + 3);
+      if (keep_slot(jj, ea, xa)) {
         word |= 1u << (jj & 31);
         ++cnt;
       }
+      if (jj + 1 < jj1 && keep_slot(jj + 1, eb, xb)) {
+        word |= 1u << ((jj + 1) & 31);
+        ++cnt;
+      }
+      ea = na;
+      eb = nb;
     }
     if (row) a.bits[static_cast<long>(w) * a.pitch + ii] = word;
   }
