@@ -700,23 +700,42 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
       const S fpa = m.fp[a];
       const int b = inc_off(t.loc, t.part, a);
       const int L = HALF ? inc_off(t.loc, t.part, a + 1) - b : inc_len(t, a, b);  // half: no folds
-      IncCursor<BITS> cur(t, b, L, gl);
-      for (int k = gl; k < L; k += kGroup) {
-        const uint32_t v = cur.v, ba = cur.ba;
+      // The gathers of an entry: its neighbour's record and F' (the row's own when the entry
+      // is skipped, so no branch surrounds a load) and its validity word.
+      struct Gathered {
+        uint32_t v, ba;
+        bool skip;
+        Atom4<S> xo;
+        S fpo;
+        uint32_t word;
+      };
+      auto gather = [&](uint32_t v, uint32_t ba, bool present) -> Gathered {
+        Gathered e;
+        e.v = v;
+        e.ba = ba;
         const bool in = (v >> 31) != 0;
         const int o = static_cast<int>(v & kIncAtom);
         // plain: an uncounted sender gives no gradient; a folded pair counts each counted end
         const bool paired = !HALF && (v & kIncPaired) != 0;
         const bool ca = a < erows, co = o < erows;
-        const bool skip = !HALF && (paired ? !(ca || co) : !(in ? co : ca));
-        const Atom4<S> xo = m.atoms[skip ? a : o];
-        const S fpo = m.fp[(HALF || in || paired) && !skip ? o : a];
-        const uint32_t word = slot_word_of<BITS>(t, ba);
-        cur.advance(t, k);
-        if (skip || !word_has(word, ba)) continue;
+        e.skip = !present || (!HALF && (paired ? !(ca || co) : !(in ? co : ca)));
+        e.xo = m.atoms[e.skip ? a : o];
+        e.fpo = m.fp[(HALF || in || paired) && !e.skip ? o : a];
+        e.word = slot_word_of<BITS>(t, ba);
+        return e;
+      };
+      auto edge = [&](const Gathered &e) {
+        if (e.skip || !word_has(e.word, e.ba)) return;
+        const uint32_t v = e.v;
+        const Atom4<S> &xo = e.xo;
+        const S fpo = e.fpo;
+        const bool in = (v >> 31) != 0;
+        const int o = static_cast<int>(v & kIncAtom);
+        const bool paired = !HALF && (v & kIncPaired) != 0;
+        const bool ca = a < erows, co = o < erows;
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
-        if (!(r2 < m.cutsq)) continue;
+        if (!(r2 < m.cutsq)) return;
         const S rinv = rsqrt_nr(r2);
         const S rr = r2 * rinv;
         const Locator<S> L2 = locate_mul(rr, m.inv_dr, m.nr);
@@ -749,6 +768,37 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
         fx += coef * dx;
         fy += coef * dy;
         fz += coef * dz;
+      };
+      // float32: entries k and k + 16 of this lane at a time: both gathers go out together,
+      // then the next pair's entries (clamped to the list's last entry, so every load is
+      // unconditional and waiting for the gathers never waits for them), then both edges are
+      // computed (C4 force sweep 750 -> 739 us). float64 takes one entry at a time with the next
+      // in flight (two at a time measured 2% slower there, at 97 VGPRs and four waves per SIMD).
+      if constexpr (sizeof(S) == 8) {
+        IncCursor<BITS> cur(t, b, L, gl);
+        for (int k = gl; k < L; k += kGroup) {
+          const Gathered e = gather(cur.v, cur.ba, true);
+          cur.advance(t, k);
+          edge(e);
+        }
+      } else if (gl < L) {
+        const int last = b + L - 1;
+        uint32_t v1 = static_cast<uint32_t>(t.inc[b + gl]);
+        uint32_t ba1 = slot_bit_address_of<BITS>(t, b + gl);
+        uint32_t v2 = static_cast<uint32_t>(t.inc[min(b + gl + kGroup, last)]);
+        uint32_t ba2 = slot_bit_address_of<BITS>(t, min(b + gl + kGroup, last));
+        for (int k = gl; k < L; k += 2 * kGroup) {
+          const Gathered e1 = gather(v1, ba1, true);
+          const Gathered e2 = gather(v2, ba2, k + kGroup < L);
+          asm volatile("" ::: "memory");  // keep the next entries' loads behind the gathers
+          const int q1 = min(b + k + 2 * kGroup, last), q2 = min(b + k + 3 * kGroup, last);
+          v1 = static_cast<uint32_t>(t.inc[q1]);
+          ba1 = slot_bit_address_of<BITS>(t, q1);
+          v2 = static_cast<uint32_t>(t.inc[q2]);
+          ba2 = slot_bit_address_of<BITS>(t, q2);
+          edge(e1);
+          edge(e2);
+        }
       }
     }
     fx = group_sum(fx);
