@@ -476,14 +476,13 @@ __device__ __forceinline__ uint32_t slot_word_of(const TwoSided &t, uint32_t ba)
   return ~0u;
 }
 
-// The force sweep's walk over its atom's incident entries k = gl, gl + 16, ... with the next
-// entry (and its bit address) in flight while the current one is computed. Per entry the sweep
-// issues, in this order: the neighbour's record and F', the validity word, then advance(): the
-// next entry's loads go out after this entry's gathers, so waiting for the gathers never waits
-// for them. A skipped entry gathers its own row's record instead (cached), so no branch surrounds
-// a load. (The density and LJ sweeps, with less arithmetic per entry to cover the latency,
-// measured faster without it, also at eight waves per SIMD: C4 density 404 -> 464 us with it,
-// C5 LJ 181 -> 183 us.)
+// The fp64 force sweep's walk over its atom's incident entries k = gl, gl + 16, ... with the
+// next entry (and its bit address) in flight while the current one is computed. Per entry the
+// sweep issues, in this order: the neighbour's record and F', the validity word, then advance():
+// the next entry's loads go out after this entry's gathers, so waiting for the gathers never
+// waits for them. A skipped entry gathers its own row's record instead (cached), so no branch
+// surrounds a load. (The density and LJ sweeps measured slower with it, also at eight waves per
+// SIMD: C4 density 404 -> 464 us, C5 LJ 181 -> 183 us; they take two entries at a time instead.)
 template <bool BITS>
 struct IncCursor {
   uint32_t v = 0, ba = 0;
