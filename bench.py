@@ -118,9 +118,20 @@ def cpu_baseline(wl, sysm, lst, max_atoms, max_edges, budget_s: float, max_steps
         "cores": threads,
         "kind": "port",
         "sample": f"{len(times)} full steps of {wl.name} (pack + one-sided EAM E/F/virial + f add), "
-                  f"{per_step * 1e3:.1f} ms/step, OpenMP C++ restatement on {threads} threads, "
-                  f"host {platform.processor() or platform.machine()}",
+                  f"{per_step * 1e3:.1f} ms/step, OpenMP C++ restatement on {threads} threads "
+                  f"of {os.cpu_count()} logical CPUs, 1 process, no MPI, host CPU {cpu_model()}",
     }
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), else the machine type."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def copy_ceiling_gbs(mib: int = 1024, reps: int = 10) -> float:
@@ -263,12 +274,9 @@ def main() -> int:
     wl = systems.make_workload(args.workload)
     sysm = wl.system()
     lst = sysm.build_list(wl.cutoff + wl.skin, kind=wl.list_kind)
-    model = ("eam", wl.tables) if wl.model == "eam" else ("lj", wl.lj)
     nall = sysm.nall
-    max_atoms = ((nall * 21 // 20) + 1023) // 1024 * 1024  # 5% headroom, like an exported bundle
-    pj = PairJax(sysm, model, precision=wl.precision, accumulation=wl.accumulation,
-                 n_hops=wl.n_hops, max_atoms=max_atoms, edges_per_atom=wl.edges_per_atom,
-                 device="cuda:0", layout=args.layout)
+    pj = PairJax.for_workload(wl, sysm, layout=args.layout, device="cuda:0")
+    max_atoms = pj.max_atoms
     setup_s = time.perf_counter() - t_setup
     print(f"[bench] {wl.name}: N={sysm.nlocal} ghosts={sysm.nghost} list entries={lst['entries']} "
           f"max_atoms={max_atoms} max_edges={pj.max_edges} setup {setup_s:.1f}s", file=sys.stderr,

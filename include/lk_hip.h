@@ -225,8 +225,7 @@ int lk_timing_read(lk_handle *h, int index, char *name, int name_len, double *to
  *
  * lk_bundle_contract fills an lk_contract for lk_create from the bundle and the run's newton
  * pair setting, the list kind following PairJaxKokkos::half_list (cpp/pair_jax_kokkos.cpp:
- * 425-431); LK_ERR_UNSUPPORTED (contract still filled) for the neighbor-matrix layout, which
- * this library does not run.
+ * 425-431), for either input layout (sparse edges or the neighbour matrix).
  * lk_bundle_model gives the model for lk_set_eam / lk_set_lj (table pointers stay valid until
  * lk_bundle_free); kind 1 eam/alloy, 2 lj/cut, 0 none (a reference bundle: LK_ERR_UNSUPPORTED);
  * accumulation -1 when the bundle names none.

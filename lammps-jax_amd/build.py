@@ -8,6 +8,7 @@ Both land next to the Python package so a repository snapshot carries them to a 
 
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -38,6 +39,40 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{REPO / 'include'}",
 ]
+
+
+def sources_hash(paths, flags=()) -> str:
+    """SHA-256 over the build inputs (names and bytes) and flags of one library."""
+    h = hashlib.sha256()
+    for f in flags:
+        h.update(f.encode() + b"\0")
+    for p in sorted(Path(q) for q in paths):
+        h.update(p.name.encode() + b"\0")
+        h.update(p.read_bytes())
+    return h.hexdigest()
+
+
+def hip_inputs() -> list[Path]:
+    return (sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + sorted(CSRC.glob("*.cpp"))
+            + [REPO / "include" / "lk_hip.h"])
+
+
+def harness_inputs() -> list[Path]:
+    return [CSRC / "harness" / "lk_harness.cpp"]
+
+
+def _stamp_path(lib: Path) -> Path:
+    return lib.with_name(lib.name + ".srchash")
+
+
+def is_current(lib: Path, inputs, flags=()) -> bool:
+    """The library exists and was built from these exact sources (its .srchash stamp)."""
+    stamp = _stamp_path(lib)
+    return lib.exists() and stamp.exists() and stamp.read_text().strip() == sources_hash(inputs, flags)
+
+
+def write_stamp(lib: Path, inputs, flags=()) -> None:
+    _stamp_path(lib).write_text(sources_hash(inputs, flags) + "\n")
 
 
 def _hipcc() -> str:
@@ -77,17 +112,29 @@ def build_hip() -> Path:
     _run([hipcc, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *map(str, objs), "-lz",
           "-o", str(tmp)])
     tmp.replace(out)
+    write_stamp(out, hip_inputs(), HIPCC_FLAGS)
     return out
+
+
+HARNESS_FLAGS = ["-O3", "-fopenmp", "-fPIC", "-shared", "-std=c++17"]
 
 
 def build_harness() -> Path:
     """Compiles the host-side LAMMPS stand-in with OpenMP."""
     out = PKG / "liblkharness.so"
     tmp = PKG / "liblkharness.so.tmp"
-    _run(["g++", "-O3", "-fopenmp", "-fPIC", "-shared", "-std=c++17",
-          str(CSRC / "harness" / "lk_harness.cpp"), "-o", str(tmp)])
+    _run(["g++", *HARNESS_FLAGS, str(CSRC / "harness" / "lk_harness.cpp"), "-o", str(tmp)])
     tmp.replace(out)
+    write_stamp(out, harness_inputs(), HARNESS_FLAGS)
     return out
+
+
+def hip_current() -> bool:
+    return is_current(PKG / "liblkhip.so", hip_inputs(), HIPCC_FLAGS)
+
+
+def harness_current() -> bool:
+    return is_current(PKG / "liblkharness.so", harness_inputs(), HARNESS_FLAGS)
 
 
 def build_all() -> list[Path]:

@@ -85,12 +85,16 @@ int ensure_bits(Handle &h, int maxneighs)
 // Buffers of the two-sided schemes: per-atom arrays sized from the contract once (first use),
 // incidence entries sized for `entries` (2 * max_edges for lists built from the packed edges,
 // 2 * rows * maxneighs for lists built from the neighbour-list slots); they grow, rarely, outside
-// any captured region.
+// any captured region. Only a first allocation or a growth synchronises the device (the old
+// buffers may still be in use by enqueued work; the cleared counts must be in place before the
+// caller's stream uses them); a step whose buffers suffice returns at once.
 int ensure_incidence(Handle &h, long entries = 0)
 {
   const long A = h.contract.max_atoms;
   hipError_t e;
+  bool fresh = false;
   if (!h.d_deg) {
+    fresh = true;
     const long chunks = (A + 1 + 4095) / 4096;
     if ((e = dalloc(&h.d_deg, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence counts)");
     if ((e = dalloc(&h.d_inc_loc, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence offsets)");
@@ -124,8 +128,10 @@ int ensure_incidence(Handle &h, long entries = 0)
     if ((e = dalloc(&h.d_inc_bit, need)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence bits)");
     h.inc_cap = need;
     h.inc_key = Handle::IncKey{};  // rebuild
+    fresh = true;
   }
-  if ((e = hipDeviceSynchronize()) != hipSuccess) return hip_fail(h, e, "initialising incidence buffers");
+  if (fresh && (e = hipDeviceSynchronize()) != hipSuccess)
+    return hip_fail(h, e, "initialising incidence buffers");
   return LK_OK;
 }
 
@@ -254,7 +260,7 @@ int lk_create(const lk_contract *c, lk_handle **out)
   h.partial_slots = static_cast<int>(tiles);
   if ((e = dalloc(&h.d_result, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(result)");
   if ((e = dalloc(&h.d_done, 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(done)");
-  if ((e = dalloc(&h.d_pack_state, 2)) != hipSuccess) return hip_fail(h, e, "hipMalloc(pack state)");
+  if ((e = dalloc(&h.d_pack_state, lk::kPackStateWords)) != hipSuccess) return hip_fail(h, e, "hipMalloc(pack state)");
   if (matrix) {
     const size_t R = static_cast<size_t>(h.matrix_rows);
     const size_t M = static_cast<size_t>(c->max_neighbors);
@@ -290,7 +296,7 @@ int lk_create(const lk_contract *c, lk_handle **out)
   (void)hipMemset(h.d_partials, 0, 8 * tiles * sizeof(double));
   (void)hipMemset(h.d_result, 0, sizeof(lk::StepResult));
   (void)hipMemset(h.d_done, 0, sizeof(int));
-  (void)hipMemset(h.d_pack_state, 0, 2 * sizeof(int));
+  (void)hipMemset(h.d_pack_state, 0, lk::kPackStateWords * sizeof(int));
   if (int rc = ensure_bits(h, 128)) return rc;
   e = hipDeviceSynchronize();
   if (e != hipSuccess) return hip_fail(h, e, "initialising buffers");
@@ -578,6 +584,8 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
   if (static_cast<long>(nlocal) + nghost > h.contract.max_atoms)
     return fail(h, LK_ERR_CAPACITY, "LAMMPS-JAX atom capacity exceeded");
   if (h.contract.pair_sum) return fail(h, LK_ERR_UNSUPPORTED, "pair-sum bundles carry no EAM/LJ model");
+  // newton pair off reports no pair virial (vflag_fdotr needs newton on; cpp:733-736)
+  if (!h.contract.newton_pair) flags &= ~LK_VIRIAL;
   hipStream_t s = as_stream(stream);
   hipError_t e = hipSuccess;
   if (h.matrix) {
@@ -658,6 +666,7 @@ int lk_pack_compute(lk_handle *w, void *stream, const double *x, const int *type
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
   if (h.model == 0) return fail(h, LK_ERR_STATE, "LAMMPS-JAX runtime is not initialized");
+  if (!h.contract.newton_pair) flags &= ~LK_VIRIAL;  // no pair virial with newton off (cpp:733-736)
   if (h.matrix) {
     // pack_atoms every step; the matrix copy only when the list was rebuilt (cpp:1011-1012)
     int rc = lk_pack_atoms(w, stream, x, type, nall);
@@ -781,8 +790,6 @@ int lk_step_result(lk_handle *w, void *stream, lk_step_info *out)
   }
   h.pending.clear();
   const lk::StepResult &r = *h.h_result;
-  // cpp/pair_jax_kokkos.cpp:1080: the next pack resets the slots this step used
-  h.cached_edge_count = r.edge_count;
   if (out) {
     out->energy = r.energy;
     for (int k = 0; k < 6; ++k) out->virial[k] = r.virial[k];

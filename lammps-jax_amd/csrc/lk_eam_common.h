@@ -31,12 +31,15 @@ __device__ __forceinline__ Coef<double> coef_from(double2 e0, double2 e1)
   return c;
 }
 
+// ResetEdgeTailFunctor of a fused pack: the slots past this pack's count that held the previous
+// pack's edges, [min(demand, max_edges), previous live count), return to the padding.
 __device__ __forceinline__ void fused_tail_reset(const FusedPack &fp)
 {
-  if (!fp.counter) return;
-  const long c = fp.counter[0];
+  if (!fp.state) return;
+  const long c = fp.state[kDemand];
   const long count = c < fp.max_edges ? c : fp.max_edges;
-  for (long e = count + static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < fp.reset_end;
+  const long reset_end = fp.state[kPrevLive];
+  for (long e = count + static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < reset_end;
        e += static_cast<long>(gridDim.x) * blockDim.x) {
     fp.senders[e] = fp.pad;
     fp.receivers[e] = fp.pad;
@@ -275,10 +278,13 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
     result->energy = (flags & LK_ENERGY) ? escale * scratch[0] : 0.0;
     for (int c = 0; c < 6; ++c)
       result->virial[c] = (flags & LK_VIRIAL) ? vscale * scratch[(c + 1) * nt] : 0.0;
-    if (pack.counter) {
-      result->edge_count = pack.counter[0];
-      result->edge_overflow = pack.counter[0] > pack.max_edges ? 1 : 0;
-      result->ghost_sender = pack.counter[1];
+    if (pack.state) {
+      const int demand = pack.state[kDemand];
+      result->edge_count = demand;
+      result->edge_overflow = demand > pack.max_edges ? 1 : 0;
+      result->ghost_sender = pack.state[kGhostFlag];
+      // every block has passed its tail reset (it precedes the done count): the live count moves
+      pack.state[kLive] = demand < pack.max_edges ? demand : pack.max_edges;
     }
     if (mirror) *mirror = *result;  // the host's pinned copy: no separate readback copy
     *done = 0;  // ready for the next launch

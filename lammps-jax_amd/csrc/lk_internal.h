@@ -23,17 +23,28 @@ struct StepResult {
   int pad;
 };
 
-// The part of the fused one-sided pack that the force sweep completes: the tail reset of the
-// slots the previous step used (ResetEdgeTailFunctor, cpp/pair_jax_kokkos.cpp:157-173) and the
-// demand count, overflow and ghost-sender flags of the step result. counter == nullptr: unused.
+// Words of the pack state (int [kPackStateWords] on the device, zero at creation). The slot
+// counts stay on the device from one pack to the next, so a caller may enqueue any number of
+// steps without reading results back and the tail reset still covers every stale slot.
+enum PackState {
+  kDemand = 0,     // edge demand count of the current pack (atomic claims of the fused packs)
+  kGhostFlag = 1,  // 1 when a kept edge starts on a ghost row
+  kLive = 2,       // packed slots that hold live edges: min(demand, max_edges) of the last pack
+  kPrevLive = 3,   // kLive before the current pack: its tail reset clears [count, kPrevLive)
+  kEdgeForceLive = 4,  // edge-force slots holding forces of the last compute
+  kPackStateWords = 5,
+};
+
+// The part of a fused pack that the model sweeps complete: the tail reset of the slots the
+// previous pack used (ResetEdgeTailFunctor, cpp/pair_jax_kokkos.cpp:157-173) and the demand
+// count, overflow and ghost-sender flags of the step result. state == nullptr: unused.
 struct FusedPack {
-  const int *counter = nullptr;  // [0] edge demand count (atomic in the pack), [1] ghost sender
+  int *state = nullptr;  // the pack state words (PackState)
   int *senders = nullptr;
   int *receivers = nullptr;
   unsigned char *mask = nullptr;
   int max_edges = 0;
-  int pad = 0;                   // padding index (max_atoms)
-  long reset_end = 0;            // slots below it held the previous step's edges
+  int pad = 0;           // padding index (max_atoms)
 };
 
 struct Handle {
@@ -67,7 +78,6 @@ struct Handle {
   uint32_t *d_bits = nullptr;   // validity bits, word w of row ii at [w * max_atoms + ii]
   int bits_words = 0;
   int packed_rows = 0;          // list rows of the last pack
-  long cached_edge_count = 0;   // host copy of the previous demand count (cpp:1080)
   int pack_serial = 0;
 
   // per-atom model state
@@ -88,7 +98,7 @@ struct Handle {
   int *d_ghost_list = nullptr;  // [nghost] ghost rows, increasing within each owner
   int ghost_off_cap = 0;
   int *d_done = nullptr;        // block counter of the last-block result reduction
-  int *d_pack_state = nullptr;  // fused one-sided step: [0] edge demand count, [1] ghost sender
+  int *d_pack_state = nullptr;  // pack state words (PackState)
   int ghost_cap = 0;
   int ghost_n = 0;
   int ghost_nlocal = 0;

@@ -22,17 +22,22 @@ namespace lk {
 
 // PackAtomsFunctor (cpp/pair_jax_kokkos.cpp:35-52): positions narrowed to the contract precision,
 // species = type - 1. The record keeps the species beside the position for one-gather lookups.
-// `clear` (optional, two ints) is zeroed for the step that follows: the fused pack's demand
-// counter and ghost-sender flag.
+// `state` (optional, the pack state words) starts the fused pack that follows: the demand counter
+// and the ghost-sender flag are zeroed and the live slot count of the previous pack is kept as
+// the bound of this pack's tail reset.
 template <typename S>
 __global__ __launch_bounds__(256) void k_pack_atoms(const double *__restrict__ x,
                                                      const int *__restrict__ type, int span,
                                                      Atom4<S> *__restrict__ atoms,
                                                      int *__restrict__ species,
-                                                     int *__restrict__ clear)
+                                                     int *__restrict__ state)
 {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (clear && i < 2) clear[i] = 0;
+  if (state && i == 0) {
+    state[kPrevLive] = state[kLive];
+    state[kDemand] = 0;
+    state[kGhostFlag] = 0;
+  }
   if (i >= span) return;
   const int sp = type[i] - 1;
   Atom4<S> a;
@@ -141,7 +146,8 @@ __global__ __launch_bounds__(1024) void k_tile_scan(const int *__restrict__ tile
                                                      const int *__restrict__ tile_flags,
                                                      int ntiles, int max_edges,
                                                      int *__restrict__ tile_off,
-                                                     StepResult *__restrict__ result)
+                                                     StepResult *__restrict__ result,
+                                                     int *__restrict__ state)
 {
   __shared__ long part[1024];
   __shared__ int flag_any;
@@ -176,6 +182,9 @@ __global__ __launch_bounds__(1024) void k_tile_scan(const int *__restrict__ tile
     tile_off[ntiles] = static_cast<int>(total);
     result->edge_count = static_cast<int>(total);
     result->edge_overflow = total > max_edges ? 1 : 0;
+    // the write pass resets [count, previous live count) after the new edges
+    state[kPrevLive] = state[kLive];
+    state[kLive] = static_cast<int>(total < max_edges ? total : max_edges);
   }
   __syncthreads();
   if (t == 0) result->ghost_sender = flag_any;
@@ -270,13 +279,15 @@ __global__ __launch_bounds__(W * 64) void k_pack_write(PackArgs a, const int *__
                                                        int *__restrict__ receivers,
                                                        unsigned char *__restrict__ mask,
                                                        const StepResult *__restrict__ result,
-                                                       long reset_end)
+                                                       const int *__restrict__ state)
 {
   const int tile = tile_of_block();
   if (tile * kWave < a.num_rows) pack_write_tile<W>(a, tile, tile_off, senders, receivers, mask);
-  // ResetEdgeTailFunctor (cpp:157-173): slots past the new count that held last step's edges
-  // return to the padding (max_atoms, max_atoms, false); a grid-stride pass over every block.
+  // ResetEdgeTailFunctor (cpp:157-173): slots past the new count that held the previous pack's
+  // edges return to the padding (max_atoms, max_atoms, false); a grid-stride pass over every
+  // block. Both bounds come from the scan pass, on the device.
   const long count = result->edge_count;
+  const long reset_end = state[kPrevLive];
   for (long e = count + static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < reset_end;
        e += static_cast<long>(gridDim.x) * blockDim.x) {
     senders[e] = a.max_atoms;
@@ -354,7 +365,7 @@ hipError_t launch_iota(hipStream_t s, int *p, int n)
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles)
 {
   hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(1024), 0, s, h.d_tile_count, tile_flags, ntiles,
-                     h.contract.max_edges, h.d_tile_off, h.d_result);
+                     h.contract.max_edges, h.d_tile_off, h.d_result, h.d_pack_state);
   return hipGetLastError();
 }
 
@@ -407,13 +418,11 @@ hipError_t launch_pack_write(Handle &h, hipStream_t s, const PackArgs &a)
 {
   constexpr int W = 4;
   const int ntiles = (a.num_rows + kWave - 1) / kWave;
-  const long reset_end = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
-                                                                     : h.contract.max_edges;
   // at least one block so the tail reset runs when the list is empty
   const int grid = tile_grid(ntiles > 0 ? ntiles : 1);
   StageTimer timer(h, s, "pack_write");
   hipLaunchKernelGGL(k_pack_write<W>, dim3(grid), dim3(W * kWave), 0, s, a, h.d_tile_off,
-                     h.d_senders, h.d_receivers, h.d_mask, h.d_result, reset_end);
+                     h.d_senders, h.d_receivers, h.d_mask, h.d_result, h.d_pack_state);
   return hipGetLastError();
 }
 
@@ -435,7 +444,7 @@ hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const in
   {
     StageTimer timer(h, s, "tile_scan");
     hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(1024), 0, s, h.d_tile_count, a.tile_flags,
-                       ntiles, h.contract.max_edges, h.d_tile_off, h.d_result);
+                       ntiles, h.contract.max_edges, h.d_tile_off, h.d_result, h.d_pack_state);
   }
   hipError_t e = launch_pack_write(h, s, a);
   ++h.pack_serial;

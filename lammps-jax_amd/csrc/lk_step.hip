@@ -44,7 +44,7 @@ struct StepPack {
   int *row_count;
   int *row_atom;
   int *tile_base;
-  int *state;  // [0] demand counter, [1] ghost-sender flag (cleared by K0)
+  int *state;  // pack state words (PackState): demand counter and ghost flag cleared by K0
   int *senders;
   int *receivers;
   unsigned char *mask;
@@ -299,10 +299,10 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
       const double esum = wave_sum(e_own);
       if (lane == 0 && tile * kWave < p.num_rows) {
         // the tile's slots [base, base + total): one claim per tile (cpp:102-110 claims per entry)
-        const int base = atomicAdd(&p.state[0], total);
+        const int base = atomicAdd(&p.state[kDemand], total);
         sbase[sub] = base;
         p.tile_base[tile] = base;
-        if (gmask != 0) atomicOr(&p.state[1], 1);
+        if (gmask != 0) atomicOr(&p.state[kGhostFlag], 1);
         a.partials[8L * tile + 0] = esum;
       }
     }
@@ -388,9 +388,14 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
   }
 }
 
+// Starts a pack without the atom records (matrix bundles, whose records come from a separate
+// lk_pack_atoms): zeroes the demand count and the ghost-sender flag.
 __global__ void k_clear_state(int *state)
 {
-  if (threadIdx.x < 2) state[threadIdx.x] = 0;
+  if (threadIdx.x == 0) {
+    state[kDemand] = 0;
+    state[kGhostFlag] = 0;
+  }
 }
 
 template <typename S, bool EAM, bool MATRIX>
@@ -451,14 +456,12 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   ++h.pack_serial;
   FusedPack fp;
   // matrix bundles keep the copy's widest row and overflow flag as the step's counts
-  fp.counter = MATRIX ? nullptr : h.d_pack_state;
+  fp.state = MATRIX ? nullptr : h.d_pack_state;
   fp.senders = h.d_senders;
   fp.receivers = h.d_receivers;
   fp.mask = h.d_mask;
   fp.max_edges = h.contract.max_edges;
   fp.pad = h.contract.max_atoms;
-  fp.reset_end = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
-                                                            : h.contract.max_edges;
   if constexpr (EAM) {
     a.pack = fp;
     return launch_eam_force(h, s, a, flags);
@@ -510,14 +513,12 @@ static hipError_t pack_fused(Handle &h, hipStream_t s, const double *x, const in
                        dim3(kStepW * kStepTPB * kWave), 0, s, p, a, ngroups);
   }
   ++h.pack_serial;
-  out->counter = h.d_pack_state;
+  out->state = h.d_pack_state;
   out->senders = h.d_senders;
   out->receivers = h.d_receivers;
   out->mask = h.d_mask;
   out->max_edges = h.contract.max_edges;
   out->pad = h.contract.max_atoms;
-  out->reset_end = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
-                                                              : h.contract.max_edges;
   return hipGetLastError();
 }
 

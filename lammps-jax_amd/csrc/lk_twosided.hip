@@ -1057,13 +1057,13 @@ static TwoSided two_sided_args(Handle &h, int nlocal, int nghost, const double *
   return t;
 }
 
-// A fused pack (`pack.counter` set) leaves the demand count and the ghost-sender flag in its
-// state words and the previous step's tail to reset; the sweeps take both from there.
+// A fused pack (`pack.state` set) leaves the demand count and the ghost-sender flag in its
+// state words and the previous pack's tail to reset; the sweeps take both from there.
 static void use_pack(TwoSided &t, const FusedPack &pack)
 {
-  if (!pack.counter) return;
+  if (!pack.state) return;
   t.pack = pack;
-  t.ghost_flag = pack.counter + 1;
+  t.ghost_flag = pack.state + kGhostFlag;
 }
 
 template <typename S, bool HALF>
@@ -1163,7 +1163,7 @@ struct EdgeOut {
   const unsigned char *mask;
   const StepResult *count;  // the pack's demand count of this step
   int max_edges;
-  long reset_end;           // slots below it held the previous step's forces
+  const int *state;         // pack state: kEdgeForceLive slots hold the previous compute's forces
   S *edge_f;
   double *f;
   double scale;
@@ -1211,7 +1211,8 @@ __device__ __forceinline__ void edge_tail_and_slots(const EdgeOut<S> &o, long ne
 {
   const long stride = static_cast<long>(gridDim.x) * blockDim.x;
   const long tid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
-  for (long e = ne + tid; e < o.reset_end; e += stride) {
+  const long reset_end = o.state[kEdgeForceLive];
+  for (long e = ne + tid; e < reset_end; e += stride) {
     S *q = o.edge_f + 3 * e;
     q[0] = S(0);
     q[1] = S(0);
@@ -1308,19 +1309,25 @@ __global__ __launch_bounds__(256) void k_lj_edge_force(LjModel<S> m, EdgeOut<S> 
 }
 
 // f.r of the total f over the nall rows (cpp:227-245) into slots 1..6 of each 64-row tile, then
-// the last block reduces every slot into the step result.
+// the last block reduces every slot into the step result. The edge-force launch before it has
+// finished: its live slot count becomes the next compute's reset bound.
 template <bool VIRIAL>
 __global__ __launch_bounds__(256) void k_fdotr_rows(const double *__restrict__ f,
                                                     const double *__restrict__ x, int nall,
                                                     int fdotr, double *partials, int ntiles,
                                                     double escale, int flags, StepResult *result,
-                                                    int *done, StepResult *mirror)
+                                                    int *done, StepResult *mirror, int *state,
+                                                    int max_edges)
 {
   constexpr int kWaves = 256 / kWave;
   __shared__ double scratch[7 * 256];
   __shared__ double tp[kWaves][6];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = wave_in_block();
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    const int c = result->edge_count;
+    state[kEdgeForceLive] = c < max_edges ? c : max_edges;
+  }
   // Each wave sums one tile; the first wave alone stores the block's tiles (finalize_last_block
   // releases the first wave's stores only). The loop bounds are the block's, for the barriers.
   for (int t0 = blockIdx.x * kWaves; t0 < ntiles; t0 += static_cast<int>(gridDim.x) * kWaves) {
@@ -1363,8 +1370,7 @@ static EdgeOut<S> edge_out(Handle &h, int nlocal, int nghost, double scale, doub
   o.mask = h.d_mask;
   o.count = h.d_result;
   o.max_edges = h.contract.max_edges;
-  o.reset_end = h.cached_edge_count < h.contract.max_edges ? h.cached_edge_count
-                                                           : h.contract.max_edges;
+  o.state = h.d_pack_state;
   o.edge_f = static_cast<S *>(h.d_edge_f);
   o.f = f;
   o.scale = scale;
@@ -1385,10 +1391,12 @@ static hipError_t launch_fdotr(Handle &h, hipStream_t s, double *f, const double
   StageTimer timer(h, s, "virial_fdotr");
   if ((flags & LK_VIRIAL) && fdotr)
     hipLaunchKernelGGL((k_fdotr_rows<true>), dim3(grid), dim3(256), 0, s, f, x, nall, fdotr,
-                       h.d_partials, ntiles, scale, flags, h.d_result, h.d_done, h.d_host_result);
+                       h.d_partials, ntiles, scale, flags, h.d_result, h.d_done, h.d_host_result,
+                       h.d_pack_state, h.contract.max_edges);
   else
     hipLaunchKernelGGL((k_fdotr_rows<false>), dim3(grid), dim3(256), 0, s, f, x, nall, fdotr,
-                       h.d_partials, ntiles, scale, flags, h.d_result, h.d_done, h.d_host_result);
+                       h.d_partials, ntiles, scale, flags, h.d_result, h.d_done, h.d_host_result,
+                       h.d_pack_state, h.contract.max_edges);
   return hipGetLastError();
 }
 

@@ -56,6 +56,11 @@ class Nve:
                  headroom: float = 1.10):
         import torch
 
+        if wl.accumulation != "onesided":
+            # The plain and half schemes leave part of the pair force on ghost rows, which the
+            # engine's reverse comm adds into the owners; this driver has no reverse comm.
+            raise ValueError(f"Nve drives the one-sided scheme only, not {wl.accumulation!r}: "
+                             "ghost force rows would need a reverse comm")
         self.torch = torch
         self.wl = wl
         self.dt = float(dt)

@@ -260,6 +260,19 @@ class PairJax:
                                 max_owned=max_owned)
         self._setup(contract, accumulation)
 
+    @classmethod
+    def for_workload(cls, wl, system, *, layout="sparse-edge", device="cuda:0",
+                     fused=True) -> "PairJax":
+        """The pair style of a named workload (systems.make_workload) on its system: the
+        workload's model, precision, scheme, n_hops and edge capacity per atom, and an atom
+        capacity with the headroom of an exported bundle (systems.atom_capacity)."""
+        from .systems import atom_capacity
+
+        model = ("eam", wl.tables) if wl.model == "eam" else ("lj", wl.lj)
+        return cls(system, model, precision=wl.precision, accumulation=wl.accumulation,
+                   n_hops=wl.n_hops, max_atoms=atom_capacity(system.nall),
+                   edges_per_atom=wl.edges_per_atom, device=device, layout=layout, fused=fused)
+
     def _setup(self, contract: N.LkContract, accumulation) -> None:
         self.contract = contract
         self.h = Handle(self.contract)

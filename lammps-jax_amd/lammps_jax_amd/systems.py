@@ -189,3 +189,9 @@ def make_workload(name: str, *, cells=None, seed: int | None = None) -> Workload
 
 
 WORKLOADS = ("lj_fcc_1k", "eam_alloy_8k", "eam_alloy_131k", "eam_alloy_1m", "lj_ghost_262k")
+
+
+def atom_capacity(nall: int) -> int:
+    """max_atoms of a bundle exported for a system of nall rows: 5% headroom, rounded up to a
+    multiple of 1024 (the benchmark's and the full-size tests' contract)."""
+    return ((nall * 21 // 20) + 1023) // 1024 * 1024

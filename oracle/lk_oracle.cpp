@@ -108,6 +108,18 @@ inline S spline_slope(const S *tab, int n, S delta, S x, bool extrapolate)
   return (c[1] + t * (S(2) * c[2] + t * (S(3) * c[3]))) / delta;
 }
 
+// The model's energy, jnp.sum of the counted rows' energies at the contract precision
+// (export.py:183-199). XLA leaves the order of that reduction to the backend (a tree on GPUs), so
+// the restatement takes the sum in float64 and rounds it to the precision once: the value every
+// summation order approaches, where a sequential float32 sum of a million rows drifts by 1e-5.
+template <typename S>
+double total_energy(const S *Ei, int rows)
+{
+  double acc = 0.0;
+  for (int i = 0; i < rows; ++i) acc += static_cast<double>(Ei[i]);
+  return static_cast<double>(static_cast<S>(acc));
+}
+
 template <typename S>
 Tables<S> make_tables(int n_el, int nrho, double drho, int nr, double dr, double cutoff,
                       const double *emb, const double *dens, const double *pair)
@@ -216,12 +228,7 @@ double eam_compute(const Tables<S> &T, const double *positions_d, const int *spe
   const bool only_owned = owned_rows_only || mode != kPlain;
   const bool use_total = !only_owned && ghost_sender;
   const int erows = use_total ? nall : nlocal;
-  double energy = 0.0;
-  {
-    S acc = S(0);
-    for (int i = 0; i < erows; ++i) acc += Ei[i];
-    energy = static_cast<double>(acc);
-  }
+  const double energy = total_energy(Ei.data(), erows);
   auto counted = [&](int a) { return a < erows; };
 
   double W[6] = {0, 0, 0, 0, 0, 0};
@@ -324,9 +331,7 @@ double lj_compute(double epsilon, double sigma, double cutoff, double edge_energ
   }
   const bool only_owned = owned_rows_only || mode != kPlain;
   const int erows = (!only_owned && ghost_sender) ? nall : nlocal;
-  S acc = S(0);
-  for (int i = 0; i < erows; ++i) acc += Ei[i];
-  const double energy = static_cast<double>(acc);
+  const double energy = total_energy(Ei.data(), erows);
 
   double W[6] = {0, 0, 0, 0, 0, 0};
   for (long e = 0; e < n_edges; ++e) {

@@ -349,6 +349,21 @@ def parse_setfl_tokens(text: str) -> dict:
     return out
 
 
+def setfl_tables(text: str) -> dict:
+    """The model tables of a setfl text, built by the oracle alone: parse_setfl_tokens for the
+    values, or_spline_coefficients for the PairEAM::interpolate coefficients (eam.py:115-135),
+    pair rows in file order (pair_table_id, eam.py:167-171)."""
+    raw = parse_setfl_tokens(text)
+    return {
+        "elements": raw["elements"], "masses": raw["masses"],
+        "nrho": raw["nrho"], "drho": raw["drho"], "nr": raw["nr"], "dr": raw["dr"],
+        "cutoff": raw["cutoff"],
+        "embedding": np.stack([spline_coefficients(v) for v in raw["F"]]),
+        "density": np.stack([spline_coefficients(v) for v in raw["rho"]]),
+        "pair": np.stack([spline_coefficients(v) for v in raw["z2r"]]),
+    }
+
+
 def dense_eam(tables, positions, species, box=None):
     """All-pairs float64 EAM, pair_eam.cpp evaluation (test_eam.py:338-394 semantics).
 

@@ -28,14 +28,16 @@ def _load_module(name: str, path: Path):
 
 
 def _ensure_built():
-    """Builds only what is missing (a fresh checkout); a built tree is used as is."""
+    """Builds a library that is missing or whose sources changed since it was built (each
+    library's .srchash stamp records the SHA-256 of the sources and flags it was built from), so
+    the tests never run a stale library."""
     pkg_build = _load_module("lk_pkg_build", PKG_ROOT / "build.py")
-    if not (PKG_ROOT / "lammps_jax_amd" / "liblkharness.so").exists():
+    if not pkg_build.harness_current():
         pkg_build.build_harness()
-    if not (PKG_ROOT / "lammps_jax_amd" / "liblkhip.so").exists():
+    if not pkg_build.hip_current():
         pkg_build.build_hip()
     ob = _load_module("lk_oracle_build", REPO / "oracle" / "build.py")
-    if not (REPO / "oracle" / "liblkoracle.so").exists():
+    if not ob.is_current():
         ob.build()
 
 

@@ -57,6 +57,34 @@ def fold_ghosts(forces: np.ndarray, nlocal: int, ghost_owner: np.ndarray) -> np.
     return out
 
 
+# Parity bars. Float64: the reference's own (tests/test_lammps.py:49-51): forces within 1e-11
+# absolute, energy within 1e-13 per atom; the virial within 1e-12 relative (normwise). Float32:
+# 1e-5 relative.
+F64_FORCE_ABS = 1.0e-11
+F64_ENERGY_PER_ATOM = 1.0e-13
+F64_VIRIAL_REL = 1.0e-12
+F32_REL = 1.0e-5
+
+
+def assert_energy(precision: int, energy: float, ref: float, natoms: int, scale: float = 1.0):
+    if precision == 8:
+        assert abs(energy - scale * ref) <= F64_ENERGY_PER_ATOM * natoms, (energy, scale * ref)
+    else:
+        assert abs(energy - scale * ref) <= F32_REL * abs(scale * ref), (energy, scale * ref)
+
+
+def assert_forces(precision: int, f, ref):
+    if precision == 8:
+        err = float(np.max(np.abs(np.asarray(f, np.float64) - ref))) if np.size(f) else 0.0
+        assert err <= F64_FORCE_ABS, err
+    else:
+        assert rel_err(f, ref) < F32_REL
+
+
+def assert_virial(precision: int, v, ref):
+    assert rel_err(v, ref) < (F64_VIRIAL_REL if precision == 8 else F32_REL)
+
+
 def rel_err(a, b) -> float:
     """Normwise relative error max|a-b| / max|b| (the reference tests' force metric)."""
     a = np.asarray(a, np.float64)
