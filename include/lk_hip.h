@@ -180,6 +180,28 @@ int lk_pack_edges(lk_handle *h, void *stream, const double *x, const int *ilist,
                   int maxneighs, int nlocal);
 
 /*
+ * lk_pack_edges without allocation: no counterpart in the reference. For callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc), it needs no handle and calls no allocator. The same cutoff filter and
+ * compaction as lk_pack_edges (same kernels, same packed order) under `contract` (checked as
+ * lk_create checks it; sparse-edge layout only), into the caller's device arrays senders,
+ * receivers [contract->max_edges] and mask [max_edges]; counts [2] (device) receives the edge
+ * demand count and the overflow flag. prev_count is the count this call's arrays held from the
+ * caller's previous pack into them (0 for fresh padding): slots [count, prev_count) return to
+ * the padding (max_atoms, max_atoms, 0), as ResetEdgeTailFunctor does.
+ * Working memory is a fixed device array of 24.2 MB per GPU, held until the process ends:
+ * at most 1,048,576 list rows and 4,194,304 validity words (rows times ceil(maxneighs / 32)) per
+ * call, else LK_ERR_CAPACITY. Every call on a GPU shares that array: calls that overlap on one
+ * GPU (on different streams, or from different threads) race. Errors return a status code and
+ * the message in err (errlen bytes).
+ */
+int lk_pack_edges_noalloc(const lk_contract *contract, void *stream, const double *x,
+                          const int *ilist, const int *numneigh, const int *neighbors,
+                          long nb_stride, int inum, int gnum, int maxneighs, int nlocal,
+                          int *senders, int *receivers, unsigned char *mask, int *counts,
+                          int prev_count, char *err, int errlen);
+
+/*
  * Energy and gradient of the model on the packed edges, added into the engine's force array:
  * f[i] += scale * F[i] (f: double [nall][3], device). flags: LK_ENERGY | LK_VIRIAL.
  */

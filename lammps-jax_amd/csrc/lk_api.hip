@@ -13,6 +13,7 @@
 
 #include "lk_device.h"
 #include "lk_internal.h"
+#include "lk_pack.h"
 
 struct lk_handle {
   lk::Handle h;
@@ -135,6 +136,70 @@ int ensure_incidence(Handle &h, long entries = 0)
   return LK_OK;
 }
 
+// The contract checks of lk_create: the reference's load_bundle_file validation
+// (cpp/lammps_jax_model.cpp:271-313) and init_style's newton checks (cpp/pair_jax_kokkos.cpp:
+// 668-673). Returns the message of the first failed check, or null.
+const char *contract_problem(const lk_contract *c)
+{
+  const bool matrix = c->input_layout == LK_LAYOUT_NEIGHBOR_MATRIX;
+  if (!matrix && c->input_layout != LK_LAYOUT_SPARSE_EDGE)
+    return "Unsupported LAMMPS-JAX input layout; re-export the bundle with the current "
+           "lammps_jax exporter";
+  // cpp/lammps_jax_model.cpp:277-279
+  if (c->max_atoms <= 0 || (matrix ? c->max_neighbors : c->max_edges) <= 0)
+    return "Invalid fixed capacities in bundle";
+  if (c->max_owned < 0 || c->max_owned > c->max_atoms)
+    return "Invalid max_owned in bundle";
+  if (c->precision != LK_FLOAT32 && c->precision != LK_FLOAT64)
+    return "Unsupported LAMMPS-JAX precision; expected float32 or float64";
+  if (c->n_hops < 1) return "Invalid n_hops in bundle";
+  if (c->n_species < 0) return "Invalid n_species in bundle";
+  if (c->cutoff < 0) return "cutoff must be non-negative";
+  const bool half_edges = c->pairing != LK_PAIRING_FULL;
+  if (c->pairing == LK_PAIRING_HALF && c->comm)
+    return "Communicating half-edge bundles now pack each boundary pair on one rank; "
+           "re-export this bundle";
+  if (c->pairing == LK_PAIRING_HALF_UNIQUE && !c->comm)
+    return "Unique-boundary bundles need a communication schedule; the partner rank's "
+           "density share arrives through reverse comm";
+  if (half_edges && c->n_hops == 1 && !c->comm)
+    return "Half-edge bundles require n_hops > 1 or a communication schedule; the "
+           "single-hop packer does not deduplicate edge directions";
+  if (c->n_hops > 1 && (c->newton != LK_NEWTON_ON || c->edge_force))
+    return "Bundles with n_hops > 1 require newton on and atom-force output; ghost force "
+           "rows must flow back through the LAMMPS reverse communication";
+  if (c->comm && c->n_hops != 1)
+    return "Communicating bundles require a one-cutoff ghost shell (n_hops = 1)";
+  if (c->comm && c->newton != LK_NEWTON_ON && (half_edges || c->edge_force))
+    return "Communicating bundles require newton on unless they pair fully and return atom "
+           "forces; ghost force rows flow back through the LAMMPS reverse communication";
+  if (c->comm && c->edge_force && !half_edges)
+    return "Communicating edge-force bundles require half-edge packing; full pairing packs "
+           "both directions and the newton scatter doubles forces";
+  // cpp/lammps_jax_model.cpp:283-297 and cpp/pair_jax_kokkos.cpp:369-373
+  if (matrix && c->edge_force)
+    return "Neighbor-matrix bundles return per-atom forces; edge-force output needs sparse "
+           "edges";
+  if (c->max_owned > 0 && !c->comm && !(matrix && c->n_hops == 1))
+    return "max_owned needs a communicating or single-hop neighbor-matrix bundle; other "
+           "layouts hold ghost rows past the owned ones";
+  if (matrix && half_edges && !c->comm)
+    return "Neighbor-matrix half pairing needs a communication schedule; the pair style "
+           "hands the model the LAMMPS half list as is";
+  if (matrix) {
+    const long rows = c->max_owned > 0 ? c->max_owned : c->max_atoms;
+    if (rows * c->max_neighbors > static_cast<long>(INT_MAX))
+      return "neighbor matrix rows times max_neighbors exceeds the int range; lower "
+             "max_owned, max_atoms, or max_neighbors";
+  }
+  // init_style newton checks (cpp/pair_jax_kokkos.cpp:668-673)
+  if (c->newton == LK_NEWTON_ON && !c->newton_pair)
+    return "LAMMPS-JAX bundle was exported for newton pair on; this run uses newton off";
+  if (c->newton == LK_NEWTON_OFF && c->newton_pair)
+    return "LAMMPS-JAX bundle was exported for newton pair off; this run uses newton on";
+  return nullptr;
+}
+
 }  // namespace
 
 extern "C" {
@@ -151,81 +216,17 @@ int lk_create(const lk_contract *c, lk_handle **out)
   }
   h.contract = *c;
   *out = wrap;
+  if (const char *problem = contract_problem(c)) return fail(h, LK_ERR_ARGUMENT, problem);
   const bool matrix = c->input_layout == LK_LAYOUT_NEIGHBOR_MATRIX;
-  if (!matrix && c->input_layout != LK_LAYOUT_SPARSE_EDGE)
-    return fail(h, LK_ERR_ARGUMENT,
-                "Unsupported LAMMPS-JAX input layout; re-export the bundle with the current "
-                "lammps_jax exporter");
-  // cpp/lammps_jax_model.cpp:277-279
-  if (c->max_atoms <= 0 || (matrix ? c->max_neighbors : c->max_edges) <= 0)
-    return fail(h, LK_ERR_ARGUMENT, "Invalid fixed capacities in bundle");
-  if (c->max_owned < 0 || c->max_owned > c->max_atoms)
-    return fail(h, LK_ERR_ARGUMENT, "Invalid max_owned in bundle");
-  if (c->precision != LK_FLOAT32 && c->precision != LK_FLOAT64)
-    return fail(h, LK_ERR_ARGUMENT, "Unsupported LAMMPS-JAX precision; expected float32 or float64");
-  if (c->n_hops < 1) return fail(h, LK_ERR_ARGUMENT, "Invalid n_hops in bundle");
-  if (c->n_species < 0) return fail(h, LK_ERR_ARGUMENT, "Invalid n_species in bundle");
-  if (c->cutoff < 0) return fail(h, LK_ERR_ARGUMENT, "cutoff must be non-negative");
   const bool half_edges = c->pairing != LK_PAIRING_FULL;
-  if (c->pairing == LK_PAIRING_HALF && c->comm)
-    return fail(h, LK_ERR_ARGUMENT,
-                "Communicating half-edge bundles now pack each boundary pair on one rank; "
-                "re-export this bundle");
-  if (c->pairing == LK_PAIRING_HALF_UNIQUE && !c->comm)
-    return fail(h, LK_ERR_ARGUMENT,
-                "Unique-boundary bundles need a communication schedule; the partner rank's "
-                "density share arrives through reverse comm");
-  if (half_edges && c->n_hops == 1 && !c->comm)
-    return fail(h, LK_ERR_ARGUMENT,
-                "Half-edge bundles require n_hops > 1 or a communication schedule; the "
-                "single-hop packer does not deduplicate edge directions");
-  if (c->n_hops > 1 && (c->newton != LK_NEWTON_ON || c->edge_force))
-    return fail(h, LK_ERR_ARGUMENT,
-                "Bundles with n_hops > 1 require newton on and atom-force output; ghost force "
-                "rows must flow back through the LAMMPS reverse communication");
-  if (c->comm && c->n_hops != 1)
-    return fail(h, LK_ERR_ARGUMENT,
-                "Communicating bundles require a one-cutoff ghost shell (n_hops = 1)");
-  if (c->comm && c->newton != LK_NEWTON_ON && (half_edges || c->edge_force))
-    return fail(h, LK_ERR_ARGUMENT,
-                "Communicating bundles require newton on unless they pair fully and return atom "
-                "forces; ghost force rows flow back through the LAMMPS reverse communication");
-  if (c->comm && c->edge_force && !half_edges)
-    return fail(h, LK_ERR_ARGUMENT,
-                "Communicating edge-force bundles require half-edge packing; full pairing packs "
-                "both directions and the newton scatter doubles forces");
-  // cpp/lammps_jax_model.cpp:283-297 and cpp/pair_jax_kokkos.cpp:369-373
-  if (matrix && c->edge_force)
-    return fail(h, LK_ERR_ARGUMENT,
-                "Neighbor-matrix bundles return per-atom forces; edge-force output needs sparse "
-                "edges");
-  if (c->max_owned > 0 && !c->comm && !(matrix && c->n_hops == 1))
-    return fail(h, LK_ERR_ARGUMENT,
-                "max_owned needs a communicating or single-hop neighbor-matrix bundle; other "
-                "layouts hold ghost rows past the owned ones");
-  if (matrix && half_edges && !c->comm)
-    return fail(h, LK_ERR_ARGUMENT,
-                "Neighbor-matrix half pairing needs a communication schedule; the pair style "
-                "hands the model the LAMMPS half list as is");
   if (matrix) {
     const long rows = c->max_owned > 0 ? c->max_owned : c->max_atoms;
-    if (rows * c->max_neighbors > static_cast<long>(INT_MAX))
-      return fail(h, LK_ERR_ARGUMENT,
-                  "neighbor matrix rows times max_neighbors exceeds the int range; lower "
-                  "max_owned, max_atoms, or max_neighbors");
     h.matrix = true;
     h.matrix_rows = static_cast<int>(rows);
     // the row kernels' internal edge capacity: every matrix slot (never exceeded)
     h.contract.max_edges = static_cast<int>(rows * c->max_neighbors);
     h.list_bits_filter = false;  // the model masks the matrix slots itself
   }
-  // init_style newton checks (cpp/pair_jax_kokkos.cpp:668-673)
-  if (c->newton == LK_NEWTON_ON && !c->newton_pair)
-    return fail(h, LK_ERR_ARGUMENT,
-                "LAMMPS-JAX bundle was exported for newton pair on; this run uses newton off");
-  if (c->newton == LK_NEWTON_OFF && c->newton_pair)
-    return fail(h, LK_ERR_ARGUMENT,
-                "LAMMPS-JAX bundle was exported for newton pair off; this run uses newton on");
   // default accumulation from the contract; matrix bundles run the row models of their list
   // (eam_pallas.py:313-343): half lists the half scheme, full lists the one-sided rows
   if (matrix)
@@ -872,6 +873,73 @@ int lk_model_buffers(lk_handle *w, void **rho, void **fp)
   if (!w) return LK_ERR_ARGUMENT;
   if (rho) *rho = w->h.d_rho;
   if (fp) *fp = w->h.d_fp;
+  return LK_OK;
+}
+
+int lk_pack_edges_noalloc(const lk_contract *contract, void *stream, const double *x,
+                          const int *ilist, const int *numneigh, const int *neighbors,
+                          long nb_stride, int inum, int gnum, int maxneighs, int nlocal,
+                          int *senders, int *receivers, unsigned char *mask, int *counts,
+                          int prev_count, char *err, int errlen)
+{
+  auto say = [&](int code, const std::string &msg) {
+    if (err && errlen > 0) {
+      std::strncpy(err, msg.c_str(), static_cast<size_t>(errlen) - 1);
+      err[errlen - 1] = 0;
+    }
+    return code;
+  };
+  if (err && errlen > 0) err[0] = 0;
+  if (!contract) return say(LK_ERR_ARGUMENT, "contract is null");
+  if (const char *problem = contract_problem(contract)) return say(LK_ERR_ARGUMENT, problem);
+  const lk_contract &c = *contract;
+  if (c.input_layout != LK_LAYOUT_SPARSE_EDGE)
+    return say(LK_ERR_UNSUPPORTED,
+               "the pack without allocation writes sparse edges; neighbor-matrix contracts copy "
+               "the list with lk_pack_edges");
+  if (inum < 0 || gnum < 0 || nlocal < 0) return say(LK_ERR_ARGUMENT, "invalid list sizes");
+  const bool multi_hop = c.n_hops > 1;
+  long rows = static_cast<long>(inum) + (multi_hop ? gnum : 0);
+  if (rows > c.max_atoms) rows = c.max_atoms;  // the collective capacity check errors this step
+  const int mnb = maxneighs > 1 ? maxneighs : 1;
+  if (rows * mnb > static_cast<long>(INT_MAX))
+    return say(LK_ERR_CAPACITY,
+               "LAMMPS-JAX neighbor pack index overflows int; reduce the bundle max_atoms or the "
+               "neigh_modify one setting");
+  if (rows > 0 && (!x || !ilist || !numneigh || !neighbors))
+    return say(LK_ERR_ARGUMENT, "invalid neighbor list arrays");
+  if (rows > 0 && nb_stride < 1) return say(LK_ERR_ARGUMENT, "invalid neighbor stride");
+  if (!senders || !receivers || !mask || !counts)
+    return say(LK_ERR_ARGUMENT, "invalid packed edge arrays");
+  const long words = (mnb + 31) / 32;
+  if (rows > lk::kScratchRows || rows * words > lk::kScratchBitWords)
+    return say(LK_ERR_CAPACITY,
+               "the pack without allocation takes at most " + std::to_string(lk::kScratchRows) +
+                   " list rows and " + std::to_string(lk::kScratchBitWords) +
+                   " validity words (rows times ceil(maxneighs / 32)); this call has " +
+                   std::to_string(rows) + " rows of " + std::to_string(words) + " words");
+  // the filter flags of lk_pack_edges (cpp/pair_jax_kokkos.cpp:850-867)
+  const bool half_edges = c.pairing != LK_PAIRING_FULL;
+  const bool full_list = !c.half_list;
+  lk::PackArgs a{};
+  a.x = x;
+  a.ilist = ilist;
+  a.numneigh = numneigh;
+  a.neighbors = neighbors;
+  a.stride = nb_stride;
+  a.num_rows = static_cast<int>(rows);
+  a.maxneighs = mnb;
+  a.max_atoms = c.max_atoms;
+  a.max_edges = c.max_edges;
+  a.nlocal = nlocal;
+  a.cutsq = c.cutoff * c.cutoff;
+  a.duplicate = c.newton_pair && c.pair_sum && !c.edge_force && !multi_hop && !c.comm;
+  a.half_edges = half_edges && full_list;
+  a.unique_boundary = half_edges && c.comm && full_list;
+  const int prev = prev_count < 0 ? 0 : (prev_count > c.max_edges ? c.max_edges : prev_count);
+  const hipError_t e = lk::launch_pack_edges_noalloc(as_stream(stream), a, senders, receivers,
+                                                     mask, counts, prev);
+  if (e != hipSuccess) return say(LK_ERR_DEVICE, std::string("pack_edges: ") + hipGetErrorString(e));
   return LK_OK;
 }
 

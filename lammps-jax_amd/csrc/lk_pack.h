@@ -55,6 +55,18 @@ __device__ __forceinline__ bool keep_entry(const PackArgs &a, int i, double xi0,
   return true;
 }
 
+// Limits of lk_pack_edges_noalloc, whose working memory is a fixed device array (lk_pack.hip):
+// list rows, and rows times validity words (one word per 32 list slots of a row).
+constexpr long kScratchRows = 1L << 20;
+constexpr long kScratchBitWords = 1L << 22;
+
+// The pack of lk_pack_edges into caller-owned arrays with the fixed device array as its working
+// memory: no allocation. `a` carries the list, the sizes and the filter flags (its bits, row and
+// tile pointers are set here); counts_out [2] (device) receives the demand count and the overflow
+// flag; prev_live bounds the tail reset. Sizes must be within the limits above.
+hipError_t launch_pack_edges_noalloc(hipStream_t s, PackArgs a, int *senders, int *receivers,
+                                     unsigned char *mask, int *counts_out, int prev_live);
+
 PackArgs pack_args(Handle &h, const double *x, const int *ilist, const int *numneigh,
                    const int *neighbors, long stride, int num_rows, int maxneighs, int nlocal,
                    int duplicate, int half_edges, int unique_boundary);

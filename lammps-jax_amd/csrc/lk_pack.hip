@@ -13,6 +13,8 @@
 // Three launches: count (filter, per-row counts, validity bits), a scan of the tile totals, and
 // the compacted write; then the tail reset of slots the previous step used.
 
+#include <mutex>
+
 #include "lk_device.h"
 #include "lk_internal.h"
 #include "lk_tile.h"
@@ -279,7 +281,8 @@ __global__ __launch_bounds__(W * 64) void k_pack_write(PackArgs a, const int *__
                                                        int *__restrict__ receivers,
                                                        unsigned char *__restrict__ mask,
                                                        const StepResult *__restrict__ result,
-                                                       const int *__restrict__ state)
+                                                       const int *__restrict__ state,
+                                                       int *__restrict__ counts_out)
 {
   const int tile = tile_of_block();
   if (tile * kWave < a.num_rows) pack_write_tile<W>(a, tile, tile_off, senders, receivers, mask);
@@ -288,6 +291,10 @@ __global__ __launch_bounds__(W * 64) void k_pack_write(PackArgs a, const int *__
   // block. Both bounds come from the scan pass, on the device.
   const long count = result->edge_count;
   const long reset_end = state[kPrevLive];
+  if (counts_out && blockIdx.x == 0 && threadIdx.x == 0) {
+    counts_out[0] = result->edge_count;
+    counts_out[1] = result->edge_overflow;
+  }
   for (long e = count + static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < reset_end;
        e += static_cast<long>(gridDim.x) * blockDim.x) {
     senders[e] = a.max_atoms;
@@ -422,7 +429,8 @@ hipError_t launch_pack_write(Handle &h, hipStream_t s, const PackArgs &a)
   const int grid = tile_grid(ntiles > 0 ? ntiles : 1);
   StageTimer timer(h, s, "pack_write");
   hipLaunchKernelGGL(k_pack_write<W>, dim3(grid), dim3(W * kWave), 0, s, a, h.d_tile_off,
-                     h.d_senders, h.d_receivers, h.d_mask, h.d_result, h.d_pack_state);
+                     h.d_senders, h.d_receivers, h.d_mask, h.d_result, h.d_pack_state,
+                     static_cast<int *>(nullptr));
   return hipGetLastError();
 }
 
@@ -449,6 +457,94 @@ hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const in
   hipError_t e = launch_pack_write(h, s, a);
   ++h.pack_serial;
   return e;
+}
+
+// ----------------------------------------------------------------------------------------------
+// The pack without allocation (lk_pack_edges_noalloc). Its working memory (validity bits, row
+// counts and row atoms, tile totals, flags and offsets, the scan's result and the slot counts)
+// is `scratch`, a file-scope device array that every GPU the library runs on holds from the
+// library's load to the end of the process: 24.2 MB. The caller owns the list and the packed
+// arrays. Every call on a GPU shares that GPU's array and leaves its contents behind, so calls
+// that overlap on one GPU race; each call writes every word it reads before reading it.
+// ----------------------------------------------------------------------------------------------
+namespace {
+
+constexpr long kScratchTiles = kScratchRows / kWave + 2;
+constexpr long kOffBits = 0;
+constexpr long kOffRowCount = kOffBits + kScratchBitWords;
+constexpr long kOffRowAtom = kOffRowCount + kScratchRows;
+constexpr long kOffTileCount = kOffRowAtom + kScratchRows;
+constexpr long kOffTileFlags = kOffTileCount + kScratchTiles;
+constexpr long kOffTileOff = kOffTileFlags + kScratchTiles;
+constexpr long kOffResult = ((kOffTileOff + kScratchTiles + 63) / 64) * 64;  // 256-byte aligned
+constexpr long kOffState = kOffResult + 64;
+constexpr long kScratchInts = kOffState + 64;
+static_assert(sizeof(StepResult) <= 64 * sizeof(int), "step result slot");
+static_assert(kPackStateWords <= 64, "pack state slot");
+
+}  // namespace
+
+static __device__ __align__(256) int scratch[kScratchInts];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+int *scratch_ptr[kMaxDevices] = {};
+
+// The device address of this GPU's `scratch`: looked up once per device, with that device
+// current, on the first call there (host code must not pass the array's own name to a kernel).
+hipError_t scratch_address(int **out)
+{
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(scratch_mutex);
+  if (!scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    scratch_ptr[dev] = static_cast<int *>(p);
+  }
+  *out = scratch_ptr[dev];
+  return hipSuccess;
+}
+
+// The previous pack's live slot count as the bound of this pack's tail reset (the scan moves it
+// to kPrevLive); a kernel, not a memset, so the call can be captured in a graph.
+__global__ void k_set_live(int *state, int live)
+{
+  if (threadIdx.x == 0) state[kLive] = live;
+}
+
+}  // namespace
+
+hipError_t launch_pack_edges_noalloc(hipStream_t s, PackArgs a, int *senders, int *receivers,
+                                     unsigned char *mask, int *counts_out, int prev_live)
+{
+  int *base = nullptr;
+  if (hipError_t e = scratch_address(&base); e != hipSuccess) return e;
+  a.pitch = a.num_rows > 0 ? a.num_rows : 1;
+  a.words = (a.maxneighs + 31) / 32;
+  a.bits = reinterpret_cast<uint32_t *>(base + kOffBits);
+  a.row_count = base + kOffRowCount;
+  a.row_atom = base + kOffRowAtom;
+  a.tile_count = base + kOffTileCount;
+  a.tile_flags = base + kOffTileFlags;
+  int *tile_off = base + kOffTileOff;
+  auto *result = reinterpret_cast<StepResult *>(base + kOffResult);
+  int *state = base + kOffState;
+  constexpr int W = 4;
+  const int ntiles = (a.num_rows + kWave - 1) / kWave;
+  hipLaunchKernelGGL(k_set_live, dim3(1), dim3(64), 0, s, state, prev_live);
+  if (ntiles > 0)
+    hipLaunchKernelGGL(k_pack_count<W>, dim3(tile_grid(ntiles)), dim3(W * kWave), 0, s, a);
+  hipLaunchKernelGGL(k_tile_scan, dim3(1), dim3(1024), 0, s, a.tile_count, a.tile_flags, ntiles,
+                     a.max_edges, tile_off, result, state);
+  hipLaunchKernelGGL(k_pack_write<W>, dim3(tile_grid(ntiles > 0 ? ntiles : 1)), dim3(W * kWave),
+                     0, s, a, tile_off, senders, receivers, mask, result, state, counts_out);
+  return hipGetLastError();
 }
 
 }  // namespace lk

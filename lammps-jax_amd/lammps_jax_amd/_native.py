@@ -34,7 +34,7 @@ EXPORTED = (
     "lk_pack_compute", "lk_step_result", "lk_timing_enable", "lk_timing_read", "lk_edge_buffers",
     "lk_staging_buffers", "lk_model_buffers", "lk_edge_forces", "lk_neighbor_matrix",
     "lk_bundle_load", "lk_bundle_free",
-    "lk_bundle_contract", "lk_bundle_model", "lk_bundle_unit_style",
+    "lk_bundle_contract", "lk_bundle_model", "lk_bundle_unit_style", "lk_pack_edges_noalloc",
 )
 
 
@@ -157,6 +157,9 @@ def load() -> ctypes.CDLL:
     lib.lk_bundle_model.restype = ip
     lib.lk_bundle_unit_style.argtypes = [vp]
     lib.lk_bundle_unit_style.restype = ctypes.c_char_p
+    lib.lk_pack_edges_noalloc.argtypes = [pp(LkContract), vp, vp, vp, vp, vp, ctypes.c_long, ip,
+                                          ip, ip, ip, vp, vp, vp, vp, ip, ctypes.c_char_p, ip]
+    lib.lk_pack_edges_noalloc.restype = ip
     _lib = lib
     return lib
 
