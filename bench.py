@@ -202,10 +202,15 @@ def slots_inside_cutoff(sysm, lst, cutoff: float) -> int:
     return kept
 
 
-def lean_step(pj, eflag: bool = True, vflag: bool = True):
+def lean_step(pj, eflag: bool = True, vflag: bool = True, rebuild_every: int = 0):
     """One engine step as a C++ caller makes it: lk_pack_compute then lk_step_result, with the
     argument list bound once (ctypes calls, no torch dispatch). The forces add into f without a
-    clear in between: LAMMPS zeroes f in its own force_clear, outside the pair style."""
+    clear in between: LAMMPS zeroes f in its own force_clear, outside the pair style.
+
+    rebuild_every > 0: every that many steps (the first one included) the step is a list-rebuild
+    step, as LAMMPS signals it (neighbor->ago == 0; here lk_set_list_epoch): the library redoes
+    its once-per-list work (tile lists, incidence lists, matrix copy) inside that step. The list
+    itself is the same one (the engine's rebuild is not the pair style's time)."""
     import ctypes
 
     from lammps_jax_amd import _native as N
@@ -224,13 +229,23 @@ def lean_step(pj, eflag: bool = True, vflag: bool = True):
     ref = ctypes.byref(info)
     pack_compute, step_result = lib.lk_pack_compute, lib.lk_step_result
 
+    set_epoch = lib.lk_set_list_epoch
+    calls = [0]
+
     def step():
+        if rebuild_every > 0 and calls[0] % rebuild_every == 0:
+            pj.list_epoch += 1
+            if set_epoch(h, ctypes.c_long(pj.list_epoch)) != N.LK_OK:
+                raise N.LammpsJaxError(1, pj.h.error())
+            step.rebuilds += 1
+        calls[0] += 1
         if pack_compute(*args) != N.LK_OK or step_result(h, stream, ref) != N.LK_OK:
             raise N.LammpsJaxError(1, pj.h.error())
         if info.edge_overflow:
             raise N.LammpsJaxError(N.LK_ERR_CAPACITY, "LAMMPS-JAX edge capacity exceeded")
         return info
 
+    step.rebuilds = 0
     return step
 
 
@@ -243,6 +258,10 @@ def main() -> int:
     ap.add_argument("--layout", default="sparse-edge", choices=("sparse-edge", "neighbor-matrix"),
                     help="bundle input layout; neighbor-matrix times the steps between list "
                          "rebuilds (the matrix is copied on rebuilds only)")
+    ap.add_argument("--rebuild-every", type=int, default=12, metavar="STEPS",
+                    help="a list-rebuild step every STEPS steps in the timed loops (the 131k-atom "
+                         "NVE run at 600 K rebuilds its list 8 times in 100 steps); the library's "
+                         "once-per-list work runs inside those steps. 0: the list never changes")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--split-steps", type=int, default=20,
@@ -286,12 +305,15 @@ def main() -> int:
     for _ in range(args.warmup):
         info = step()
     torch.cuda.synchronize(dev)
+    step = lean_step(pj, rebuild_every=args.rebuild_every)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         info = step()
     torch.cuda.synchronize(dev)
     elapsed = time.perf_counter() - t0
-    print(f"[bench] timed {args.steps} steps in {elapsed:.4f}s", file=sys.stderr, flush=True)
+    rebuilds_timed = step.rebuilds
+    print(f"[bench] timed {args.steps} steps ({rebuilds_timed} list-rebuild steps) in "
+          f"{elapsed:.4f}s", file=sys.stderr, flush=True)
     # the same steps through the Python host mirror (PairJax.compute: f cleared by torch each
     # step, result wrapped in Python objects), reported beside the C-caller rate
     torch.cuda.synchronize(dev)
@@ -303,9 +325,10 @@ def main() -> int:
     # stage timing: the same steps again with HIP events recorded around every launch on the
     # launch stream (lk_timing_*); kept out of the timed loop above, whose rate they would slow
     pj.h.timing_enable(True)
+    step_t = lean_step(pj, rebuild_every=args.rebuild_every)
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        pj.compute()
+        step_t()
     torch.cuda.synchronize(dev)
     events_ms = 1e3 * (time.perf_counter() - t0) / args.steps
     stages = pj.h.timing()
@@ -313,7 +336,7 @@ def main() -> int:
     # forces-only steps (eflag = vflag = 0), as most MD steps run between thermo outputs
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
-    step_f = lean_step(pj, eflag=False, vflag=False)
+    step_f = lean_step(pj, eflag=False, vflag=False, rebuild_every=args.rebuild_every)
     for _ in range(args.steps):
         step_f()
     torch.cuda.synchronize(dev)
@@ -338,7 +361,9 @@ def main() -> int:
     S = wl.precision
     words = (lst["maxneighs"] + 31) // 32
     stage_us = {k: 1e3 * tot / cnt for k, (tot, cnt) in stages.items()}
-    device_us = sum(stage_us.values())
+    # per step: once-per-list stages amortised over the steps they ran in
+    stage_us_step = {k: 1e3 * tot / args.steps for k, (tot, cnt) in stages.items()}
+    device_us = sum(stage_us_step.values())
     two = wl.accumulation != "onesided"
     matrix = args.layout == "neighbor-matrix"
     if matrix:  # the count reports the widest row; the rows keep the slots inside the cutoff
@@ -394,6 +419,8 @@ def main() -> int:
             "layout": args.layout,
             "step": "pack_atoms + pack_edges + model E/F/virial + f add + host readback "
                     "(lk_pack_compute + lk_step_result; f cleared by the engine, not timed)",
+            "list_rebuild_every": args.rebuild_every,
+            "list_rebuild_steps_timed": rebuilds_timed,
         },
         "roofline": {
             "bound": "hbm",
@@ -407,6 +434,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "nve": nve,
         "stages_us": {k: round(v, 2) for k, v in sorted(stage_us.items())},
+        "stages_us_per_step": {k: round(v, 2) for k, v in sorted(stage_us_step.items())},
         "stage_timing_ms_per_step": round(events_ms, 4),
         "device_us_per_step": round(device_us, 2),
         "python_loop_ms_per_step": round(python_loop_ms, 4),

@@ -22,7 +22,7 @@ CSRC = ROOT / "csrc"
 PKG = ROOT / "lammps_jax_amd"
 BUILD = ROOT / "_build"
 
-HIP_SOURCES = ["lk_api.hip", "lk_pack.hip", "lk_eam.hip", "lk_lj.hip", "lk_step.hip",
+HIP_SOURCES = ["lk_api.hip", "lk_pack.hip", "lk_eam.hip", "lk_lj.hip", "lk_step.hip", "lk_tiles.hip",
                "lk_twosided.hip"]
 # host-only parts of liblkhip.so; -ffp-contract=off keeps the spline coefficients of the setfl
 # reader rounding as the numpy restatement does

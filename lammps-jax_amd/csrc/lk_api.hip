@@ -57,7 +57,10 @@ void free_all(Handle &h)
                   h.d_result,    h.d_ghost_owner, h.d_ghost_off, h.d_ghost_list, h.d_done,
                   h.d_deg,       h.d_inc_loc,   h.d_inc_part,    h.d_inc_tmp,   h.d_inc,
                   h.d_rho_part,  h.d_epair,     h.d_pack_state,  h.d_inc_bit,   h.d_edge_f,
-                  h.d_matrix,    h.d_num_neighbors, h.d_identity, h.d_inc_len};
+                  h.d_matrix,    h.d_num_neighbors, h.d_identity, h.d_inc_len,
+                  h.tl.keys,     h.tl.keys_sorted, h.tl.rows_in, h.tl.order,  h.tl.sort_tmp,
+                  h.tl.atom,     h.tl.nn,       h.tl.uni,        h.tl.ucount,   h.tl.lid,
+                  h.tl.box};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);

@@ -158,6 +158,26 @@ struct Handle {
     }
   } inc_key;
 
+  // Tile lists of the fused one-sided float64 EAM step (lk_tiles.hip), built once per list: the
+  // list rows in Hilbert order of their positions cut into 128-row tiles, each tile's neighbour
+  // union (the atoms its list entries name) and the 16-bit union index of every list entry.
+  struct TileList {
+    uint32_t *keys = nullptr;       // [rows_cap] Hilbert key of each list row
+    uint32_t *keys_sorted = nullptr;
+    int *rows_in = nullptr;         // [rows_cap] 0..rows-1
+    int *order = nullptr;           // [rows_cap] list row at each tile position
+    void *sort_tmp = nullptr;       // radix-sort working memory
+    size_t sort_bytes = 0;
+    int *atom = nullptr;            // [tiles_cap * 128] atom of each position (-1: none)
+    int *nn = nullptr;              // [tiles_cap * 128] list slots of each position
+    int *uni = nullptr;             // [tiles_cap * union cap] union atoms, ascending
+    int *ucount = nullptr;          // [tiles_cap] union size; -1: past the cap
+    uint64_t *lid = nullptr;        // [tiles_cap * groups * 128] four 16-bit ids per word
+    unsigned long long *box = nullptr;  // [6] bounding box of the rows (ordered-integer doubles)
+    int rows_cap = 0, tiles_cap = 0, groups = 0;
+    IncKey key;                     // the list (and epoch) they were built from
+  } tl;
+
   size_t scalar_bytes() const { return contract.precision == LK_FLOAT64 ? 8 : 4; }
 };
 

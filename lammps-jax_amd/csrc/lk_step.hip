@@ -23,6 +23,7 @@
 
 #include "lk_eam_common.h"
 #include "lk_pack.h"
+#include "lk_tiles.h"
 
 namespace lk {
 
@@ -447,7 +448,18 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   } else {
     hipLaunchKernelGGL(k_clear_state, dim3(1), dim3(64), 0, s, h.d_pack_state);
   }
-  if (ntiles > 0) {
+  bool tiled = false;
+  if constexpr (EAM && !MATRIX && sizeof(S) == 8) {
+    // float64 EAM over an engine list: the pack and density over tile lists (lk_tiles.hip)
+    if (tile_step_eligible(h, num_rows, maxneighs)) {
+      if (hipError_t e1 = launch_step_tiles(h, s, x, type, ilist, numneigh, neighbors, stride,
+                                            num_rows, maxneighs, nlocal, nghost, a);
+          e1 != hipSuccess)
+        return e1;
+      tiled = true;
+    }
+  }
+  if (ntiles > 0 && !tiled) {
     StageTimer timer(h, s, "step_pack");
     const int grid = step_pack_grid<EAM>(ngroups, h.num_cus);
     hipLaunchKernelGGL((k_step_pack<S, EAM, MATRIX>), dim3(grid),

@@ -1,0 +1,155 @@
+"""GPU parity of the tile-list path of the fused float64 one-sided EAM step.
+
+The fused float64 EAM step orders the list rows along a Hilbert curve, cuts them into 128-row
+tiles and stages each tile's neighbour union in LDS; a tile whose union exceeds 1,280 atoms walks
+the engine's list from memory instead. These cases drive both kinds of tile in one step, a list
+handed over in scrambled row order, and steps that reuse the tile lists (positions moved, same
+list) next to steps after a rebuild. Bars: the reference's float64 ones (forces within 1e-11
+absolute, energy within 1e-13 per atom, virial within 1e-12 relative)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from lk_testutil import assert_energy, assert_forces, assert_virial
+from lammps_jax_amd import harness, systems
+from lammps_jax_amd.pair import PairJax
+
+pytestmark = pytest.mark.gpu
+
+TILE_ROWS, UNION_CAP, GRID_BITS = 128, 1280, 5
+
+
+def _hilbert_key(q: np.ndarray, bits: int) -> np.ndarray:
+    """J. Skilling's Hilbert index ("Programming the Hilbert curve", AIP Conf. Proc. 707, 381
+    (2004)) of integer cells q [n, 3], axes interleaved with axis 0 most significant."""
+    X = [q[:, 0].astype(np.int64), q[:, 1].astype(np.int64), q[:, 2].astype(np.int64)]
+    Q = 1 << (bits - 1)
+    while Q > 1:
+        P = Q - 1
+        for i in range(3):
+            hit = (X[i] & Q) != 0
+            t = np.where(hit, 0, (X[0] ^ X[i]) & P)
+            X[0] = np.where(hit, X[0] ^ P, X[0] ^ t)
+            if i:
+                X[i] = X[i] ^ t
+        Q >>= 1
+    X[1] ^= X[0]
+    X[2] ^= X[1]
+    t = np.zeros_like(X[0])
+    Q = 1 << (bits - 1)
+    while Q > 1:
+        t = np.where((X[2] & Q) != 0, t ^ (Q - 1), t)
+        Q >>= 1
+    key = np.zeros_like(X[0])
+    for b in range(bits - 1, -1, -1):
+        for i in range(3):
+            key = (key << 1) | (((X[i] ^ t) >> b) & 1)
+    return key
+
+
+def union_sizes(sysm, lst) -> np.ndarray:
+    """The union size of every tile, with the rows in the library's tile order (Hilbert keys of
+    a 32^3 grid over the rows' bounding box, stable sort)."""
+    rows = lst["inum"] + lst["gnum"]
+    ilist = lst["ilist"][:rows]
+    x = sysm.x[ilist]
+    lo, hi = x.min(0), x.max(0)
+    span = hi - lo
+    c = np.where(span > 0, np.floor((x - lo) / np.where(span > 0, span, 1.0) * (1 << GRID_BITS)), 0)
+    q = np.clip(c, 0, (1 << GRID_BITS) - 1).astype(np.int64)
+    order = np.argsort(_hilbert_key(q, GRID_BITS), kind="stable")
+    stride, nb, nn = lst["stride"], lst["neighbors"], lst["numneigh"]
+    sizes = []
+    for t0 in range(0, rows, TILE_ROWS):
+        ids = []
+        for i in ilist[order[t0:t0 + TILE_ROWS]]:
+            js = nb[np.arange(nn[i]) * stride + i] & 0x3FFFFFFF
+            ids.append(js)
+        sizes.append(len(np.unique(np.concatenate(ids))))
+    return np.asarray(sizes)
+
+
+def _long_cutoff_case(seed: int, scramble: bool):
+    """An fcc alloy with an 8 A cutoff (plus 1 A skin): about 220 list slots per row, so a
+    128-row tile names 1,100-1,500 distinct atoms, on both sides of the union cap."""
+    nx = ny = nz = 7
+    a = 3.8
+    box = np.array([nx * a, ny * a, nz * a])
+    rng = np.random.default_rng(seed)
+    x = systems.fcc_lattice(nx, ny, nz, a) + rng.normal(0.0, 0.1, size=(4 * nx * ny * nz, 3))
+    types = np.where(rng.random(len(x)) < 0.64, 1, 2).astype(np.int32)
+    tables = systems.synthetic_alloy_tables(cutoff=8.0)
+    wl = systems.Workload("eam_long_cutoff", "eam", 8, systems.wrap(x, box), types, box,
+                          tables["cutoff"], 1.0, 1, harness.LIST_FULL, 256, "onesided",
+                          tables=tables)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    if scramble:
+        n = lst["inum"]
+        lst["ilist"][:n] = lst["ilist"][:n][rng.permutation(n)]
+    return wl, sysm, lst
+
+
+def _oracle(wl, sysm, pj):
+    pos, sp = O.pack_atoms(sysm.x, sysm.type, sysm.nall, pj.max_atoms, 8)
+    s, r, m, _, _ = O.pack_neighbors(sysm.x, sysm.list, max_atoms=pj.max_atoms,
+                                     max_edges=pj.max_edges, nlocal=sysm.nlocal,
+                                     cutoff=wl.cutoff)
+    return O.eam_compute(wl.tables, pos, sp, ghost_owner=sysm.ghost_owner, nlocal=sysm.nlocal,
+                         nghost=sysm.nghost, senders=s, receivers=r, mask=m, mode=O.ONESIDED,
+                         precision=8)
+
+
+def _check(wl, sysm, pj, info, label):
+    ref = _oracle(wl, sysm, pj)
+    nl = sysm.nlocal
+    assert info.edge_overflow == 0, label
+    assert_energy(8, info.energy, ref["energy"], nl)
+    assert_forces(8, pj.forces()[:nl], ref["forces"][:nl])
+    assert_virial(8, info.virial, ref["virial"])
+
+
+@pytest.mark.parametrize("scramble", [False, True])
+def test_tiles_over_and_under_the_union_cap(gpu, scramble):
+    wl, sysm, lst = _long_cutoff_case(seed=21, scramble=scramble)
+    assert lst["maxneighs"] <= 256, lst["maxneighs"]
+    sizes = union_sizes(sysm, lst)
+    over = int((sizes > UNION_CAP).sum())
+    print(f"tile case scramble={scramble} nall={sysm.nall} maxneighs={lst['maxneighs']} "
+          f"tiles={len(sizes)} over_cap={over}", flush=True)
+    # the case exercises both the staged tiles and the ones that gather from memory
+    assert 0 < over < len(sizes)
+    pj = PairJax(sysm, ("eam", wl.tables), precision=8, accumulation="onesided",
+                 edges_per_atom=256)
+    _check(wl, sysm, pj, pj.compute(), "first step")
+
+
+def test_tile_lists_reused_until_the_list_changes(gpu):
+    """Positions move between steps while the list stays (the tile lists are reused: same rows,
+    same unions, new coordinates), then the engine rebuilds and the tiles follow the new list."""
+    wl = systems.make_workload("eam_alloy_131k", cells=(6, 6, 6), seed=5)
+    sysm = wl.system()
+    sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    pj = PairJax(sysm, ("eam", wl.tables), precision=8, accumulation="onesided")
+    _check(wl, sysm, pj, pj.compute(), "step 0")
+    rng = np.random.default_rng(3)
+    for step in (1, 2):
+        # a small displacement of every atom (owned and ghost images alike), list kept
+        d = rng.normal(0.0, 0.02, size=(sysm.nlocal, 3))
+        x = sysm.x.copy()
+        x[:sysm.nlocal] += d
+        x[sysm.nlocal:] += d[sysm.ghost_owner]
+        sysm.x = x
+        pj.x.copy_(pj.torch.from_numpy(x).to(pj.device))
+        print(f"tile reuse step {step}", flush=True)
+        _check(wl, sysm, pj, pj.compute(), f"step {step} (list kept)")
+    # the engine reneighbours: new positions, new ghosts, new list
+    moved = systems.wrap(sysm.x[:sysm.nlocal], wl.box)
+    sysm2 = harness.System(moved, sysm.type[:sysm.nlocal], wl.box, wl.cutghost)
+    sysm2.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    pj.rebind(sysm2)
+    print("tile rebuild step", flush=True)
+    _check(wl, sysm2, pj, pj.compute(), "after the rebuild")
