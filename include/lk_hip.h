@@ -260,6 +260,19 @@ int lk_bundle_model(const lk_bundle *b, int *kind, lk_eam_tables *eam, lk_lj_par
                     int *accumulation);
 const char *lk_bundle_unit_style(const lk_bundle *b);
 
+/*
+ * A DYNAMO setfl potential (.eam.alloy) read from text in memory, the host side of
+ * `pair_coeff * * file.eam.alloy`: replaces lammps_jax.eam.load_setfl (python/lammps_jax/eam.py:
+ * 174-227, with PairEAM::interpolate's coefficients, eam.py:115-135). The text is what the file
+ * holds (the caller decompresses); `source` names it in error messages (status LK_ERR_ARGUMENT,
+ * e.g. "<source>: 3 unparsed trailing values"). The result is an eam/alloy lk_bundle with no
+ * contract: lk_bundle_model gives its tables, lk_bundle_element the name and mass of element
+ * `index` (LK_ERR_ARGUMENT past the last one); free it with lk_bundle_free.
+ */
+int lk_setfl_parse(const char *text, long len, const char *source, lk_bundle **out, char *err,
+                   int errlen);
+int lk_bundle_element(const lk_bundle *b, int index, char *name, int name_len, double *mass);
+
 /* Device pointers of the handle's buffers (for tests and for engines that read them). */
 int lk_edge_buffers(lk_handle *h, int **senders, int **receivers, unsigned char **mask);
 int lk_staging_buffers(lk_handle *h, void **atoms, int **species);

@@ -183,10 +183,10 @@ void interpolate(const double *f, int n, double *coef)
 
 // DYNAMO setfl (eam.py:174-227): 3 comment lines, then whitespace-separated tokens: element
 // count and names, the grid (nrho drho nr dr cutoff), per element a 4-token header (Z, mass,
-// lattice constant, lattice) with F(rho) and rho(r), then r*phi for pairs (i, j <= i).
-void load_setfl(lk_bundle &b, const std::string &path)
+// lattice constant, lattice) with F(rho) and rho(r), then r*phi for pairs (i, j <= i). `path`
+// names the source in messages.
+void parse_setfl(lk_bundle &b, const std::string &text, const std::string &path)
 {
-  const std::string text = read_text(path, "setfl file");
   size_t pos = 0;
   for (int line = 0; line < 3; ++line) {
     pos = text.find('\n', pos);
@@ -237,6 +237,11 @@ void load_setfl(lk_bundle &b, const std::string &path)
   if (k != tok.size())
     throw std::runtime_error(path + ": " + std::to_string(tok.size() - k) +
                              " unparsed trailing values");
+}
+
+void load_setfl(lk_bundle &b, const std::string &path)
+{
+  parse_setfl(b, read_text(path, "setfl file"), path);
 }
 
 std::string dir_of(const std::string &path)
@@ -458,5 +463,36 @@ int lk_bundle_model(const lk_bundle *b, int *kind, lk_eam_tables *eam, lk_lj_par
 }
 
 const char *lk_bundle_unit_style(const lk_bundle *b) { return b ? b->unit_style.c_str() : ""; }
+
+int lk_setfl_parse(const char *text, long len, const char *source, lk_bundle **out, char *err,
+                   int errlen)
+{
+  if (!out || !text || len < 0) {
+    set_error(err, errlen, "invalid setfl arguments");
+    return LK_ERR_ARGUMENT;
+  }
+  *out = nullptr;
+  auto *b = new lk_bundle();
+  b->kind = 1;
+  try {
+    parse_setfl(*b, std::string(text, static_cast<size_t>(len)), source ? source : "setfl");
+  } catch (const std::exception &e) {
+    set_error(err, errlen, e.what());
+    delete b;
+    return LK_ERR_ARGUMENT;
+  }
+  *out = b;
+  return LK_OK;
+}
+
+int lk_bundle_element(const lk_bundle *b, int index, char *name, int name_len, double *mass)
+{
+  if (!b || b->kind != 1 || index < 0 || index >= static_cast<int>(b->elements.size()))
+    return LK_ERR_ARGUMENT;
+  if (name && name_len > 0)
+    std::snprintf(name, static_cast<size_t>(name_len), "%s", b->elements[index].c_str());
+  if (mass) *mass = b->masses[static_cast<size_t>(index)];
+  return LK_OK;
+}
 
 }  // extern "C"

@@ -35,6 +35,7 @@ EXPORTED = (
     "lk_staging_buffers", "lk_model_buffers", "lk_edge_forces", "lk_neighbor_matrix",
     "lk_bundle_load", "lk_bundle_free",
     "lk_bundle_contract", "lk_bundle_model", "lk_bundle_unit_style", "lk_pack_edges_noalloc",
+    "lk_setfl_parse", "lk_bundle_element",
 )
 
 
@@ -157,6 +158,11 @@ def load() -> ctypes.CDLL:
     lib.lk_bundle_model.restype = ip
     lib.lk_bundle_unit_style.argtypes = [vp]
     lib.lk_bundle_unit_style.restype = ctypes.c_char_p
+    lib.lk_setfl_parse.argtypes = [ctypes.c_char_p, ctypes.c_long, ctypes.c_char_p, pp(vp),
+                                   ctypes.c_char_p, ip]
+    lib.lk_setfl_parse.restype = ip
+    lib.lk_bundle_element.argtypes = [vp, ip, ctypes.c_char_p, ip, pp(ctypes.c_double)]
+    lib.lk_bundle_element.restype = ip
     lib.lk_pack_edges_noalloc.argtypes = [pp(LkContract), vp, vp, vp, vp, vp, ctypes.c_long, ip,
                                           ip, ip, ip, vp, vp, vp, vp, ip, ctypes.c_char_p, ip]
     lib.lk_pack_edges_noalloc.restype = ip

@@ -1,107 +1,98 @@
-"""DYNAMO setfl (.eam.alloy) tables for the EAM model.
+"""DYNAMO setfl (.eam.alloy) potentials for the EAM model, read by the library's C++ reader.
 
-Mirrors the reference's table interface, python/lammps_jax/eam.py: load_setfl (174-227),
-spline_coefficients (115-135, PairEAM::interpolate) and pair_table_id (167-171). The tables are
-built on the host once per pair_coeff and uploaded to the device by lk_set_eam.
+The text goes to lk_setfl_parse (csrc/lk_bundle.cpp): the reader and the PairEAM::interpolate
+coefficient code that also serve a bundle's "eam_setfl" at pair_coeff, so the tables a host
+uploads and the tables a bundle carries come from one implementation. This module moves the text
+in and copies the tables out, in the layout of the reference's host tables
+(python/lammps_jax/eam.py:174-227): per element the embedding F(rho) and density rho(r) cubics,
+the r*phi cubics of the element pairs in file order, and the symmetric element-pair row index.
+It also writes setfl text, for synthetic potentials.
 """
 
 from __future__ import annotations
 
+import ctypes
 import gzip
 from pathlib import Path
 
 import numpy as np
 
+from . import _native as N
 
-def read_table_lines(path) -> list[str]:
-    opener = gzip.open if str(path).endswith(".gz") else open
-    with opener(path, "rt") as handle:
-        return handle.read().splitlines()
+_GZIP_MAGIC = b"\x1f\x8b"
 
 
-def spline_coefficients(table) -> np.ndarray:
-    """(n, 4) cubic coefficients: value(t) = c0 + t*(c1 + t*(c2 + t*c3)) in each interval.
-
-    Derivatives: 5-point interior stencil, 1st/2nd-order ends; the last row has c2 = c3 = 0.
-    """
-    f = np.asarray(table, dtype=np.float64)
-    n = f.size
-    d = np.empty(n)
-    d[0] = f[1] - f[0]
-    d[1] = 0.5 * (f[2] - f[0])
-    d[n - 2] = 0.5 * (f[n - 1] - f[n - 3])
-    d[n - 1] = f[n - 1] - f[n - 2]
-    m = np.arange(2, n - 2)
-    d[m] = ((f[m - 2] - f[m + 2]) + 8.0 * (f[m + 1] - f[m - 1])) / 12.0
-    step = f[1:] - f[:-1]
-    coef = np.zeros((n, 4))
-    coef[:, 0] = f
-    coef[:, 1] = d
-    coef[:-1, 2] = 3.0 * step - 2.0 * d[:-1] - d[1:]
-    coef[:-1, 3] = d[:-1] + d[1:] - 2.0 * step
-    return coef
+def read_text(path) -> str:
+    """The file's text; gzip members (by their magic bytes, whatever the name) are inflated."""
+    data = Path(path).read_bytes()
+    if data.startswith(_GZIP_MAGIC):
+        data = gzip.decompress(data)
+    return data.decode()
 
 
-def pair_table_id(a, b):
-    """Row of the pair table for elements a and b: lower triangle in file order."""
-    hi = np.maximum(a, b)
-    lo = np.minimum(a, b)
-    return hi * (hi + 1) // 2 + lo
+def _element_pair_rows(n_el: int) -> np.ndarray:
+    """[n_el, n_el] row of each element pair in the file's pair section, which lists the pairs
+    (a, b <= a) a-major; symmetric in a and b."""
+    rows = np.empty((n_el, n_el), dtype=np.int32)
+    row = 0
+    for a in range(n_el):
+        for b in range(a + 1):
+            rows[a, b] = rows[b, a] = row
+            row += 1
+    return rows
 
 
-def parse_setfl_text(lines: list[str], source: str = "setfl") -> dict:
-    """Parses setfl lines: 3 comment lines, element line, grid line, then per element a 4-token
-    header, F(rho) and rho(r), then r*phi for element pairs (i, j <= i) in file order."""
-    tokens = " ".join(lines[3:]).split()
-    n_elements = int(tokens[0])
-    elements = tokens[1:1 + n_elements]
-    pos = 1 + n_elements
-    nrho, drho, nr, dr, cutoff = tokens[pos:pos + 5]
-    nrho, nr = int(nrho), int(nr)
-    drho, dr, cutoff = float(drho), float(dr), float(cutoff)
-    pos += 5
-    masses, embedding, density, raw = [], [], [], {"F": [], "rho": [], "z2r": []}
-    for _ in range(n_elements):
-        masses.append(float(tokens[pos + 1]))
-        pos += 4
-        values = np.array(tokens[pos:pos + nrho], dtype=np.float64)
-        raw["F"].append(values)
-        embedding.append(spline_coefficients(values))
-        pos += nrho
-        values = np.array(tokens[pos:pos + nr], dtype=np.float64)
-        raw["rho"].append(values)
-        density.append(spline_coefficients(values))
-        pos += nr
-    pair = []
-    pair_index = np.zeros((n_elements, n_elements), dtype=np.int32)
-    for i in range(n_elements):
-        for j in range(i + 1):
-            pair_index[i, j] = pair_index[j, i] = len(pair)
-            values = np.array(tokens[pos:pos + nr], dtype=np.float64)
-            raw["z2r"].append(values)
-            pair.append(spline_coefficients(values))
-            pos += nr
-    if pos != len(tokens):
-        raise ValueError(f"{source}: {len(tokens) - pos} unparsed trailing values")
-    return {
-        "elements": elements,
-        "masses": masses,
-        "nrho": nrho,
-        "drho": drho,
-        "nr": nr,
-        "dr": dr,
-        "cutoff": cutoff,
-        "embedding": np.stack(embedding),
-        "density": np.stack(density),
-        "pair": np.stack(pair),
-        "pair_index": pair_index,
-        "raw": raw,
-    }
+def parse_setfl_text(text: str, source: str = "setfl") -> dict:
+    """Tables of a setfl potential given as text (ValueError with the reader's message when the
+    text is not one)."""
+    lib = N.load()
+    body = text.encode()
+    err = ctypes.create_string_buffer(512)
+    handle = ctypes.c_void_p()
+    rc = lib.lk_setfl_parse(body, len(body), str(source).encode(), ctypes.byref(handle), err,
+                            len(err))
+    if rc != N.LK_OK:
+        raise ValueError(err.value.decode())
+    try:
+        kind, accumulation, tabs = ctypes.c_int(), ctypes.c_int(), N.LkEamTables()
+        if lib.lk_bundle_model(handle, ctypes.byref(kind), ctypes.byref(tabs), None,
+                               ctypes.byref(accumulation)) != N.LK_OK:
+            raise ValueError(f"{source}: no eam/alloy tables")
+        n_el = tabs.n_el
+        name = ctypes.create_string_buffer(64)
+        mass = ctypes.c_double()
+        elements, masses = [], []
+        for e in range(n_el):
+            if lib.lk_bundle_element(handle, e, name, len(name), ctypes.byref(mass)) != N.LK_OK:
+                raise ValueError(f"{source}: element {e} missing")
+            elements.append(name.value.decode())
+            masses.append(mass.value)
+
+        def cubics(ptr, count, nodes):
+            flat = np.ctypeslib.as_array(ptr, shape=(count * nodes * 4,))
+            return flat.reshape(count, nodes, 4).copy()
+
+        n_pairs = n_el * (n_el + 1) // 2
+        out = {
+            "elements": elements, "masses": masses,
+            "nrho": tabs.nrho, "drho": tabs.drho, "nr": tabs.nr, "dr": tabs.dr,
+            "cutoff": tabs.cutoff,
+            "embedding": cubics(tabs.embedding, n_el, tabs.nrho),
+            "density": cubics(tabs.density, n_el, tabs.nr),
+            "pair": cubics(tabs.pair, n_pairs, tabs.nr),
+            "pair_index": _element_pair_rows(n_el),
+        }
+    finally:
+        lib.lk_bundle_free(handle)
+    # the cubics interpolate the file's node values: column 0 holds them exactly
+    out["raw"] = {"F": list(out["embedding"][:, :, 0]), "rho": list(out["density"][:, :, 0]),
+                  "z2r": list(out["pair"][:, :, 0])}
+    return out
 
 
 def load_setfl(path) -> dict:
-    """Parses a DYNAMO setfl file (optionally gzipped) into spline-ready tables."""
-    return parse_setfl_text(read_table_lines(path), source=str(path))
+    """Tables of a setfl file (optionally gzipped)."""
+    return parse_setfl_text(read_text(path), source=str(path))
 
 
 def format_setfl(elements, masses, nrho, drho, nr, dr, cutoff, F, rho, z2r,

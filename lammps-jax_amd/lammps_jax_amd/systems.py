@@ -102,7 +102,7 @@ def synthetic_alloy(seed: int = 2024, nr: int = 2000, nrho: int = 2000, cutoff: 
 def synthetic_alloy_tables(seed: int = 2024, **kwargs) -> dict:
     """The synthetic alloy as parsed spline tables (text round trip, like a file on disk)."""
     text = setfl_mod.format_setfl(**synthetic_alloy(seed, **kwargs))
-    return setfl_mod.parse_setfl_text(text.splitlines(), source="synthetic alloy")
+    return setfl_mod.parse_setfl_text(text, source="synthetic alloy")
 
 
 # --------------------------------------------------------------------------------------------

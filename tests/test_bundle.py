@@ -3,8 +3,9 @@
 The loader restates lammps_jax::load_bundle_file (cpp/lammps_jax_model.cpp:212-315): contract
 keys read by first match in the exporter's sorted JSON, defaults for keys older bundles lack, and
 the validation messages in the reference's order. Each rejection case below is one of the
-reference's checks, with the message the reference raises. The setfl tables a bundle names are
-checked against the numpy loader bit for bit and against what the spline construction fixes:
+reference's checks, with the message the reference raises. The setfl tables a bundle names (and
+the same C++ reader's tables through lk_setfl_parse) are checked bit for bit against the
+oracle's own setfl reader and coefficient code, and against what the spline construction fixes:
 the cubic of interval m ends at node m+1 with the slope of node m+1 (PairEAM::interpolate,
 eam.py:115-135), so a wrong stencil, sign or index fails here. No device calls."""
 
@@ -16,6 +17,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+import oracle as O
 from conftest import REPO
 from lammps_jax_amd import _native as N
 from lammps_jax_amd import setfl
@@ -55,19 +57,21 @@ def _load_error(path) -> str:
 # -- model tables -------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("name", ["tiny.eam.alloy", "CuZr.eam.alloy.gz"])
-def test_eam_bundle_tables_equal_setfl_loader(tmp_path, name):
+def test_eam_bundle_tables_equal_the_oracle(tmp_path, name):
     src = GOLDEN / name
     path = tmp_path / "eam.json"
-    ref = setfl.load_setfl(src)
+    ref = O.setfl_tables(setfl.read_text(src))
     write_bundle(path, kind="eam/alloy", max_atoms=1000, max_edges=64000,
                  cutoff=ref["cutoff"], setfl=src, n_species=len(ref["elements"]),
                  accumulation="onesided", comm_widths=[1])
     b = Bundle(path)
-    tabs = b.eam_tables()
-    for key in ("nrho", "drho", "nr", "dr", "cutoff"):
-        assert tabs[key] == ref[key]
-    for key in ("embedding", "density", "pair"):
-        np.testing.assert_array_equal(tabs[key], ref[key])
+    direct = setfl.load_setfl(src)
+    for tabs in (b.eam_tables(), direct):
+        for key in ("nrho", "drho", "nr", "dr", "cutoff"):
+            assert tabs[key] == ref[key]
+        for key in ("embedding", "density", "pair"):
+            np.testing.assert_array_equal(tabs[key], ref[key])
+    assert direct["elements"] == ref["elements"] and direct["masses"] == ref["masses"]
     kind, _, accum = b.model()
     assert kind == "eam" and accum == "onesided"
 

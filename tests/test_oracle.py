@@ -78,13 +78,18 @@ def test_setfl_rejects_trailing_values(tmp_path):
 # --------------------------------------------------------------------------------------------
 
 def test_spline_coefficients_three_ways_agree():
+    """The oracle's C and numpy restatements, and the library's reader (a one-element setfl
+    whose three tables are the same values), agree bit for bit."""
     rng = np.random.default_rng(3)
     f = np.cumsum(rng.normal(size=57))
     a = O.spline_coefficients(f)
     b = O.spline_coefficients_np(f)
-    c = setfl_mod.spline_coefficients(f)
+    text = setfl_mod.format_setfl(["X"], [1.0], f.size, 0.1, f.size, 0.1, 0.1 * (f.size - 1),
+                                  F=[f], rho=[f], z2r=[f])
+    t = setfl_mod.parse_setfl_text(text, source="random walk")
     np.testing.assert_array_equal(a, b)
-    np.testing.assert_array_equal(a, c)
+    for c in (t["embedding"][0], t["density"][0], t["pair"][0]):
+        np.testing.assert_array_equal(a, c)
 
 
 def test_spline_reproduces_cubics_on_interior_intervals():
