@@ -221,6 +221,56 @@ int lk_pack_compute(lk_handle *h, void *stream, const double *x, const int *type
                     int inum, int gnum, int maxneighs, int nlocal, int nghost, int flags,
                     double scale, double *f);
 
+/*
+ * The EAM model pass split at its exchanges, for engines that move ghost rows between ranks
+ * (EAM over packed edges, one-sided or half scheme; LK_ERR_UNSUPPORTED otherwise). Replaces the
+ * mid-program exchange of the reference's communicating bundles: the model program requests each
+ * exchange and PairJaxKokkos::service_model_comm runs LAMMPS' forward or reverse comm on the
+ * model's device rows (cpp/pair_jax_kokkos.cpp:444-469). Here the engine drives it:
+ *
+ *   lk_pack_atoms, lk_pack_edges      (as for lk_compute)
+ *   lk_model_density                  densities into the handle's rho rows: one-sided rows
+ *                                     complete, half ghost rows holding partial sums
+ *   for site = 0, 1, ... while lk_model_comm(site) == LK_OK:
+ *       forward: comm->forward_comm   rows[ghost] <- rows[owner]
+ *       reverse: comm->reverse_comm   rows[owner] += rows[ghost]
+ *     on `rows` (width scalars per atom at the contract precision), through the
+ *     lk_comm_* buffer calls below in the pair style's pack/unpack hooks
+ *   lk_model_force                    F' of every row from its density, the force sweep, energy
+ *                                     and virial into the step result (lk_step_result)
+ *
+ * The exchanges are the reference's (eam.py:316-317 for the half scheme: reverse, then forward;
+ * eam_pallas.py:337 for complete rows: forward). No ghost map is needed. lk_model_force takes
+ * the same nlocal and nghost as the density pass of the same pack (LK_ERR_STATE otherwise).
+ */
+int lk_model_density(lk_handle *h, void *stream, int nlocal, int nghost);
+int lk_model_comm(lk_handle *h, int site, int *forward, void **rows, int *width);
+int lk_model_force(lk_handle *h, void *stream, int nlocal, int nghost, int flags, double scale,
+                   double *f);
+
+/*
+ * LAMMPS comm buffers for model rows on the device: the pair style's
+ * pack_forward_comm_kokkos / unpack_forward_comm_kokkos / pack_reverse_comm_kokkos /
+ * unpack_reverse_comm_kokkos (cpp/pair_jax_kokkos.cpp:523-571, row functors cpp:247-318).
+ * rows: device [max_atoms][width] scalars at the contract precision; buf: device doubles,
+ * `slots` = ceil(width * scalar bytes / 8) per atom (the comm_forward / comm_reverse size the
+ * pair style declares, cpp:643-647), odd 4-byte tails zero-padded. sendlist: device row
+ * indices, each named once per call (one swap); indices outside max_atoms are skipped.
+ *   pack_forward:    buf[i] = rows[sendlist[i]]          (*size = n * slots)
+ *   unpack_forward:  rows[first + i] = buf[i]
+ *   pack_reverse:    buf[i] = rows[first + i]             (*size = n * slots)
+ *   unpack_reverse:  rows[sendlist[i]] += buf[i]          (the adjoint of the forward copy)
+ * Stream-ordered; `size` may be NULL.
+ */
+int lk_comm_pack_forward(lk_handle *h, void *stream, const void *rows, int width,
+                         const int *sendlist, int n, double *buf, int *size);
+int lk_comm_unpack_forward(lk_handle *h, void *stream, void *rows, int width, int first, int n,
+                           const double *buf);
+int lk_comm_pack_reverse(lk_handle *h, void *stream, const void *rows, int width, int first,
+                         int n, double *buf, int *size);
+int lk_comm_unpack_reverse(lk_handle *h, void *stream, void *rows, int width, const int *sendlist,
+                           int n, const double *buf);
+
 /* Synchronises the stream and returns energy, virial and the pack counts of the last step. */
 int lk_step_result(lk_handle *h, void *stream, lk_step_info *out);
 

@@ -23,7 +23,7 @@ PKG = ROOT / "lammps_jax_amd"
 BUILD = ROOT / "_build"
 
 HIP_SOURCES = ["lk_api.hip", "lk_pack.hip", "lk_eam.hip", "lk_lj.hip", "lk_step.hip", "lk_tiles.hip",
-               "lk_twosided.hip"]
+               "lk_twosided.hip", "lk_comm.hip"]
 # host-only parts of liblkhip.so; -ffp-contract=off keeps the spline coefficients of the setfl
 # reader rounding as the numpy restatement does
 HOST_SOURCES = ["lk_bundle.cpp"]

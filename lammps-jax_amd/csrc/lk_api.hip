@@ -70,6 +70,15 @@ void free_all(Handle &h)
 
 hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
 
+// Two-sided incidence lists come from the list slots unless the pack's filter depends on the
+// positions (unique boundary) or duplicates edges, or a validity-bit address would not fit in
+// 27 bits.
+bool incidence_from_list(const Handle &h)
+{
+  const long bit_words = static_cast<long>((h.list_maxneighs + 31) / 32) * h.contract.max_atoms;
+  return h.list_neighbors && !h.list_unique && !h.list_duplicate && bit_words < (1L << 27);
+}
+
 int ensure_bits(Handle &h, int maxneighs)
 {
   const int words = (maxneighs + 31) / 32;
@@ -201,6 +210,39 @@ const char *contract_problem(const lk_contract *c)
   if (c->newton == LK_NEWTON_OFF && c->newton_pair)
     return "LAMMPS-JAX bundle was exported for newton pair off; this run uses newton on";
   return nullptr;
+}
+
+int split_check(Handle &h, int nlocal, int nghost)
+{
+  if (h.model == 0) return fail(h, LK_ERR_STATE, "LAMMPS-JAX runtime is not initialized");
+  if (h.model != 1 || h.matrix || h.contract.edge_force || h.contract.pair_sum ||
+      (h.accum != LK_ACCUM_ONESIDED && h.accum != LK_ACCUM_HALF))
+    return fail(h, LK_ERR_UNSUPPORTED,
+                "the split model pass runs EAM over packed edges in the one-sided or half "
+                "scheme");
+  if (nlocal < 0 || nghost < 0) return fail(h, LK_ERR_ARGUMENT, "invalid compute arguments");
+  if (static_cast<long>(nlocal) + nghost > h.contract.max_atoms)
+    return fail(h, LK_ERR_CAPACITY, "LAMMPS-JAX atom capacity exceeded");
+  return LK_OK;
+}
+
+// A comm call moves n rows of `width` scalars; n is at most the atom capacity and the buffer's
+// n * slots doubles must be countable in int (the size the pack reports to LAMMPS).
+int comm_check(Handle &h, int width, int n, bool rows_ok, bool buf_ok)
+{
+  if (h.model == 0) return fail(h, LK_ERR_STATE, "LAMMPS-JAX runtime is not initialized");
+  if (width < 1 || width > (1 << 20) || n < 0 || n > h.contract.max_atoms ||
+      static_cast<long>(n) * lk::comm_slots(h, width) > static_cast<long>(INT_MAX))
+    return fail(h, LK_ERR_ARGUMENT, "invalid comm width or row count");
+  if (n > 0 && (!rows_ok || !buf_ok)) return fail(h, LK_ERR_ARGUMENT, "invalid comm arrays");
+  return LK_OK;
+}
+
+int comm_span_check(Handle &h, int first, int n)
+{
+  if (first < 0 || static_cast<long>(first) + n > h.contract.max_atoms)
+    return fail(h, LK_ERR_ARGUMENT, "comm rows outside the atom capacity");
+  return LK_OK;
 }
 
 }  // namespace
@@ -643,11 +685,7 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
                   "density fold");
     if ((flags & LK_VIRIAL) && h.contract.newton_pair && nlocal + nghost > 0 && !h.x_last)
       return fail(h, LK_ERR_STATE, "the f.r virial needs the positions of a prior pack");
-    // incidence lists from the list slots unless the pack's filter depends on the positions
-    // (unique boundary) or duplicates edges, or a validity-bit address would not fit 27 bits
-    const long bit_words = static_cast<long>((h.list_maxneighs + 31) / 32) * h.contract.max_atoms;
-    const bool from_list = h.list_neighbors && !h.list_unique && !h.list_duplicate &&
-                           bit_words < (1L << 27);
+    const bool from_list = incidence_from_list(h);
     if (h.contract.edge_force && h.model == 2) {
       e = lk::launch_edge_force(h, s, nlocal, nghost, flags, scale, f, h.x_last, false);
     } else {
@@ -876,6 +914,124 @@ int lk_model_buffers(lk_handle *w, void **rho, void **fp)
   if (!w) return LK_ERR_ARGUMENT;
   if (rho) *rho = w->h.d_rho;
   if (fp) *fp = w->h.d_fp;
+  return LK_OK;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Split model pass and the comm buffers (service_model_comm, cpp:444-469; the pair style's
+// pack/unpack_{forward,reverse}_comm_kokkos, cpp:523-571)
+// ---------------------------------------------------------------------------------------------
+
+int lk_model_density(lk_handle *w, void *stream, int nlocal, int nghost)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (int rc = split_check(h, nlocal, nghost)) return rc;
+  hipStream_t s = as_stream(stream);
+  hipError_t e;
+  if (h.accum == LK_ACCUM_ONESIDED) {
+    e = lk::launch_eam_onesided(h, s, nlocal, nghost, 1.0, nullptr, 0, lk::kPhaseDensity);
+  } else {
+    const bool from_list = incidence_from_list(h);
+    if (int rc = ensure_incidence(h, from_list ? 2L * h.list_rows * h.list_maxneighs : 0))
+      return rc;
+    e = lk::launch_two_sided(h, s, nlocal, nghost, 0, 1.0, nullptr, h.x_last, from_list,
+                             lk::FusedPack{}, lk::kPhaseDensity);
+  }
+  if (e != hipSuccess) return hip_fail(h, e, "model density");
+  h.split_serial = h.pack_serial;
+  h.split_nall = nlocal + nghost;
+  h.result_mirrored = false;
+  return LK_OK;
+}
+
+int lk_model_comm(lk_handle *w, int site, int *forward, void **rows, int *width)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (int rc = split_check(h, 0, 0)) return rc;
+  // one-sided rows are complete: forward only (eam_pallas.py:337, half_edges False); the half
+  // scheme leaves partial densities on ghost rows: reverse, then forward (eam.py:316-317)
+  const int sites = h.accum == LK_ACCUM_HALF ? 2 : 1;
+  if (site < 0 || site >= sites) return LK_ERR_ARGUMENT;
+  if (forward) *forward = (sites == 2 && site == 0) ? 0 : 1;
+  if (rows) *rows = h.d_rho;
+  if (width) *width = 1;
+  return LK_OK;
+}
+
+int lk_model_force(lk_handle *w, void *stream, int nlocal, int nghost, int flags, double scale,
+                   double *f)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (int rc = split_check(h, nlocal, nghost)) return rc;
+  if (!f) return fail(h, LK_ERR_ARGUMENT, "invalid compute arguments");
+  if (h.split_serial != h.pack_serial || h.split_nall != nlocal + nghost)
+    return fail(h, LK_ERR_STATE,
+                "lk_model_force needs this step's lk_model_density (same pack and atoms)");
+  if (!h.contract.newton_pair) flags &= ~LK_VIRIAL;  // cpp:733-736
+  if (h.accum == LK_ACCUM_HALF && (flags & LK_VIRIAL) && nlocal + nghost > 0 && !h.x_last)
+    return fail(h, LK_ERR_STATE, "the f.r virial needs the positions of a prior pack");
+  hipStream_t s = as_stream(stream);
+  hipError_t e;
+  if (h.accum == LK_ACCUM_ONESIDED)
+    e = lk::launch_eam_onesided(h, s, nlocal, nghost, scale, f, flags, lk::kPhaseForce);
+  else
+    e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, h.x_last,
+                             incidence_from_list(h), lk::FusedPack{}, lk::kPhaseForce);
+  if (e != hipSuccess) return hip_fail(h, e, "model force");
+  h.split_serial = -1;
+  h.result_mirrored = true;
+  return LK_OK;
+}
+
+int lk_comm_pack_forward(lk_handle *w, void *stream, const void *rows, int width,
+                         const int *sendlist, int n, double *buf, int *size)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (int rc = comm_check(h, width, n, rows && sendlist, buf != nullptr)) return rc;
+  hipError_t e = lk::launch_comm_pack_forward(h, as_stream(stream), rows, width, sendlist, n, buf);
+  if (e != hipSuccess) return hip_fail(h, e, "pack_forward_comm");
+  if (size) *size = n * lk::comm_slots(h, width);
+  return LK_OK;
+}
+
+int lk_comm_unpack_forward(lk_handle *w, void *stream, void *rows, int width, int first, int n,
+                           const double *buf)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (int rc = comm_check(h, width, n, rows != nullptr, buf != nullptr)) return rc;
+  if (int rc = comm_span_check(h, first, n)) return rc;
+  hipError_t e = lk::launch_comm_unpack_forward(h, as_stream(stream), rows, width, first, n, buf);
+  if (e != hipSuccess) return hip_fail(h, e, "unpack_forward_comm");
+  return LK_OK;
+}
+
+int lk_comm_pack_reverse(lk_handle *w, void *stream, const void *rows, int width, int first,
+                         int n, double *buf, int *size)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (int rc = comm_check(h, width, n, rows != nullptr, buf != nullptr)) return rc;
+  if (int rc = comm_span_check(h, first, n)) return rc;
+  hipError_t e = lk::launch_comm_pack_reverse(h, as_stream(stream), rows, width, first, n, buf);
+  if (e != hipSuccess) return hip_fail(h, e, "pack_reverse_comm");
+  if (size) *size = n * lk::comm_slots(h, width);
+  return LK_OK;
+}
+
+int lk_comm_unpack_reverse(lk_handle *w, void *stream, void *rows, int width, const int *sendlist,
+                           int n, const double *buf)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (int rc = comm_check(h, width, n, rows && sendlist, buf != nullptr)) return rc;
+  hipError_t e =
+      lk::launch_comm_unpack_reverse(h, as_stream(stream), rows, width, sendlist, n, buf);
+  if (e != hipSuccess) return hip_fail(h, e, "unpack_reverse_comm");
   return LK_OK;
 }
 

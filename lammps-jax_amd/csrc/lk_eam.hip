@@ -97,6 +97,18 @@ __global__ __launch_bounds__(W * TPB * 64) LK_EIGHT_WAVES void k_eam_density_row
   }
 }
 
+// F and F' of rows [first, last) from their densities (rows the engine's forward exchange filled
+// with their owner's density); no energy: the owner's row counts it.
+template <typename S>
+__global__ __launch_bounds__(256) void k_embed_rows(EamArgs<S> a, int first, int last)
+{
+  const int i = first + blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= last) return;
+  S F, Fp;
+  embed(a, clamp_species(static_cast<int>(a.atoms[i].w), a.n_el), a.rho[i], F, Fp);
+  a.fp[i] = Fp;
+}
+
 // Forward comm stand-in: ghost rows read their owner's F' (LAMMPS forward_comm on one rank).
 template <typename S>
 __global__ __launch_bounds__(256) void k_forward_rows(S *__restrict__ v,
@@ -290,11 +302,20 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
 
 template <typename S>
 static hipError_t eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
-                               double *f, int flags)
+                               double *f, int flags, int phase)
 {
   EamArgs<S> a = eam_args<S>(h, nlocal, scale, f);
   a.flags = flags;
   const int ntiles = (h.packed_rows + kWave - 1) / kWave;
+  if (phase == kPhaseForce) {
+    // the engine's forward exchange gave every ghost row its owner's density
+    if (nghost > 0) {
+      StageTimer timer(h, s, "embed_ghosts");
+      hipLaunchKernelGGL(k_embed_rows<S>, dim3((nghost + 255) / 256), dim3(256), 0, s, a, nlocal,
+                         nlocal + nghost);
+    }
+    return launch_eam_force(h, s, a, flags);
+  }
   if (ntiles > 0) {
     const int ngroups = (ntiles + kDensTPB - 1) / kDensTPB;
     const int grid = persistent_grid(ngroups, 2, h.num_cus);
@@ -302,6 +323,7 @@ static hipError_t eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
     hipLaunchKernelGGL((k_eam_density_rows<S, kDensW, kDensTPB>), dim3(grid),
                        dim3(kDensW * kDensTPB * kWave), 0, s, a, ngroups);
   }
+  if (phase == kPhaseDensity) return hipGetLastError();
   if (nghost > 0) {
     StageTimer timer(h, s, "forward_fp");
     hipLaunchKernelGGL(k_forward_rows<S>, dim3((nghost + 255) / 256), dim3(256), 0, s,
@@ -339,10 +361,11 @@ hipError_t launch_eam_force(Handle &h, hipStream_t s, EamArgs<float> a, int flag
 }
 
 hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
-                               double *f, int flags)
+                               double *f, int flags, int phase)
 {
-  if (h.contract.precision == LK_FLOAT64) return eam_onesided<double>(h, s, nlocal, nghost, scale, f, flags);
-  return eam_onesided<float>(h, s, nlocal, nghost, scale, f, flags);
+  if (h.contract.precision == LK_FLOAT64)
+    return eam_onesided<double>(h, s, nlocal, nghost, scale, f, flags, phase);
+  return eam_onesided<float>(h, s, nlocal, nghost, scale, f, flags, phase);
 }
 
 }  // namespace lk

@@ -79,6 +79,8 @@ struct Handle {
   int bits_words = 0;
   int packed_rows = 0;          // list rows of the last pack
   int pack_serial = 0;
+  int split_serial = -1;        // pack_serial of the last lk_model_density (split model pass)
+  int split_nall = -1;          // its nlocal + nghost
 
   // per-atom model state
   void *d_fp = nullptr;      // F'(rho) [max_atoms]
@@ -213,8 +215,14 @@ hipError_t launch_pack_edges(Handle &h, hipStream_t s, const double *x, const in
                              const int *numneigh, const int *neighbors, long stride, int num_rows,
                              int maxneighs, int nlocal, int duplicate, int half_edges,
                              int unique_boundary);
+// Phases of the EAM model pass. kPhaseAll runs it whole (the single-rank ghost map stands in for
+// the engine's exchange); kPhaseDensity stops after the densities (the handle's rho rows, ghost
+// partials included), and kPhaseForce starts from rho rows the engine has completed by its
+// exchange (every ghost row holding its owner's density): F' on every row, then the force sweep.
+enum ModelPhase { kPhaseAll = 0, kPhaseDensity = 1, kPhaseForce = 2 };
+
 hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
-                               double *f, int flags);
+                               double *f, int flags, int phase = kPhaseAll);
 hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
                               double *f, int flags, const FusedPack &pack = FusedPack{});
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles);
@@ -226,7 +234,18 @@ hipError_t launch_edge_force(Handle &h, hipStream_t s, int nlocal, int nghost, i
 
 hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
                             double scale, double *f, const double *x, bool from_list,
-                            const FusedPack &pack = FusedPack{});
+                            const FusedPack &pack = FusedPack{}, int phase = kPhaseAll);
+
+// LAMMPS comm buffers for model rows (lk_comm.hip): `slots` doubles per buffer row.
+int comm_slots(const Handle &h, int width);
+hipError_t launch_comm_pack_forward(Handle &h, hipStream_t s, const void *rows, int width,
+                                    const int *list, int n, double *buf);
+hipError_t launch_comm_unpack_forward(Handle &h, hipStream_t s, void *rows, int width, int first,
+                                      int n, const double *buf);
+hipError_t launch_comm_pack_reverse(Handle &h, hipStream_t s, const void *rows, int width,
+                                    int first, int n, double *buf);
+hipError_t launch_comm_unpack_reverse(Handle &h, hipStream_t s, void *rows, int width,
+                                      const int *list, int n, const double *buf);
 
 // The one-sided step's first two launches alone (atom records, then the pack without a model):
 // the pack of the two-sided schemes whose incidence lists come from the list slots. `out`

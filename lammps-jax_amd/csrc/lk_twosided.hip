@@ -1069,25 +1069,38 @@ static void use_pack(TwoSided &t, const FusedPack &pack)
 template <typename S, bool HALF>
 static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
                                 double scale, double *f, const double *x, bool from_list,
-                                const FusedPack &pack)
+                                const FusedPack &pack, int phase)
 {
   EamArgs<S> m = eam_args<S>(h, nlocal, scale, f);
   TwoSided t = two_sided_args(h, nlocal, nghost, x);
   use_pack(t, pack);
   if (from_list && h.list_bits_filter) t.inc_bit = h.d_inc_bit;
   m.flags = flags;
-  S *rho_part = static_cast<S *>(h.d_rho_part);
+  // Split passes exchange the handle's rho rows: the density sweep writes its partials there and
+  // the embedding reads them back completed (every row, ghosts included, holding its atom's
+  // whole density), so no ghost map folds or copies; only owned rows count their energy.
+  const bool split = phase != kPhaseAll;
+  S *rho_part = static_cast<S *>(split ? h.d_rho : h.d_rho_part);
+  if (split) {
+    t.ghost_off = nullptr;
+    t.owned_rows_only = 1;
+  }
   const int nblk = t.nblk > 0 ? t.nblk : 1;
   const int grid = grid_for(h, nblk, 1, 1);
-  if (t.nblk > 0) {
+  if (t.nblk > 0 && phase != kPhaseForce) {
     StageTimer timer(h, s, "eam_density");
     hipLaunchKernelGGL((k_eam_density_inc<S, HALF, false>), dim3(grid_for(h, nblk, 1, 2)),
                        dim3(kRowBlock), 0, s, m, t, rho_part, static_cast<S *>(nullptr));
   }
+  if (phase == kPhaseDensity) return hipGetLastError();
   if (t.nblk > 0) {
     StageTimer timer(h, s, "eam_embed");
-    hipLaunchKernelGGL((k_eam_embed_inc<S, HALF>), dim3(t.nblk), dim3(kWave), 0, s, m, t,
-                       static_cast<const S *>(rho_part), static_cast<const S *>(nullptr));
+    if (split)  // every row from its completed density
+      hipLaunchKernelGGL((k_eam_embed_inc<S, false>), dim3(t.nblk), dim3(kWave), 0, s, m, t,
+                         static_cast<const S *>(rho_part), static_cast<const S *>(nullptr));
+    else
+      hipLaunchKernelGGL((k_eam_embed_inc<S, HALF>), dim3(t.nblk), dim3(kWave), 0, s, m, t,
+                         static_cast<const S *>(rho_part), static_cast<const S *>(nullptr));
   }
   // one launch even with no rows: its last block writes the step result
   StageTimer timer(h, s, "eam_force");
@@ -1493,10 +1506,12 @@ hipError_t launch_edge_force(Handle &h, hipStream_t s, int nlocal, int nghost, i
 
 hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, int flags,
                             double scale, double *f, const double *x, bool from_list,
-                            const FusedPack &pack)
+                            const FusedPack &pack, int phase)
 {
   hipError_t e = hipSuccess;
-  if (from_list) {
+  if (phase == kPhaseForce) {
+    // the incidence lists are the ones this step's density pass used
+  } else if (from_list) {
     // once per list: the engine's epoch (or every step when it gives none) and the list's shape
     Handle::IncKey key;
     key.epoch = h.list_epoch;
@@ -1520,10 +1535,14 @@ hipError_t launch_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost, in
   const bool half = h.accum == LK_ACCUM_HALF;
   if (h.model == 1) {
     if (f64)
-      return half ? eam_two_sided<double, true>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack)
-                  : eam_two_sided<double, false>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack);
-    return half ? eam_two_sided<float, true>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack)
-                : eam_two_sided<float, false>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack);
+      return half ? eam_two_sided<double, true>(h, s, nlocal, nghost, flags, scale, f, x,
+                                                from_list, pack, phase)
+                  : eam_two_sided<double, false>(h, s, nlocal, nghost, flags, scale, f, x,
+                                                 from_list, pack, phase);
+    return half ? eam_two_sided<float, true>(h, s, nlocal, nghost, flags, scale, f, x, from_list,
+                                             pack, phase)
+                : eam_two_sided<float, false>(h, s, nlocal, nghost, flags, scale, f, x, from_list,
+                                              pack, phase);
   }
   if (f64) return lj_two_sided<double>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack);
   return lj_two_sided<float>(h, s, nlocal, nghost, flags, scale, f, x, from_list, pack);

@@ -35,7 +35,9 @@ EXPORTED = (
     "lk_staging_buffers", "lk_model_buffers", "lk_edge_forces", "lk_neighbor_matrix",
     "lk_bundle_load", "lk_bundle_free",
     "lk_bundle_contract", "lk_bundle_model", "lk_bundle_unit_style", "lk_pack_edges_noalloc",
-    "lk_setfl_parse", "lk_bundle_element",
+    "lk_setfl_parse", "lk_bundle_element", "lk_model_density", "lk_model_comm", "lk_model_force",
+    "lk_comm_pack_forward", "lk_comm_unpack_forward", "lk_comm_pack_reverse",
+    "lk_comm_unpack_reverse",
 )
 
 
@@ -163,6 +165,20 @@ def load() -> ctypes.CDLL:
     lib.lk_setfl_parse.restype = ip
     lib.lk_bundle_element.argtypes = [vp, ip, ctypes.c_char_p, ip, pp(ctypes.c_double)]
     lib.lk_bundle_element.restype = ip
+    lib.lk_model_density.argtypes = [vp, vp, ip, ip]
+    lib.lk_model_density.restype = ip
+    lib.lk_model_comm.argtypes = [vp, ip, pp(ip), pp(vp), pp(ip)]
+    lib.lk_model_comm.restype = ip
+    lib.lk_model_force.argtypes = [vp, vp, ip, ip, ip, dp, vp]
+    lib.lk_model_force.restype = ip
+    lib.lk_comm_pack_forward.argtypes = [vp, vp, vp, ip, vp, ip, vp, pp(ip)]
+    lib.lk_comm_pack_forward.restype = ip
+    lib.lk_comm_unpack_forward.argtypes = [vp, vp, vp, ip, ip, ip, vp]
+    lib.lk_comm_unpack_forward.restype = ip
+    lib.lk_comm_pack_reverse.argtypes = [vp, vp, vp, ip, ip, ip, vp, pp(ip)]
+    lib.lk_comm_pack_reverse.restype = ip
+    lib.lk_comm_unpack_reverse.argtypes = [vp, vp, vp, ip, vp, ip, vp]
+    lib.lk_comm_unpack_reverse.restype = ip
     lib.lk_pack_edges_noalloc.argtypes = [pp(LkContract), vp, vp, vp, vp, vp, ctypes.c_long, ip,
                                           ip, ip, ip, vp, vp, vp, vp, ip, ctypes.c_char_p, ip]
     lib.lk_pack_edges_noalloc.restype = ip

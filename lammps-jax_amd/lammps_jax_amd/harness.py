@@ -51,6 +51,12 @@ def _load() -> ctypes.CDLL:
     lib.lkh_build_list.restype = ip
     lib.lkh_error.argtypes = [vp]
     lib.lkh_error.restype = ctypes.c_char_p
+    lib.lkh_nswaps.argtypes = [vp]
+    lib.lkh_nswaps.restype = ip
+    lib.lkh_swap.argtypes = [vp, ip, ctypes.POINTER(ip)]
+    lib.lkh_swap.restype = ip
+    lib.lkh_swap_sendlist.argtypes = [vp, ip]
+    lib.lkh_swap_sendlist.restype = ctypes.POINTER(ctypes.c_int)
     _lib = lib
     return lib
 
@@ -94,6 +100,18 @@ class System:
     @property
     def nall(self) -> int:
         return self.nlocal + self.nghost
+
+    def swaps(self) -> list[tuple[np.ndarray, int]]:
+        """LAMMPS' ghost swaps on this one rank, in forward order: (sendlist, first) per swap;
+        the sendlist's rows (owned rows or ghosts of earlier swaps) arrive as rows first,
+        first + 1, ... A forward exchange runs them in order, a reverse one backwards."""
+        lib = _load()
+        out = []
+        for k in range(lib.lkh_nswaps(self._h)):
+            first = ctypes.c_int()
+            n = lib.lkh_swap(self._h, k, ctypes.byref(first))
+            out.append((_copy(lib.lkh_swap_sendlist(self._h, k), n, np.int32), first.value))
+        return out
 
     def update_ghosts(self, x_owned: np.ndarray) -> None:
         """Forward comm of positions: ghosts follow their owners with the image shift."""

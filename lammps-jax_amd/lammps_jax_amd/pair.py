@@ -217,6 +217,48 @@ def read_device(ptr: int, count: int, np_dtype) -> np.ndarray:
     return host
 
 
+class DeviceComm:
+    """LAMMPS' Kokkos comm of per-atom model rows on one rank, through the library's buffer calls.
+
+    The swaps are the harness's (Comm::borders): forward_comm runs them in order, packing the
+    swap's send list into the device buffer (pack_forward_comm_kokkos) and unpacking it as the
+    swap's received ghost rows (unpack_forward_comm_kokkos); reverse_comm runs them backwards,
+    packing the received rows (pack_reverse_comm_kokkos) and adding them into the sent rows
+    (unpack_reverse_comm_kokkos). On one rank the buffer goes straight from pack to unpack,
+    as LAMMPS does for a swap whose partner is the rank itself."""
+
+    def __init__(self, pair: "PairJax", system):
+        torch = pair.torch
+        self.pair = pair
+        self.swaps = [(torch.from_numpy(lst).to(pair.device), first, len(lst))
+                      for lst, first in system.swaps()]
+        n_max = max((n for _, _, n in self.swaps), default=0)
+        self.buf = torch.zeros(max(n_max, 1) * 16, dtype=torch.float64, device=pair.device)
+
+    def _buffer(self, n, width):
+        slots = -(-width * self.pair.contract.precision // 8)
+        if self.buf.numel() < max(n * slots, 1):
+            self.buf = self.pair.torch.zeros(n * slots, dtype=self.pair.torch.float64,
+                                             device=self.pair.device)
+        return self.buf.data_ptr()
+
+    def forward(self, rows: int, width: int) -> None:
+        lib, h, st = self.pair.h.lib, self.pair.h.ptr, self.pair.stream()
+        for sendlist, first, n in self.swaps:
+            buf = self._buffer(n, width)
+            self.pair.h.check(lib.lk_comm_pack_forward(h, st, rows, width, sendlist.data_ptr(),
+                                                       n, buf, None))
+            self.pair.h.check(lib.lk_comm_unpack_forward(h, st, rows, width, first, n, buf))
+
+    def reverse(self, rows: int, width: int) -> None:
+        lib, h, st = self.pair.h.lib, self.pair.h.ptr, self.pair.stream()
+        for sendlist, first, n in reversed(self.swaps):
+            buf = self._buffer(n, width)
+            self.pair.h.check(lib.lk_comm_pack_reverse(h, st, rows, width, first, n, buf, None))
+            self.pair.h.check(lib.lk_comm_unpack_reverse(h, st, rows, width, sendlist.data_ptr(),
+                                                         n, buf))
+
+
 class PairJax:
     """pair_style jax/kk + pair_coeff for one rank: device state, per-step compute.
 
@@ -393,6 +435,30 @@ class PairJax:
                           self.neighbors.data_ptr(), lst["stride"], lst["inum"], lst["gnum"],
                           lst["maxneighs"], nlocal)
         self.h.compute(st, nlocal, nghost, flags, self.scale, self.f.data_ptr())
+
+    def compute_split(self, comm, eflag=True, vflag=True) -> StepInfo:
+        """The model pass with the engine's exchanges between its phases (lk_model_density,
+        then every exchange lk_model_comm names through `comm` (a DeviceComm or anything with
+        forward(rows, width) / reverse(rows, width)), then lk_model_force) after the pack."""
+        s, lst = self.system, self.system.list
+        st = self.stream()
+        lib, h = self.h.lib, self.h.ptr
+        self.f.zero_()
+        flags = (N.LK_ENERGY if eflag else 0) | (N.LK_VIRIAL if vflag else 0)
+        self.h.pack_atoms(st, self.x.data_ptr(), self.type.data_ptr(), s.nall)
+        self.h.pack_edges(st, self.x.data_ptr(), self.ilist.data_ptr(), self.numneigh.data_ptr(),
+                          self.neighbors.data_ptr(), lst["stride"], lst["inum"], lst["gnum"],
+                          lst["maxneighs"], s.nlocal)
+        self.h.check(lib.lk_model_density(h, st, s.nlocal, s.nghost))
+        site = 0
+        forward, rows, width = ctypes.c_int(), ctypes.c_void_p(), ctypes.c_int()
+        while lib.lk_model_comm(h, site, ctypes.byref(forward), ctypes.byref(rows),
+                                ctypes.byref(width)) == N.LK_OK:
+            (comm.forward if forward.value else comm.reverse)(rows.value, width.value)
+            site += 1
+        self.h.check(lib.lk_model_force(h, st, s.nlocal, s.nghost, flags, self.scale,
+                                        self.f.data_ptr()))
+        return self.h.step_result(st)
 
     def pack(self, x=None) -> StepInfo:
         """pack_atoms + pack_edges alone (optionally at other positions), then the readback."""
