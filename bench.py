@@ -170,6 +170,30 @@ def calibrate_copy(mib: int) -> int:
     return 0
 
 
+def calibrate_gather(mib: int) -> int:
+    """Random gathers of known footprint for the PMC byte counters: a table of MIB MiB read in a
+    random row order, ten dispatches each of two row sizes. 128-byte rows: every row is one
+    whole 128-byte line read once, so a dispatch fetches the table (plus its int64 indices)
+    exactly once and writes it once. 32-byte rows (the size of a float64 atom record): four rows
+    share a line, so what the counter reads above the table size is lines fetched again after
+    eviction."""
+    import torch
+
+    for width in (16, 4):  # doubles per row: 128-byte and 32-byte rows
+        n = mib * (1 << 20) // (8 * width)
+        table = torch.arange(n * width, dtype=torch.float64, device="cuda:0").reshape(n, width)
+        idx = torch.randperm(n, device="cuda:0")
+        out = torch.empty_like(table)
+        for _ in range(10):
+            torch.index_select(table, 0, idx, out=out)
+        torch.cuda.synchronize()
+        print(json.dumps({"row_bytes": 8 * width, "rows": n, "table_bytes": n * 8 * width,
+                          "index_bytes": n * 8, "dispatches": 10}))
+        del table, idx, out
+        torch.cuda.empty_cache()
+    return 0
+
+
 def pmc_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` from the committed PMC summary, or None.
 
@@ -272,6 +296,9 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB ten times (scales the PMC "
                          "byte counters) and exit")
+    ap.add_argument("--calibrate-gather", type=int, default=0, metavar="MIB",
+                    help="only run random-order row gathers over a MIB MiB table (128-byte and "
+                         "32-byte rows, ten dispatches each) for the PMC byte counters and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one GPU per box); "
@@ -279,6 +306,8 @@ def main() -> int:
         return 2
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
+    if args.calibrate_gather:
+        return calibrate_gather(args.calibrate_gather)
 
     import torch
 
