@@ -39,14 +39,20 @@ def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: 
     (E = slots inside the cutoff; only the internal receivers are written)."""
     rec = 4 * S  # atom record: x, y, z, species
     if two_sided:
-        if stage == "inc_count":
-            return 9 * E + 8 * A
-        if stage == "inc_scan":
-            return 8 * A
-        if stage == "inc_fill":
-            return 9 * E + 8 * E + 8 * A
-        if stage == "inc_sort":
-            return 8 * E + 8 * E + 8 * E
+        # the list-built incidence lists (once per list): E in-entries sorted by atom
+        if stage == "inc_count":  # the list read, row counts and atom counts out
+            return 4 * entries + 8 * R + 8 * A
+        if stage == "inc_fill":  # the list read, E (atom, slot) pairs out
+            return 4 * entries + 8 * R + 8 * E
+        if stage == "inc_sort":  # radix passes of 8 key bits, each reading and writing the pairs
+            passes = -(-max(1, (2 * A).bit_length()) // 8)
+            return passes * 16 * E
+        if stage == "inc_scan":  # the out-entry prefix and the atom offsets
+            return 16 * A
+        if stage == "inc_place":  # out-entries from the list, in-entries from the sorted pairs
+            return 4 * entries + 8 * R + 8 * E + 8 * E + 4 * E + 8 * E
+        if stage == "inc_fold":
+            return 8 * E + 4 * A
         if stage == "eam_density":
             return 8 * E + rec * A + S * A
         if stage == "eam_embed":
@@ -400,7 +406,8 @@ def main() -> int:
     sb_kw = dict(R=R, A=A, N=N, E=E, entries=lst["entries"], S=S, words=words, two_sided=two,
                  matrix=matrix)
     kernel_stages = {k: v for k, v in stage_us.items() if stage_bytes(k, **sb_kw) > 0}
-    dom = max(kernel_stages, key=kernel_stages.get)
+    # the kernel that takes most of a step (once-per-list stages by their share per step)
+    dom = max(kernel_stages, key=lambda k: stage_us_step[k])
     dom_bytes = stage_bytes(dom, **sb_kw)
     achieved = dom_bytes / (stage_us[dom] * 1e-6) / 1e9
     sb = survey_bytes(R=R, A=A, N=N, E=E, entries=lst["entries"], S=S)

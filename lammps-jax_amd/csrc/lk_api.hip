@@ -60,7 +60,8 @@ void free_all(Handle &h)
                   h.d_matrix,    h.d_num_neighbors, h.d_identity, h.d_inc_len,
                   h.tl.keys,     h.tl.keys_sorted, h.tl.rows_in, h.tl.order,  h.tl.sort_tmp,
                   h.tl.atom,     h.tl.nn,       h.tl.uni,        h.tl.ucount,   h.tl.lid,
-                  h.tl.box};
+                  h.tl.box,      h.d_sort_keys, h.d_sort_vals,   h.d_sort_tmp,  h.d_sort_rows,
+                  h.d_sort_pre};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -109,13 +110,13 @@ int ensure_incidence(Handle &h, long entries = 0)
   if (!h.d_deg) {
     fresh = true;
     const long chunks = (A + 1 + 4095) / 4096;
-    if ((e = dalloc(&h.d_deg, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence counts)");
+    if ((e = dalloc(&h.d_deg, A + 2)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence counts)");
     if ((e = dalloc(&h.d_inc_loc, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence offsets)");
     if ((e = dalloc(&h.d_inc_part, chunks)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence chunks)");
     if ((e = dalloc(&h.d_inc_len, A + 1)) != hipSuccess) return hip_fail(h, e, "hipMalloc(incidence lengths)");
     if ((e = hipMalloc(&h.d_rho_part, A * h.scalar_bytes())) != hipSuccess) return hip_fail(h, e, "hipMalloc(rho partials)");
     if ((e = hipMalloc(&h.d_epair, A * h.scalar_bytes())) != hipSuccess) return hip_fail(h, e, "hipMalloc(pair energy)");
-    if ((e = hipMemset(h.d_deg, 0, sizeof(int) * (A + 1))) != hipSuccess) return hip_fail(h, e, "hipMemset(incidence counts)");
+    if ((e = hipMemset(h.d_deg, 0, sizeof(int) * (A + 2))) != hipSuccess) return hip_fail(h, e, "hipMemset(incidence counts)");
   }
   const long need = entries > 2L * h.contract.max_edges ? entries : 2L * h.contract.max_edges;
   // an incidence entry keeps the other atom in 30 bits (side and pair flags above it)

@@ -117,7 +117,7 @@ struct Handle {
   std::map<std::string, std::pair<double, long>> stage_ms;
 
   // incidence lists of the two-sided schemes (lk_twosided.hip), allocated on first use
-  int *d_deg = nullptr;         // [max_atoms + 1] incident-edge counts, zero between steps
+  int *d_deg = nullptr;         // [max_atoms + 2] per-atom counts of the incidence builds
   int *d_inc_loc = nullptr;     // [max_atoms + 1] offsets within each scan chunk
   int *d_inc_part = nullptr;    // [chunks] chunk offsets
   uint32_t *d_inc_tmp = nullptr;  // [2 max_edges] (edge << 1 | side), unsorted
@@ -138,6 +138,17 @@ struct Handle {
   bool list_bits_filter = true;    // list-built incidence filtered by the pack's validity bits
   uint32_t *d_inc_bit = nullptr;  // [capacity] validity-bit address of each list-built entry
   long inc_cap = 0;               // capacity of d_inc_tmp / d_inc / d_inc_bit (entries)
+  // the list-built incidence lists' in-entries sorted by atom: keys and values before and after
+  // the radix sort, the row counts and offsets, the out-entry prefix over atoms, and the
+  // memory of the scans and the sort
+  uint32_t *d_sort_keys = nullptr;  // [sort_cap] 2 arrays
+  uint32_t *d_sort_vals = nullptr;  // [sort_cap] 2 arrays
+  int *d_sort_rows = nullptr;       // [2 (rows_cap + 1)] row counts, row offsets
+  int *d_sort_pre = nullptr;        // [max_atoms + 2] out-entries of the atoms below
+  void *d_sort_tmp = nullptr;
+  long sort_cap = 0;
+  long sort_rows_cap = 0;
+  size_t sort_tmp_bytes = 0;
   // the neighbour list of the last lk_pack_edges: the two-sided incidence lists are built from
   // its slots once per list (lk_set_list_epoch) and filtered each step by the pack's bits
   const int *list_ilist = nullptr;

@@ -23,6 +23,10 @@
 //            edge with the side in the top bit (side 1: this atom is the receiver)
 //   sweeps   16 lanes per atom walk the sorted segment; a fixed butterfly sums the lanes.
 
+#include <algorithm>
+
+#include <hipcub/hipcub.hpp>
+
 #include "lk_eam_common.h"
 
 namespace lk {
@@ -273,76 +277,223 @@ __device__ __forceinline__ uint32_t slot_bit(const ListArgs &L, int ii, int jj)
          static_cast<uint32_t>(jj & 31);
 }
 
-// One thread per row: the row's kept slots count once on its own atom, and once on each
-// neighbour (deg was cleared before).
-__global__ __launch_bounds__(256) void k_inc_list_count(ListArgs L)
-{
-  const int ii = blockIdx.x * blockDim.x + threadIdx.x;
-  if (ii >= L.rows) return;
-  int nn;
-  const int i = list_row(L, ii, nn);
-  if (i < 0) return;
-  int out = 0;
-  for (int jj = 0; jj < nn; ++jj) {
-    int j;
-    if (!list_neighbor(L, i, jj, j)) continue;
-    ++out;
-    atomicAdd(&L.deg[j], 1);
-  }
-  if (out) atomicAdd(&L.deg[i], out);
-}
-
-// One thread per row: out-entries in slot order at the front of the row atom's list; each
-// in-entry's key (f << 1 | 1) into the neighbour's in-part, counting its deg down (deg ends at
-// the out-count, which the sort reads).
-__global__ __launch_bounds__(256) void k_inc_list_fill(ListArgs L)
-{
-  const int ii = blockIdx.x * blockDim.x + threadIdx.x;
-  if (ii >= L.rows) return;
-  int nn;
-  const int i = list_row(L, ii, nn);
-  if (i < 0) return;
-  const int b = inc_off(L.loc, L.part, i);
-  int k = 0;
-  for (int jj = 0; jj < nn; ++jj) {
-    int j;
-    if (!list_neighbor(L, i, jj, j)) continue;
-    L.inc[b + k] = j;
-    L.inc_bit[b + k] = slot_bit(L, ii, jj);
-    ++k;
-    const uint32_t f = static_cast<uint32_t>(jj) * static_cast<uint32_t>(L.rows) +
-                       static_cast<uint32_t>(ii);
-    const int pj = inc_off(L.loc, L.part, j) + atomicSub(&L.deg[j], 1) - 1;
-    L.tmp[pj] = (f << 1) | 1u;
-  }
-}
-
-// Plain scheme only, one wave per atom, between fill and sort. An in-entry (row i names atom a)
-// whose reverse slot is one of a's out-entries (a's row names i) gives a the same pair force:
-// the two slots pass the pack's distance filter together (r^2 is the same sum of the negated
-// differences), and a's plain-scheme share of edge i -> a, -g = coef (x_i - x_a), equals that of
-// a -> i (coef depends on r only). Such an in-entry is dropped (its key set to all ones, which
-// the sort leaves out) and the out-entry marked (bit 30), and the sweeps weigh the out-entry by
-// the ends whose rows count. Each owned pair is then evaluated once per end instead of twice.
+// An in-entry (row i names atom a) whose reverse slot is one of a's out-entries (a's row names
+// i) gives a the same pair force in the plain scheme: the two slots pass the pack's distance
+// filter together (r^2 is the same sum of the negated differences), and a's plain-scheme share of
+// edge i -> a, -g = coef (x_i - x_a), equals that of a -> i (coef depends on r only). Such an
+// in-entry is dropped and the out-entry marked (kIncPaired), and the sweeps weigh the out-entry
+// by the ends whose rows count. Each owned pair is then evaluated once per end instead of twice.
 constexpr uint32_t kIncPaired = 1u << 30;
 constexpr uint32_t kIncAtom = 0x3FFFFFFFu;
 
-__global__ __launch_bounds__(256) void k_inc_list_fold(ListArgs L, int nsort)
+// ---------------------------------------------------------------------------------------------
+// The list-built incidence lists by one stable radix sort (once per list)
+// ---------------------------------------------------------------------------------------------
+// An atom's list is its out-entries (its own row's kept slots, in slot order) followed by its
+// in-entries (the kept slots of other rows that name it). The out-entries need no sorting: the
+// row's thread writes them. The in-entries are the kept slots keyed by the atom they name,
+// compacted row by row (row ii's slots in slot order, rows in list order) and radix-sorted by
+// that key; the sort is stable, so each atom's in-entries keep that row-major order: a
+// deterministic list without an atomic. With out[a] the out-entries of atom a and pre[a] their
+// prefix over the atoms below a, atom a's list starts at pre[a] + (in-entries of the atoms below
+// a: the sorted keys' lower bound of a), and the in-entry at sorted position p lands at
+// p + pre[a + 1].
+
+// One wave per 64-row tile (four per block): each lane counts its row's kept slots (the row
+// atom's out-entries); tilecnt[tile] = the tile's total, tilecnt[ntiles] = 0 so the scan's total
+// lands in the last offset.
+__global__ __launch_bounds__(256) void k_inc_tiles_count(ListArgs L, int ntiles,
+                                                         int *__restrict__ tilecnt)
+{
+  const int tile = blockIdx.x * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (tile > ntiles) return;  // whole wave
+  const int ii = tile * kWave + lane;
+  int c = 0;
+  if (tile < ntiles && ii < L.rows) {
+    int nn;
+    const int i = list_row(L, ii, nn);
+    if (i >= 0) {
+#pragma unroll 4
+      for (int jj = 0; jj < nn; ++jj) {
+        int j;
+        c += list_neighbor(L, i, jj, j) ? 1 : 0;
+      }
+      L.deg[i] = c;
+    }
+  }
+  const int tot = wave_sum(c);
+  if (lane == 0) tilecnt[tile] = tot;
+}
+
+// The in-entry keys (the atom a kept slot names) and values (the slot id f = jj * rows + ii),
+// tile by tile from the tile's offset, slot-major inside the tile: at each slot the wave's kept
+// entries are one contiguous run (ballot + rank), so the stores coalesce.
+__global__ __launch_bounds__(256) void k_inc_tiles_emit(ListArgs L, int ntiles,
+                                                        const int *__restrict__ tileoff,
+                                                        uint32_t *__restrict__ keys,
+                                                        uint32_t *__restrict__ vals)
+{
+  const int tile = blockIdx.x * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (tile >= ntiles) return;  // whole wave
+  const int ii = tile * kWave + lane;
+  int nn = 0, i = -1;
+  if (ii < L.rows) i = list_row(L, ii, nn);
+  const int nmax = wave_max_int(nn);
+  int cursor = tileoff[tile];
+  for (int jj = 0; jj < nmax; ++jj) {
+    int j = 0;
+    const bool kept = jj < nn && list_neighbor(L, i, jj, j);
+    const uint64_t M = wave_ballot(kept);
+    if (kept) {
+      const int q = cursor + lanes_below(M);
+      keys[q] = static_cast<uint32_t>(j);
+      vals[q] = static_cast<uint32_t>(jj) * static_cast<uint32_t>(L.rows) +
+                static_cast<uint32_t>(ii);
+    }
+    cursor += __popcll(M);
+  }
+}
+
+// first sorted position of key `k` (keys ascending, n entries)
+__device__ __forceinline__ int lower_bound_key(const uint32_t *keys, int n, uint32_t k)
+{
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = lo + ((hi - lo) >> 1);
+    if (keys[mid] < k) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// list offsets of atoms 0 .. atoms (inclusive); part[] stays zero (absolute offsets)
+__global__ __launch_bounds__(256) void k_inc_atoms_loc(const uint32_t *__restrict__ keys, int n,
+                                                       const int *__restrict__ pre, int atoms,
+                                                       int *__restrict__ loc)
+{
+  const int a = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a > atoms) return;
+  loc[a] = pre[a] + lower_bound_key(keys, n, static_cast<uint32_t>(a));
+}
+
+// out-entries, one thread per row: the neighbour and the slot's validity-bit address
+__global__ __launch_bounds__(256) void k_inc_rows_place(ListArgs L)
+{
+  const int ii = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ii >= L.rows) return;
+  int nn;
+  const int i = list_row(L, ii, nn);
+  if (i < 0) return;
+  int q = L.loc[i];
+  for (int jj = 0; jj < nn; ++jj) {
+    int j;
+    if (!list_neighbor(L, i, jj, j)) continue;
+    L.inc[q] = j;
+    L.inc_bit[q] = slot_bit(L, ii, jj);
+    ++q;
+  }
+}
+
+// Out-entries through LDS, one wave (block) per 64-row tile: each lane stages its row's kept
+// neighbours (and their slot numbers) in LDS, a row to `pitch` entries (odd: no bank conflicts),
+// then the wave writes the rows one after another, 64 consecutive entries per store. The list is
+// read slot-major and the lists written atom-major, both coalesced. Eight list slots per lane are
+// loaded before any is used, so eight loads of each wave are in flight.
+__global__ __launch_bounds__(kWave) void k_inc_tiles_place(ListArgs L, int ntiles, int pitch)
+{
+  extern __shared__ int stage[];  // [64][pitch] neighbours, then [64][pitch] slot numbers (u8)
+  const int tile = blockIdx.x;
+  const int lane = threadIdx.x;
+  if (tile >= ntiles) return;
+  const int ii = tile * kWave + lane;
+  int nn = 0, i = -1;
+  if (ii < L.rows) i = list_row(L, ii, nn);
+  int *sj = stage + lane * pitch;
+  unsigned char *sq = reinterpret_cast<unsigned char *>(stage + kWave * pitch) + lane * pitch;
+  const int base_own = i >= 0 ? L.loc[i] : 0;  // loaded with the list, not inside the row loop
+  int c = 0;
+  constexpr int kBatch = 8;
+  for (int j0 = 0; j0 < nn; j0 += kBatch) {
+    int raw[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q)
+      raw[q] = j0 + q < nn ? L.neighbors[static_cast<long>(j0 + q) * L.stride + i] : 0;
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int j = raw[q] & kNeighMask;
+      // list_neighbor's filter on the loaded entry
+      if (j0 + q < nn && j < L.max_atoms && !(L.half_filter && j < i)) {
+        sj[c] = j;
+        sq[c] = static_cast<unsigned char>(j0 + q);
+        ++c;
+      }
+    }
+  }
+  __syncthreads();
+  for (int r = 0; r < kWave; ++r) {
+    const int cr = __shfl(c, r, kWave);
+    if (cr == 0) continue;  // wave-uniform
+    const int base = __shfl(base_own, r, kWave);
+    const int *rj = stage + r * pitch;
+    const unsigned char *rq = reinterpret_cast<const unsigned char *>(stage + kWave * pitch) + r * pitch;
+    for (int k = lane; k < cr; k += kWave) {
+      L.inc[base + k] = rj[k];
+      L.inc_bit[base + k] = slot_bit(L, tile * kWave + r, rq[k]);
+    }
+  }
+}
+
+// keys of the sort's unused tail [kept, n) (kept read on the device): the pad key, above every atom
+__global__ __launch_bounds__(256) void k_inc_pad_keys(uint32_t *__restrict__ keys,
+                                                      const int *__restrict__ kept, int n,
+                                                      uint32_t pad)
+{
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p < n && p >= *kept) keys[p] = pad;
+}
+
+// in-entries, one thread per sorted position: the row atom with the side bit, and the slot's
+// validity-bit address
+__global__ __launch_bounds__(256) void k_inc_sorted_place(ListArgs L,
+                                                          const uint32_t *__restrict__ keys,
+                                                          const uint32_t *__restrict__ vals, int n,
+                                                          const int *__restrict__ pre)
+{
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n) return;
+  const uint32_t key = keys[p];
+  if (key >= static_cast<uint32_t>(L.max_atoms)) return;  // the pad of an unused tail
+  const int a = static_cast<int>(key);
+  const uint32_t f = vals[p];
+  const int ii = static_cast<int>(f % static_cast<uint32_t>(L.rows));
+  const int jj = static_cast<int>(f / static_cast<uint32_t>(L.rows));
+  const int q = p + pre[a + 1];
+  L.inc[q] = static_cast<int>(static_cast<uint32_t>(L.ilist[ii]) | (1u << 31));
+  L.inc_bit[q] = slot_bit(L, ii, jj);
+}
+
+// Plain scheme only, one wave per atom, after the lists are placed: the fold above (an in-entry
+// whose row atom is also one of the atom's out-entries is dropped and that out-entry marked),
+// then the kept in-entries close up in order; len[a] = the list's length.
+__global__ __launch_bounds__(256) void k_inc_list_fold_sorted(ListArgs L, int natoms)
 {
   const int atom = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  if (atom >= nsort) return;  // whole wave
+  if (atom >= natoms) return;  // whole wave
   const int b0 = inc_off(L.loc, L.part, atom);
   const int out = L.deg[atom];
   const int b = b0 + out;
   const int len = inc_off(L.loc, L.part, atom + 1) - b;
-  if (out == 0 || len == 0) return;
+  int kept = 0;
   for (int c0 = 0; c0 < len; c0 += kWave) {
     const bool mine = c0 + lane < len;
     int row_atom = -1;
+    uint32_t bit = 0;
     if (mine) {
-      const uint32_t f = L.tmp[b + c0 + lane] >> 1;
-      row_atom = L.ilist[static_cast<int>(f % static_cast<uint32_t>(L.rows))];
+      row_atom = static_cast<int>(static_cast<uint32_t>(L.inc[b + c0 + lane]) & kIncAtom);
+      bit = L.inc_bit[b + c0 + lane];
     }
     int hit = -1;
     for (int c1 = 0; c1 < out; c1 += kWave) {
@@ -353,58 +504,20 @@ __global__ __launch_bounds__(256) void k_inc_list_fold(ListArgs L, int nsort)
         if (hit < 0 && wm == row_atom) hit = c1 + m;
       }
     }
-    if (hit >= 0) {
+    // every lane has read the chunk (row_atom, bit) before any write below, and a kept entry
+    // moves to a position no later than its own, so the close-up is safe in place
+    if (mine && hit >= 0)
       L.inc[b0 + hit] = static_cast<int>(static_cast<uint32_t>(row_atom) | kIncPaired);
-      L.tmp[b + c0 + lane] = 0xFFFFFFFFu;
+    const bool keep = mine && hit < 0;
+    const uint64_t M = wave_ballot(keep);
+    if (keep) {
+      const int q = b + kept + lanes_below(M);
+      L.inc[q] = static_cast<int>(static_cast<uint32_t>(row_atom) | (1u << 31));
+      L.inc_bit[q] = bit;
     }
+    kept += __popcll(M);
   }
-}
-
-// One wave per atom: rank sort of the in-part by slot key (keys are distinct), so its store
-// order is ascending f whatever order the fill left; then the other atom (side bit set) and the
-// slot's validity-bit address. Entries the fold dropped (key all ones) are left out; the list's
-// length goes to len.
-__global__ __launch_bounds__(256) void k_inc_list_sort(ListArgs L, int nsort)
-{
-  const int atom = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
-  const int lane = threadIdx.x & (kWave - 1);
-  if (atom >= nsort) return;  // whole wave
-  const int b0 = inc_off(L.loc, L.part, atom);
-  const int out = L.deg[atom];
-  const int b = b0 + out;
-  const int len = inc_off(L.loc, L.part, atom + 1) - b;
-  int kept = 0;  // in-entries the fold left (all of them without folding)
-  for (int c0 = 0; c0 < len; c0 += kWave) {
-    const uint32_t v = c0 + lane < len ? L.tmp[b + c0 + lane] : 0xFFFFFFFFu;
-    kept += __popcll(wave_ballot(v != 0xFFFFFFFFu));
-  }
-  if (lane == 0) {
-    L.deg[atom] = 0;  // read by the whole wave above; zero again between builds
-    L.len[atom] = out + kept;
-  }
-  for (int c0 = 0; c0 < len; c0 += kWave) {
-    const bool mine = c0 + lane < len;
-    const uint32_t v = mine ? L.tmp[b + c0 + lane] : 0xFFFFFFFFu;
-    int rank = 0;
-    for (int c1 = 0; c1 < len; c1 += kWave) {
-      const uint32_t w = c1 + lane < len ? L.tmp[b + c1 + lane] : 0xFFFFFFFFu;
-#pragma unroll 16
-      for (int m = 0; m < kWave; ++m) {
-        // lane m's key broadcast through a scalar register (v_readlane), not the LDS crossbar
-        const uint32_t wm =
-            static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(w), m));
-        rank += wm < v ? 1 : 0;
-      }
-    }
-    if (mine && v != 0xFFFFFFFFu) {
-      const uint32_t f = v >> 1;
-      const int ii = static_cast<int>(f % static_cast<uint32_t>(L.rows));
-      const int jj = static_cast<int>(f / static_cast<uint32_t>(L.rows));
-      const int i = L.ilist[ii];
-      L.inc[b + rank] = static_cast<int>(static_cast<uint32_t>(i) | (1u << 31));
-      L.inc_bit[b + rank] = slot_bit(L, ii, jj);
-    }
-  }
+  if (lane == 0) L.len[atom] = out + kept;
 }
 
 template <typename T>
@@ -983,6 +1096,10 @@ static hipError_t build_incidence(Handle &h, hipStream_t s, int nall)
   return hipGetLastError();
 }
 
+// Lists of at most this many slots sort all of them (the unused tail padded) instead of reading
+// the kept count back: the read back would stall the stream for more than the padding costs.
+constexpr long kIncSortExact = 1L << 22;
+
 static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall, bool fold)
 {
   ListArgs L;
@@ -1003,33 +1120,126 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall, 
   L.len = h.d_inc_len;
   L.fold = fold ? 1 : 0;
   L.inc_bit = h.d_inc_bit;
-  const long slots = static_cast<long>(L.rows) * L.maxneighs;
-  const int row_blocks = (L.rows + 255) / 256;
+  const int rows = L.rows;
+  const int atoms = h.contract.max_atoms;
+  // at most one in-entry per list slot (ensure_incidence keeps rows * maxneighs within int)
+  const long slots_max = static_cast<long>(rows) * L.maxneighs;
+  // keys are atoms below max_atoms; the pad key (all ones in key_bits) sorts above them all
+  int key_bits = 1;
+  while ((1L << key_bits) <= atoms) ++key_bits;
+  const uint32_t pad = static_cast<uint32_t>((1L << key_bits) - 1);
+  hipError_t e = hipSuccess;
+  if (slots_max > h.sort_cap || rows + 1L > h.sort_rows_cap || !h.d_sort_pre) {
+    // the working arrays grow (rarely) for a larger list; a previous build may still use them
+    size_t b_scan_rows = 0, b_scan_atoms = 0, b_sort = 0;
+    const int cap = static_cast<int>(slots_max > 0 ? slots_max : 1);
+    e = hipcub::DeviceScan::ExclusiveSum(nullptr, b_scan_rows, static_cast<int *>(nullptr),
+                                         static_cast<int *>(nullptr), rows + 1, s);
+    if (e == hipSuccess)
+      e = hipcub::DeviceScan::ExclusiveSum(nullptr, b_scan_atoms, static_cast<int *>(nullptr),
+                                           static_cast<int *>(nullptr), atoms + 2, s);
+    if (e == hipSuccess)
+      e = hipcub::DeviceRadixSort::SortPairs(nullptr, b_sort, static_cast<uint32_t *>(nullptr),
+                                             static_cast<uint32_t *>(nullptr),
+                                             static_cast<uint32_t *>(nullptr),
+                                             static_cast<uint32_t *>(nullptr), cap, 0, key_bits, s);
+    if (e != hipSuccess) return e;
+    const size_t tmp = std::max(b_sort, std::max(b_scan_rows, b_scan_atoms));
+    if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+    for (void *q : {static_cast<void *>(h.d_sort_keys), static_cast<void *>(h.d_sort_vals),
+                    static_cast<void *>(h.d_sort_rows), static_cast<void *>(h.d_sort_pre),
+                    h.d_sort_tmp})
+      if (q) (void)hipFree(q);
+    h.d_sort_keys = nullptr;
+    h.d_sort_vals = nullptr;
+    h.d_sort_rows = nullptr;
+    h.d_sort_pre = nullptr;
+    h.d_sort_tmp = nullptr;
+    h.sort_cap = h.sort_rows_cap = 0;
+    h.sort_tmp_bytes = 0;
+    if ((e = hipMalloc(&h.d_sort_keys, 2 * static_cast<size_t>(cap) * sizeof(uint32_t))) != hipSuccess) return e;
+    if ((e = hipMalloc(&h.d_sort_vals, 2 * static_cast<size_t>(cap) * sizeof(uint32_t))) != hipSuccess) return e;
+    if ((e = hipMalloc(&h.d_sort_rows, 2 * (static_cast<size_t>(rows) + 1) * sizeof(int))) != hipSuccess) return e;
+    if ((e = hipMalloc(&h.d_sort_pre, (static_cast<size_t>(atoms) + 2) * sizeof(int))) != hipSuccess) return e;
+    if ((e = hipMalloc(&h.d_sort_tmp, tmp > 0 ? tmp : 1)) != hipSuccess) return e;
+    h.sort_cap = cap;
+    h.sort_rows_cap = rows + 1L;
+    h.sort_tmp_bytes = tmp;
+  }
+  uint32_t *keys_in = h.d_sort_keys, *keys_out = h.d_sort_keys + h.sort_cap;
+  uint32_t *vals_in = h.d_sort_vals, *vals_out = h.d_sort_vals + h.sort_cap;
+  const int ntiles = (rows + kWave - 1) / kWave;
+  int *tilecnt = h.d_sort_rows, *tileoff = h.d_sort_rows + (ntiles + 1);
+  int kept = 0;
   {
     StageTimer timer(h, s, "inc_count");
-    const long n = static_cast<long>(h.contract.max_atoms) + 1;
+    const long n = static_cast<long>(atoms) + 2;  // deg holds max_atoms + 2 counts
     hipLaunchKernelGGL(k_clear_int, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
                        h.d_deg, n);
-    if (slots > 0)
-      hipLaunchKernelGGL(k_inc_list_count, dim3(row_blocks), dim3(256), 0, s, L);
+    const int chunks = (atoms + 1 + kScanChunk - 1) / kScanChunk;
+    hipLaunchKernelGGL(k_clear_int, dim3((chunks + 255) / 256), dim3(256), 0, s, h.d_inc_part,
+                       static_cast<long>(chunks));
+    hipLaunchKernelGGL(k_inc_tiles_count, dim3((ntiles + 1 + 3) / 4), dim3(256), 0, s, L, ntiles,
+                       tilecnt);
+    size_t bytes = h.sort_tmp_bytes;
+    if ((e = hipcub::DeviceScan::ExclusiveSum(h.d_sort_tmp, bytes, tilecnt, tileoff, ntiles + 1,
+                                              s)) != hipSuccess)
+      return e;
+    if (slots_max > kIncSortExact) {
+      // a large list: the in-entry count sizes the sort (one read back per list)
+      if ((e = hipMemcpyAsync(&kept, tileoff + ntiles, sizeof(int), hipMemcpyDeviceToHost, s)) !=
+          hipSuccess)
+        return e;
+      if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
+    } else {
+      // a small one: the sort takes every slot, its unused tail padded, and nothing waits
+      kept = static_cast<int>(slots_max);
+    }
+  }
+  if (ntiles > 0) {
+    StageTimer timer(h, s, "inc_fill");
+    hipLaunchKernelGGL(k_inc_tiles_emit, dim3((ntiles + 3) / 4), dim3(256), 0, s, L, ntiles,
+                       tileoff, keys_in, vals_in);
+  }
+  if (kept > 0 && slots_max <= kIncSortExact)
+    hipLaunchKernelGGL(k_inc_pad_keys, dim3((kept + 255) / 256), dim3(256), 0, s, keys_in,
+                       tileoff + ntiles, kept, pad);
+  if (kept > 0) {
+    StageTimer timer(h, s, "inc_sort");
+    size_t bytes = h.sort_tmp_bytes;
+    if ((e = hipcub::DeviceRadixSort::SortPairs(h.d_sort_tmp, bytes, keys_in, keys_out, vals_in,
+                                                vals_out, kept, 0, key_bits, s)) != hipSuccess)
+      return e;
   }
   {
     StageTimer timer(h, s, "inc_scan");
-    const int n = h.contract.max_atoms + 1;
-    const int chunks = (n + kScanChunk - 1) / kScanChunk;
-    hipLaunchKernelGGL(k_scan_chunks, dim3(chunks), dim3(kScanThreads), 0, s, h.d_deg, n,
-                       h.d_inc_loc, h.d_inc_part);
-    hipLaunchKernelGGL(k_scan_parts, dim3(1), dim3(kScanThreads), 0, s, h.d_inc_part, chunks);
+    // pre[a] = out-entries of the atoms below a (deg holds each atom's out-entries; deg[atoms]
+    // and deg[atoms + 1] are zero)
+    size_t bytes = h.sort_tmp_bytes;
+    if ((e = hipcub::DeviceScan::ExclusiveSum(h.d_sort_tmp, bytes, h.d_deg, h.d_sort_pre,
+                                              atoms + 2, s)) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(k_inc_atoms_loc, dim3((atoms + 1 + 255) / 256), dim3(256), 0, s, keys_out,
+                       kept, h.d_sort_pre, atoms, h.d_inc_loc);
   }
-  if (slots > 0) {
-    StageTimer timer(h, s, "inc_fill");
-    hipLaunchKernelGGL(k_inc_list_fill, dim3(row_blocks), dim3(256), 0, s, L);
+  {
+    StageTimer timer(h, s, "inc_place");
+    // out-entries staged in LDS per tile when the slot numbers fit a byte, else row by row
+    const int pitch = L.maxneighs | 1;
+    const size_t lds = static_cast<size_t>(kWave) * pitch * (sizeof(int) + 1);
+    if (L.maxneighs <= 255 && lds <= 65536) {
+      if (ntiles > 0)
+        hipLaunchKernelGGL(k_inc_tiles_place, dim3(ntiles), dim3(kWave), lds, s, L, ntiles, pitch);
+    } else {
+      hipLaunchKernelGGL(k_inc_rows_place, dim3((rows + 255) / 256), dim3(256), 0, s, L);
+    }
+    if (kept > 0)
+      hipLaunchKernelGGL(k_inc_sorted_place, dim3((kept + 255) / 256), dim3(256), 0, s, L,
+                         keys_out, vals_out, kept, h.d_sort_pre);
   }
-  if (nall > 0) {
-    StageTimer timer(h, s, "inc_sort");
-    if (L.fold)
-      hipLaunchKernelGGL(k_inc_list_fold, dim3((nall + 3) / 4), dim3(256), 0, s, L, nall);
-    hipLaunchKernelGGL(k_inc_list_sort, dim3((nall + 3) / 4), dim3(256), 0, s, L, nall);
+  if (L.fold && nall > 0) {
+    StageTimer timer(h, s, "inc_fold");
+    hipLaunchKernelGGL(k_inc_list_fold_sorted, dim3((nall + 3) / 4), dim3(256), 0, s, L, nall);
   }
   return hipGetLastError();
 }
