@@ -219,6 +219,7 @@ __global__ __launch_bounds__(256) void k_tile_rows(const int *__restrict__ order
 }
 
 struct TileBuild {
+  int tiles;
   const int *atom;
   const int *nn;
   const int *neighbors;
@@ -240,7 +241,10 @@ __global__ __launch_bounds__(1024) void k_tile_union(TileBuild b)
   __shared__ unsigned short rank[kTileHash];
   __shared__ int sorted[kTileSortN];
   __shared__ int count, fill;
-  const int tile = blockIdx.x;
+  // XCD-grouped: consecutive tiles (neighbours along the curve, sharing list lines) run on one
+  // XCD and meet in its L2
+  const int tile = tile_of_block();
+  if (tile >= b.tiles) return;  // whole block
   const int tid = threadIdx.x;
   constexpr uint32_t kMask = kTileHash - 1;
   for (int k = tid; k < kTileHash; k += 1024) keys[k] = -1;
@@ -695,7 +699,8 @@ hipError_t build_tile_list(Handle &h, hipStream_t s, const double *x, const int 
   b.uni = T.uni;
   b.ucount = T.ucount;
   b.lid = T.lid;
-  hipLaunchKernelGGL(k_tile_union, dim3(tiles), dim3(1024), 0, s, b);
+  b.tiles = tiles;
+  hipLaunchKernelGGL(k_tile_union, dim3(tile_grid(tiles)), dim3(1024), 0, s, b);
   return hipGetLastError();
 }
 
