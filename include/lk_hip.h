@@ -6,7 +6,10 @@
  * sized once from the contract capacities (never resized), and the per-step results.
  *
  * Every entry point is stream-ordered on the caller's HIP stream (the Kokkos execution space
- * stream in a LAMMPS build); only lk_step_result synchronises. Pointers named x, f, ilist,
+ * stream in a LAMMPS build); per step only lk_step_result synchronises. Work done once per
+ * neighbour list may wait once: the two-sided schemes read one count back when they build the
+ * incidence lists of a list over 4 M slots, and a working buffer that grows for a larger list
+ * waits for the device before it is replaced. Pointers named x, f, ilist,
  * numneigh and neighbors are device pointers owned by the caller (the engine) and are never
  * freed here. Errors return a status code; lk_last_error gives the message. Nothing throws
  * across this boundary.
