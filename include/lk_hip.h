@@ -274,7 +274,13 @@ int lk_comm_pack_reverse(lk_handle *h, void *stream, const void *rows, int width
 int lk_comm_unpack_reverse(lk_handle *h, void *stream, void *rows, int width, const int *sendlist,
                            int n, const double *buf);
 
-/* Synchronises the stream and returns energy, virial and the pack counts of the last step. */
+/*
+ * Waits for the last step and returns its energy, virial and pack counts. After a model pass it
+ * polls the result copy the pass's last block writes into pinned host memory (its sequence
+ * number last), which returns as soon as the pass has produced it; the stream stays ordered.
+ * Past a bounded number of polls, after a pack alone, or with stage timing on, it synchronises
+ * the stream instead, which also reports any error of the pass.
+ */
 int lk_step_result(lk_handle *h, void *stream, lk_step_info *out);
 
 /*

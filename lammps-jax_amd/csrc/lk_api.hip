@@ -71,6 +71,17 @@ void free_all(Handle &h)
 
 hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
 
+// Polls of the pinned result copy before lk_step_result falls back to a stream wait (tens of
+// milliseconds: far longer than a step).
+constexpr long kResultSpins = 1L << 22;
+
+// A model pass was enqueued whose last block writes the pinned result copy.
+void mark_mirrored(Handle &h)
+{
+  h.result_mirrored = true;
+  ++h.mirror_expected;
+}
+
 // Two-sided incidence lists come from the list slots unless the pack's filter depends on the
 // positions (unique boundary) or duplicates edges, or a validity-bit address would not fit in
 // 27 bits.
@@ -326,7 +337,8 @@ int lk_create(const lk_contract *c, lk_handle **out)
     if ((e = hipMalloc(&h.d_edge_f, E * 3 * S)) != hipSuccess) return hip_fail(h, e, "hipMalloc(edge forces)");
     (void)hipMemset(h.d_edge_f, 0, E * 3 * S);
   }
-  if ((e = hipHostMalloc(reinterpret_cast<void **>(&h.h_result), sizeof(lk::StepResult))) != hipSuccess)
+  if ((e = hipHostMalloc(reinterpret_cast<void **>(&h.h_result), sizeof(lk::StepResult),
+                        hipHostMallocCoherent)) != hipSuccess)
     return hip_fail(h, e, "hipHostMalloc(result)");
   std::memset(h.h_result, 0, sizeof(lk::StepResult));
   if ((e = hipHostGetDevicePointer(reinterpret_cast<void **>(&h.d_host_result), h.h_result, 0)) != hipSuccess)
@@ -663,7 +675,7 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
       e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, h.x_last, true);
     }
     if (e != hipSuccess) return hip_fail(h, e, "compute");
-    h.result_mirrored = true;
+    mark_mirrored(h);
     return LK_OK;
   }
   if (h.accum == LK_ACCUM_ONESIDED) {
@@ -697,7 +709,7 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
     }
   }
   if (e != hipSuccess) return hip_fail(h, e, "compute");
-  h.result_mirrored = true;
+  mark_mirrored(h);
   return LK_OK;
 }
 
@@ -772,7 +784,7 @@ int lk_pack_compute(lk_handle *w, void *stream, const double *x, const int *type
       if (e == hipSuccess)
         e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, x, true, fp);
       if (e != hipSuccess) return hip_fail(h, e, "fused two-sided step");
-      h.result_mirrored = true;
+      mark_mirrored(h);
       return LK_OK;
     }
   }
@@ -807,7 +819,7 @@ int lk_pack_compute(lk_handle *w, void *stream, const double *x, const int *type
                                           neighbors, nb_stride, static_cast<int>(rows),
                                           max_neighbors_per_atom, nlocal, nghost, flags, scale, f);
   if (e != hipSuccess) return hip_fail(h, e, "fused step");
-  h.result_mirrored = true;
+  mark_mirrored(h);
   return LK_OK;
 }
 
@@ -819,10 +831,26 @@ int lk_step_result(lk_handle *w, void *stream, lk_step_info *out)
   // After a model pass its last block has already written the pinned copy; a pack alone
   // leaves the counts on the device.
   hipError_t e = hipSuccess;
-  if (!h.result_mirrored)
-    e = hipMemcpyAsync(h.h_result, h.d_result, sizeof(lk::StepResult), hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (e != hipSuccess) return hip_fail(h, e, "step result");
+  bool seen = false;
+  if (h.result_mirrored && h.pending.empty()) {
+    // The last block writes the pinned copy with its sequence number last: poll it rather than
+    // wait for the stream's completion signal. The stream stays ordered (the next launches queue
+    // behind the pass). Bounded: past the spin budget the stream wait below decides, and it also
+    // reports any error of the pass.
+    for (long spin = 0; spin < kResultSpins; ++spin) {
+      if (__atomic_load_n(&h.h_result->seq, __ATOMIC_ACQUIRE) == h.mirror_expected) {
+        seen = true;
+        break;
+      }
+      __builtin_ia32_pause();
+    }
+  }
+  if (!seen) {
+    if (!h.result_mirrored)
+      e = hipMemcpyAsync(h.h_result, h.d_result, sizeof(lk::StepResult), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(h, e, "step result");
+  }
   for (const auto &p : h.pending) {
     float ms = 0.0f;
     if (hipEventElapsedTime(&ms, h.event_pool[p.a], h.event_pool[p.b]) == hipSuccess) {
@@ -983,7 +1011,7 @@ int lk_model_force(lk_handle *w, void *stream, int nlocal, int nghost, int flags
                              incidence_from_list(h), lk::FusedPack{}, lk::kPhaseForce);
   if (e != hipSuccess) return hip_fail(h, e, "model force");
   h.split_serial = -1;
-  h.result_mirrored = true;
+  mark_mirrored(h);
   return LK_OK;
 }
 

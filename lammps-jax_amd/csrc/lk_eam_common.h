@@ -286,7 +286,17 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
       // every block has passed its tail reset (it precedes the done count): the live count moves
       pack.state[kLive] = demand < pack.max_edges ? demand : pack.max_edges;
     }
-    if (mirror) *mirror = *result;  // the host's pinned copy: no separate readback copy
+    result->seq += 1;
+    if (mirror) {
+      // the host's pinned copy, no separate readback: every field, a system-scope fence, then
+      // the sequence number the host waits for
+      StepResult copy = *result;
+      const int seq = copy.seq;
+      copy.seq = mirror->seq;
+      *mirror = copy;
+      __threadfence_system();
+      __hip_atomic_store(&mirror->seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
     *done = 0;  // ready for the next launch
   }
 }

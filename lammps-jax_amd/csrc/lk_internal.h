@@ -20,7 +20,7 @@ struct StepResult {
   int edge_count;      // demand count of the last pack (may exceed max_edges)
   int edge_overflow;   // 1 when the last pack exceeded max_edges
   int ghost_sender;    // 1 when a packed edge starts on a ghost row
-  int pad;
+  int seq;             // model passes completed (the host's pinned copy is written last)
 };
 
 // Words of the pack state (int [kPackStateWords] on the device, zero at creation). The slot
@@ -92,7 +92,8 @@ struct Handle {
   StepResult *d_result = nullptr;
   StepResult *h_result = nullptr;  // pinned
   StepResult *d_host_result = nullptr;  // device view of h_result (written by the last block)
-  bool result_mirrored = false;         // the last enqueued work ends with that write
+  bool result_mirrored = false;
+  int mirror_expected = 0;  // seq the pinned copy holds once the enqueued model passes finish         // the last enqueued work ends with that write
 
   // single-rank comm description (ghost -> owner), uploaded by lk_set_ghost_map
   int *d_ghost_owner = nullptr;
