@@ -128,3 +128,63 @@ def test_workload_at_full_size(gpu, name):
     assert again.energy == info.energy
     np.testing.assert_array_equal(again.virial, info.virial)
     np.testing.assert_array_equal(pj.forces(), f)
+
+
+def _model_checks(wl, sysm, info, f, ref, rows):
+    nl = sysm.nlocal
+    f_ref = ref["forces"][:rows]
+    if wl.precision == 8:
+        assert abs(info.energy - ref["energy"]) / nl <= F64_ENERGY_PER_ATOM
+        assert float(np.max(np.abs(f[:rows] - f_ref))) <= F64_FORCE_ABS
+    else:
+        assert abs(info.energy - ref["energy"]) / nl <= F32_ENERGY_PER_ATOM
+        assert rel_err(f[:rows], f_ref) < F32_REL
+
+
+def test_neighbor_matrix_layout_at_full_size(gpu):
+    """The 131k-atom workload through a neighbour-matrix contract (the list copied into the
+    [max_neighbors][rows] matrix once, then the row models with the model's r^2 < rc^2 mask):
+    the same kept pairs as the packed edges, so the oracle's one-sided results at the reference's
+    float64 bars."""
+    wl = systems.make_workload("eam_alloy_131k")
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=wl.list_kind)
+    pj = PairJax.for_workload(wl, sysm, layout="neighbor-matrix")
+    print(f"full-size matrix case: nlocal={sysm.nlocal} maxneighs={lst['maxneighs']}", flush=True)
+    info = pj.compute()
+    f = pj.forces().copy()
+    ref, _ = _oracle(wl, sysm, lst, pj)
+    assert info.edge_overflow == 0
+    _model_checks(wl, sysm, info, f, ref, sysm.nlocal)
+    assert rel_err(info.virial, ref["virial"]) < 1e-12
+    assert np.all(f[sysm.nlocal:sysm.nall] == 0.0)
+
+
+@pytest.mark.parametrize("name", ["eam_alloy_8k", "eam_alloy_131k"])
+def test_split_pass_at_full_size(gpu, name):
+    """The model pass split at its exchanges (lk_model_density, the engine's exchanges through
+    the lk_comm_* buffer calls over the harness's ghost swaps, lk_model_force) at full size, with
+    no ghost map on the handle: the half scheme of the 8k workload and the one-sided scheme of the
+    131k workload against the oracle."""
+    from lammps_jax_amd.pair import DeviceComm
+
+    wl = systems.make_workload(name)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=wl.list_kind)
+    pj = PairJax.for_workload(wl, sysm, fused=False)
+    pj.h.set_ghost_map(sysm.nlocal, np.zeros(0, np.int32))
+    print(f"full-size split case {name}: nlocal={sysm.nlocal} nghost={sysm.nghost}", flush=True)
+    info = pj.compute_split(DeviceComm(pj, sysm))
+    f = pj.forces().copy()
+    ref, _ = _oracle(wl, sysm, lst, pj)
+    assert info.edge_overflow == 0
+    rows = sysm.nlocal if wl.accumulation == "onesided" else sysm.nall
+    _model_checks(wl, sysm, info, f, ref, rows)
+    if wl.accumulation == "onesided":
+        assert rel_err(info.virial, ref["virial"]) < 1e-12
+    else:
+        assert rel_err(info.virial, O.virial_fdotr(ref["forces"][:sysm.nall], sysm.x,
+                                                   sysm.nall)) < 1e-12
+    rho, fp = pj.model_rows()
+    assert rel_err(rho[:sysm.nlocal], ref["rho"][:sysm.nlocal]) < 1e-13
+    assert rel_err(fp[:sysm.nall], ref["fp"][:sysm.nall]) < 1e-13
