@@ -24,6 +24,7 @@
 //   sweeps   16 lanes per atom walk the sorted segment; a fixed butterfly sums the lanes.
 
 #include <algorithm>
+#include <climits>
 
 #include <hipcub/hipcub.hpp>
 
@@ -474,34 +475,95 @@ __global__ __launch_bounds__(256) void k_inc_sorted_place(ListArgs L,
   L.inc_bit[q] = slot_bit(L, ii, jj);
 }
 
-// Plain scheme only, one wave per atom, after the lists are placed: the fold above (an in-entry
-// whose row atom is also one of the atom's out-entries is dropped and that out-entry marked),
-// then the kept in-entries close up in order; len[a] = the list's length.
+constexpr int kFoldLanes = 16;    // lanes per atom in the fold
+constexpr int kFoldSlots = 256;   // LDS hash slots per atom: up to kFoldSlots / 2 out-entries
+
+__device__ __forceinline__ int fold_slot(int atom)
+{
+  return static_cast<int>((static_cast<uint32_t>(atom) * 0x9E3779B1u) >> 24);
+}
+
+// Plain scheme only, after the lists are placed: the fold above (an in-entry whose row atom is
+// also one of the atom's out-entries is dropped and the first such out-entry marked), then the
+// kept in-entries close up in order; len[a] = the list's length. Sixteen lanes per atom, sixteen
+// atoms per block. When every atom of the block has at most kFoldSlots / 2 out-entries, each atom's
+// out-entries go into an open-addressing table in LDS (partner atom -> lowest out index) and each
+// in-entry probes it; otherwise the in-entries are compared against every out-entry by shuffles,
+// with the loops run to the wave's longest list so every shuffle reads an active lane.
 __global__ __launch_bounds__(256) void k_inc_list_fold_sorted(ListArgs L, int natoms)
 {
-  const int atom = blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  constexpr int G = kFoldLanes;
+  __shared__ int keys[256 / G][kFoldSlots];
+  __shared__ int first[256 / G][kFoldSlots];
   const int lane = threadIdx.x & (kWave - 1);
-  if (atom >= natoms) return;  // whole wave
-  const int b0 = inc_off(L.loc, L.part, atom);
-  const int out = L.deg[atom];
+  const int g = lane / G, gl = lane % G, grp = threadIdx.x / G;
+  const int atom = blockIdx.x * (256 / G) + grp;
+  const bool have = atom < natoms;
+  int b0 = 0, out = 0, len = 0;
+  if (have) {
+    b0 = inc_off(L.loc, L.part, atom);
+    out = L.deg[atom];
+    len = inc_off(L.loc, L.part, atom + 1) - b0 - out;
+  }
   const int b = b0 + out;
-  const int len = inc_off(L.loc, L.part, atom + 1) - b;
+  const bool hashed = !__syncthreads_or(out > kFoldSlots / 2);  // block-uniform
+  if (hashed) {
+    for (int i = gl; i < kFoldSlots; i += G) {
+      keys[grp][i] = -1;
+      first[grp][i] = INT_MAX;
+    }
+    __syncthreads();
+    for (int c = gl; c < out; c += G) {
+      const int w = static_cast<int>(static_cast<uint32_t>(L.inc[b0 + c]) & kIncAtom);
+      int h = fold_slot(w);
+      // at most half the slots are taken, so an empty or matching slot is always reached
+      for (int t = 0; t < kFoldSlots; ++t) {
+        const int old = atomicCAS(&keys[grp][h], -1, w);
+        if (old == -1 || old == w) {
+          atomicMin(&first[grp][h], c);
+          break;
+        }
+        h = (h + 1) & (kFoldSlots - 1);
+      }
+    }
+    __syncthreads();
+  }
+  const int len_max = wave_max_int(len), out_max = wave_max_int(out);
+  if (len_max == 0) {  // whole wave
+    if (have && gl == 0) L.len[atom] = out;
+    return;
+  }
   int kept = 0;
-  for (int c0 = 0; c0 < len; c0 += kWave) {
-    const bool mine = c0 + lane < len;
+  for (int c0 = 0; c0 < len_max; c0 += G) {
+    const bool mine = c0 + gl < len;
     int row_atom = -1;
     uint32_t bit = 0;
     if (mine) {
-      row_atom = static_cast<int>(static_cast<uint32_t>(L.inc[b + c0 + lane]) & kIncAtom);
-      bit = L.inc_bit[b + c0 + lane];
+      row_atom = static_cast<int>(static_cast<uint32_t>(L.inc[b + c0 + gl]) & kIncAtom);
+      bit = L.inc_bit[b + c0 + gl];
     }
     int hit = -1;
-    for (int c1 = 0; c1 < out; c1 += kWave) {
-      const int w = c1 + lane < out ? static_cast<int>(L.inc[b0 + c1 + lane] & kIncAtom) : -1;
-      const int n = min(kWave, out - c1);
-      for (int m = 0; m < n; ++m) {
-        const int wm = __builtin_amdgcn_readlane(w, m);
-        if (hit < 0 && wm == row_atom) hit = c1 + m;
+    if (hashed) {
+      if (mine) {
+        int h = fold_slot(row_atom);
+        for (int t = 0; t < kFoldSlots; ++t) {
+          const int k = keys[grp][h];
+          if (k == row_atom) {
+            hit = first[grp][h];
+            break;
+          }
+          if (k < 0) break;
+          h = (h + 1) & (kFoldSlots - 1);
+        }
+      }
+    } else {
+      for (int c1 = 0; c1 < out_max; c1 += G) {
+        const int w = c1 + gl < out ? static_cast<int>(L.inc[b0 + c1 + gl] & kIncAtom) : -2;
+#pragma unroll
+        for (int m = 0; m < G; ++m) {
+          const int wm = __shfl(w, g * G + m, kWave);
+          if (hit < 0 && wm == row_atom) hit = c1 + m;
+        }
       }
     }
     // every lane has read the chunk (row_atom, bit) before any write below, and a kept entry
@@ -509,15 +571,15 @@ __global__ __launch_bounds__(256) void k_inc_list_fold_sorted(ListArgs L, int na
     if (mine && hit >= 0)
       L.inc[b0 + hit] = static_cast<int>(static_cast<uint32_t>(row_atom) | kIncPaired);
     const bool keep = mine && hit < 0;
-    const uint64_t M = wave_ballot(keep);
+    const uint64_t M = (wave_ballot(keep) >> (g * G)) & 0xFFFFull;
     if (keep) {
-      const int q = b + kept + lanes_below(M);
+      const int q = b + kept + __popcll(M & ((1ull << gl) - 1ull));
       L.inc[q] = static_cast<int>(static_cast<uint32_t>(row_atom) | (1u << 31));
       L.inc_bit[q] = bit;
     }
     kept += __popcll(M);
   }
-  if (lane == 0) L.len[atom] = out + kept;
+  if (have && gl == 0) L.len[atom] = out + kept;
 }
 
 template <typename T>
@@ -1239,7 +1301,8 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall, 
   }
   if (L.fold && nall > 0) {
     StageTimer timer(h, s, "inc_fold");
-    hipLaunchKernelGGL(k_inc_list_fold_sorted, dim3((nall + 3) / 4), dim3(256), 0, s, L, nall);
+    hipLaunchKernelGGL(k_inc_list_fold_sorted, dim3((nall + 256 / kFoldLanes - 1) / (256 / kFoldLanes)),
+                       dim3(256), 0, s, L, nall);
   }
   return hipGetLastError();
 }

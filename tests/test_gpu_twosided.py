@@ -13,6 +13,8 @@ virial)."""
 
 from __future__ import annotations
 
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -120,6 +122,23 @@ def test_plain_lj_ghost_rows_float32(gpu):
                               n_hops=2)
     ref = _oracle(wl, sysm, lst, pj, 4, O.PLAIN, n_hops=2)
     _check(pj, sysm, ref, 4)
+
+
+def test_plain_lj_long_cutoff(gpu):
+    """LJ float64 on a full list with a 3.6 sigma cutoff: about 165 pair ends per owned atom, more
+    than the incidence fold's LDS table takes (128 out-entries per atom), so the fold compares the
+    entries by shuffles instead."""
+    base = systems.make_workload("lj_fcc_1k", cells=(6, 6, 6))
+    wl = dataclasses.replace(base, cutoff=3.6, lj=dict(base.lj, cutoff=3.6))
+    sysm = systems.System(wl.x, wl.types, wl.box, wl.cutoff + wl.skin)
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    pj = PairJax(sysm, ("lj", wl.lj), precision=8, accumulation="plain", edges_per_atom=256)
+    print(f"two-sided case lj long cutoff nall={sysm.nall}", flush=True)
+    ref = _oracle(wl, sysm, lst, pj, 8, O.PLAIN)
+    s, _, m, _, _ = O.pack_neighbors(sysm.x, lst, max_atoms=pj.max_atoms, max_edges=pj.max_edges,
+                                     nlocal=sysm.nlocal, cutoff=wl.cutoff)
+    assert np.bincount(s[m.astype(bool)]).max() > 128
+    _check(pj, sysm, ref, 8)
 
 
 @pytest.mark.parametrize("name,kind,accum", [
