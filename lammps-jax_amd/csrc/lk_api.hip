@@ -61,7 +61,7 @@ void free_all(Handle &h)
                   h.tl.keys,     h.tl.keys_sorted, h.tl.rows_in, h.tl.order,  h.tl.sort_tmp,
                   h.tl.atom,     h.tl.nn,       h.tl.uni,        h.tl.ucount,   h.tl.lid,
                   h.tl.box,      h.d_sort_keys, h.d_sort_vals,   h.d_sort_tmp,  h.d_sort_rows,
-                  h.d_sort_pre};
+                  h.d_sort_pre,  h.d_rowmark,   h.d_nonrow};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -548,6 +548,23 @@ int lk_set_ghost_map(lk_handle *w, int nlocal, int nghost, const int *ghost_owne
   return LK_OK;
 }
 
+// One-sided EAM over a list with fewer owned rows than owned atoms (LAMMPS' neigh_modify include):
+// the atoms without a row still take part at zero density (launch_embed_nonrows). The marks and
+// per-block energies are allocated on the first such list, with a device synchronisation.
+static int prepare_nonrows(Handle &h, int inum, int nlocal)
+{
+  h.nonrow_blocks = 0;
+  if (h.model != 1 || h.accum != LK_ACCUM_ONESIDED || h.matrix || inum >= nlocal) return LK_OK;
+  if (!h.d_rowmark) {
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMalloc(&h.d_rowmark, static_cast<size_t>(h.contract.max_atoms));
+    if (e == hipSuccess) e = dalloc(&h.d_nonrow, static_cast<size_t>(lk::kNonrowBlocks));
+    if (e != hipSuccess) return hip_fail(h, e, "hipMalloc(row marks)");
+  }
+  h.nonrow_blocks = lk::kNonrowBlocks;
+  return LK_OK;
+}
+
 int lk_pack_atoms(lk_handle *w, void *stream, const double *x, const int *type, int nall)
 {
   if (!w) return LK_ERR_ARGUMENT;
@@ -604,6 +621,7 @@ int lk_pack_edges(lk_handle *w, void *stream, const double *x, const int *ilist,
     h.list_duplicate = 0;
     h.inc_key = Handle::IncKey{};  // a new matrix: incidence lists are rebuilt
     h.packed_rows = num_rows;
+    h.nonrow_blocks = 0;  // row i is atom i
     h.matrix_copied = true;
     h.matrix_epoch = h.list_epoch;
     h.result_mirrored = false;
@@ -626,9 +644,12 @@ int lk_pack_edges(lk_handle *w, void *stream, const double *x, const int *ilist,
   h.list_half_filter = half_filter;
   h.list_unique = unique;
   h.list_duplicate = duplicate;
+  if (int rc = prepare_nonrows(h, inum, nlocal)) return rc;
   hipError_t e = lk::launch_pack_edges(h, as_stream(stream), x, ilist, numneigh, neighbors,
                                        nb_stride, static_cast<int>(rows), max_neighbors_per_atom,
                                        nlocal, duplicate, half_filter, unique);
+  if (e == hipSuccess && h.nonrow_blocks > 0)
+    e = lk::launch_mark_rows(h, as_stream(stream), ilist, static_cast<int>(rows), nlocal);
   if (e != hipSuccess) return hip_fail(h, e, "pack_edges");
   h.result_mirrored = false;
   return LK_OK;
@@ -815,6 +836,7 @@ int lk_pack_compute(lk_handle *w, void *stream, const double *x, const int *type
                 "one-sided EAM needs the ghost map of this step (lk_set_ghost_map) for the F' "
                 "forward exchange");
   if (int rc = ensure_bits(h, max_neighbors_per_atom)) return rc;
+  if (int rc = prepare_nonrows(h, inum, nlocal)) return rc;
   hipError_t e = lk::launch_step_onesided(h, as_stream(stream), x, type, nall, ilist, numneigh,
                                           neighbors, nb_stride, static_cast<int>(rows),
                                           max_neighbors_per_atom, nlocal, nghost, flags, scale, f);

@@ -109,6 +109,56 @@ __global__ __launch_bounds__(256) void k_embed_rows(EamArgs<S> a, int first, int
   a.fp[i] = Fp;
 }
 
+// Owned atoms without a row. The reference's model evaluates every owned atom: one that no row
+// of the list names as sender has rho = 0 and adds F(0) to the energy; the rows that name it read
+// F'(0) (eam.py:285-301). mark[i] = 1 for each owned atom that is a row of this step's list.
+__global__ __launch_bounds__(256) void k_mark_clear(unsigned char *__restrict__ mark, int n)
+{
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) mark[i] = 0;
+}
+
+__global__ __launch_bounds__(256) void k_mark_rows(const int *__restrict__ ilist, int rows,
+                                                   int nlocal, unsigned char *__restrict__ mark)
+{
+  const int ii = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ii >= rows) return;
+  const int i = ilist[ii];
+  if (i >= 0 && i < nlocal) mark[i] = 1;
+}
+
+// After the density pass: each unmarked owned atom gets rho = 0 and F'(0) (and its ghost images
+// F'(0) through the single-rank map when `ghost_off` is given); the F(0) energies sum in a fixed
+// order into extra[blockIdx.x] (gridDim.x = kNonrowBlocks).
+template <typename S>
+__global__ __launch_bounds__(256) void k_embed_nonrows(EamArgs<S> a,
+                                                       const unsigned char *__restrict__ mark,
+                                                       int nlocal, const int *ghost_off,
+                                                       const int *ghost_list,
+                                                       double *__restrict__ extra)
+{
+  __shared__ double part[256 / kWave];
+  double e = 0.0;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nlocal; i += gridDim.x * blockDim.x) {
+    if (mark[i]) continue;
+    S F, Fp;
+    embed(a, clamp_species(static_cast<int>(a.atoms[i].w), a.n_el), S(0), F, Fp);
+    a.fp[i] = Fp;
+    if (a.rho) a.rho[i] = S(0);
+    e += static_cast<double>(F);
+    if (ghost_off)
+      for (int q = ghost_off[i]; q < ghost_off[i + 1]; ++q) a.fp[ghost_list[q]] = Fp;
+  }
+  e = wave_sum(e);
+  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = e;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double b = 0.0;
+    for (int w = 0; w < 256 / kWave; ++w) b += part[w];
+    extra[blockIdx.x] = b;
+  }
+}
+
 // Forward comm stand-in: ghost rows read their owner's F' (LAMMPS forward_comm on one rank).
 template <typename S>
 __global__ __launch_bounds__(256) void k_forward_rows(S *__restrict__ v,
@@ -297,7 +347,7 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
     }
   }
   finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done,
-                      reinterpret_cast<double *>(lds), a.pack, a.mirror);
+                      reinterpret_cast<double *>(lds), a.pack, a.mirror, a.extra, a.nextra);
 }
 
 template <typename S>
@@ -323,6 +373,8 @@ static hipError_t eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
     hipLaunchKernelGGL((k_eam_density_rows<S, kDensW, kDensTPB>), dim3(grid),
                        dim3(kDensW * kDensTPB * kWave), 0, s, a, ngroups);
   }
+  if (h.nonrow_blocks > 0)
+    if (hipError_t e = launch_embed_nonrows(h, s, nlocal, false); e != hipSuccess) return e;
   if (phase == kPhaseDensity) return hipGetLastError();
   if (nghost > 0) {
     StageTimer timer(h, s, "forward_fp");
@@ -366,6 +418,30 @@ hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
   if (h.contract.precision == LK_FLOAT64)
     return eam_onesided<double>(h, s, nlocal, nghost, scale, f, flags, phase);
   return eam_onesided<float>(h, s, nlocal, nghost, scale, f, flags, phase);
+}
+
+hipError_t launch_mark_rows(Handle &h, hipStream_t s, const int *ilist, int rows, int nlocal)
+{
+  const int n = h.contract.max_atoms;
+  hipLaunchKernelGGL(k_mark_clear, dim3((n + 255) / 256), dim3(256), 0, s, h.d_rowmark, n);
+  if (rows > 0)
+    hipLaunchKernelGGL(k_mark_rows, dim3((rows + 255) / 256), dim3(256), 0, s, ilist, rows,
+                       nlocal, h.d_rowmark);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_nonrows(Handle &h, hipStream_t s, int nlocal, bool forward)
+{
+  const int *off = forward ? h.d_ghost_off : nullptr;
+  if (h.contract.precision == LK_FLOAT64)
+    hipLaunchKernelGGL(k_embed_nonrows<double>, dim3(kNonrowBlocks), dim3(256), 0, s,
+                       eam_args<double>(h, nlocal, 1.0, nullptr), h.d_rowmark, nlocal, off,
+                       h.d_ghost_list, h.d_nonrow);
+  else
+    hipLaunchKernelGGL(k_embed_nonrows<float>, dim3(kNonrowBlocks), dim3(256), 0, s,
+                       eam_args<float>(h, nlocal, 1.0, nullptr), h.d_rowmark, nlocal, off,
+                       h.d_ghost_list, h.d_nonrow);
+  return hipGetLastError();
 }
 
 }  // namespace lk

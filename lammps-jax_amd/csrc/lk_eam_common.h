@@ -79,7 +79,9 @@ struct EamArgs {
   int ntiles;
   int flags;
   FusedPack pack;
-  StepResult *mirror;  // device view of the host's pinned result
+  StepResult *mirror;   // device view of the host's pinned result
+  const double *extra;  // energies of owned atoms without a row, one per k_embed_nonrows block
+  int nextra;           // 0 when every owned atom is a row
 };
 
 // Species index into the tables. XLA clamps out-of-range gathers, so types past the table's
@@ -237,7 +239,8 @@ inline int persistent_grid(int ngroups, int blocks_per_cu, int num_cus)
 }
 
 // The last block of a launch to finish reduces the tile partials (slot 0 + slot 7 energy, slots
-// 1..6 virial) in a fixed order into the step result, so no separate finalize launch is needed.
+// 1..6 virial) and the `nextra` energies of `extra` in a fixed order into the step result, so no
+// separate finalize launch is needed.
 // Every thread of the block calls it after its last write of partials; `scratch` holds
 // 7 * blockDim.x doubles of LDS that is no longer in use. Returns in every block. The energy is
 // scaled by `escale`, the virial by `vscale` (1 when the partials already hold scaled forces).
@@ -251,7 +254,8 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
                                                     StepResult *result, int *done,
                                                     double *scratch,
                                                     const FusedPack &pack = FusedPack{},
-                                                    StepResult *mirror = nullptr)
+                                                    StepResult *mirror = nullptr,
+                                                    const double *extra = nullptr, int nextra = 0)
 {
   __shared__ int last_block;
   if (threadIdx.x < kWave) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
@@ -267,6 +271,8 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
     acc[0] += q[0] + q[7];
     for (int c = 1; c < 7; ++c) acc[c] += q[c];
   }
+  if (t == 0)
+    for (int k = 0; k < nextra; ++k) acc[0] += extra[k];
   for (int c = 0; c < 7; ++c) scratch[c * nt + t] = acc[c];
   __syncthreads();
   for (int off = nt / 2; off >= 1; off >>= 1) {
@@ -338,6 +344,8 @@ inline EamArgs<S> eam_args(Handle &h, int nlocal, double scale, double *f)
   a.flags = 0;
   a.pack = FusedPack{};
   a.mirror = h.d_host_result;
+  a.extra = h.d_nonrow;
+  a.nextra = h.nonrow_blocks;
   return a;
 }
 

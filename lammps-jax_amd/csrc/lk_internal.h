@@ -85,6 +85,11 @@ struct Handle {
   // per-atom model state
   void *d_fp = nullptr;      // F'(rho) [max_atoms]
   void *d_rho = nullptr;     // rho [max_atoms]
+  // owned atoms that are no row of the list (a list over part of the owned atoms), one-sided
+  // EAM: allocated on first use
+  unsigned char *d_rowmark = nullptr;  // [max_atoms] 1: the owned atom is a row of this list
+  double *d_nonrow = nullptr;          // [kNonrowBlocks] their embedding energy, per block
+  int nonrow_blocks = 0;               // kNonrowBlocks when this step's list misses owned atoms
   // block partials: energy and virial, reduced in a fixed order
   void *d_edge_f = nullptr;     // edge-force contracts: per-edge model forces [max_edges][3]
   double *d_partials = nullptr;
@@ -235,6 +240,14 @@ enum ModelPhase { kPhaseAll = 0, kPhaseDensity = 1, kPhaseForce = 2 };
 
 hipError_t launch_eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
                                double *f, int flags, int phase = kPhaseAll);
+
+// One-sided EAM over a list that misses owned atoms (inum < nlocal, as LAMMPS' neigh_modify
+// include gives): the marks of the owned atoms that are rows (before the density pass), then
+// rho = 0, F'(0) (and, with `forward`, F'(0) to their ghost images) and the F(0) energies of the
+// others (after it), which the force sweep adds to the step's energy.
+constexpr int kNonrowBlocks = 64;
+hipError_t launch_mark_rows(Handle &h, hipStream_t s, const int *ilist, int rows, int nlocal);
+hipError_t launch_embed_nonrows(Handle &h, hipStream_t s, int nlocal, bool forward);
 hipError_t launch_lj_onesided(Handle &h, hipStream_t s, int nlocal, int nghost, double scale,
                               double *f, int flags, const FusedPack &pack = FusedPack{});
 hipError_t launch_tile_scan(Handle &h, hipStream_t s, const int *tile_flags, int ntiles);

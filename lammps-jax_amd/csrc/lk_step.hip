@@ -448,6 +448,9 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   } else {
     hipLaunchKernelGGL(k_clear_state, dim3(1), dim3(64), 0, s, h.d_pack_state);
   }
+  const bool nonrows = EAM && h.nonrow_blocks > 0;  // the list misses owned atoms
+  if (nonrows)
+    if (hipError_t e = launch_mark_rows(h, s, ilist, num_rows, nlocal); e != hipSuccess) return e;
   bool tiled = false;
   if constexpr (EAM && !MATRIX && sizeof(S) == 8) {
     // float64 EAM over an engine list: the pack and density over tile lists (lk_tiles.hip)
@@ -475,6 +478,8 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   fp.max_edges = h.contract.max_edges;
   fp.pad = h.contract.max_atoms;
   if constexpr (EAM) {
+    if (nonrows)
+      if (hipError_t e = launch_embed_nonrows(h, s, nlocal, nghost > 0); e != hipSuccess) return e;
     a.pack = fp;
     return launch_eam_force(h, s, a, flags);
   }
