@@ -176,7 +176,9 @@ int lk_pack_atoms(lk_handle *h, void *stream, const double *x, const int *type, 
  * ilist [inum+gnum], numneigh [nall], neighbors: LayoutLeft, entry (i, jj) at
  * neighbors[jj * nb_stride + i]; special-bond bits are masked off. Rows scanned are
  * inum (+ gnum when n_hops > 1), clamped to max_atoms. The edge count and overflow flag stay on
- * the device until lk_step_result.
+ * the device until lk_step_result. A list over part of the owned atoms (inum < nlocal, as
+ * neigh_modify include gives) is valid: the one-sided EAM pass gives each owned atom without a
+ * row zero density, F(0) and F'(0), as the reference's model does for an atom with no edges.
  */
 int lk_pack_edges(lk_handle *h, void *stream, const double *x, const int *ilist,
                   const int *numneigh, const int *neighbors, long nb_stride, int inum, int gnum,
