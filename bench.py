@@ -285,6 +285,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="eam_alloy_131k")
+    ap.add_argument("--atom-order", default="lattice", choices=("lattice", "sorted"),
+                    help="owned-atom order: the lattice generator's, or LAMMPS' default spatial "
+                         "sort (atom_modify sort: bins of half the neighbour cutoff)")
     ap.add_argument("--layout", default="sparse-edge", choices=("sparse-edge", "neighbor-matrix"),
                     help="bundle input layout; neighbor-matrix times the steps between list "
                          "rebuilds (the matrix is copied on rebuilds only)")
@@ -325,7 +328,7 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     t_setup = time.perf_counter()
-    wl = systems.make_workload(args.workload)
+    wl = systems.make_workload(args.workload, order=args.atom_order)
     sysm = wl.system()
     lst = sysm.build_list(wl.cutoff + wl.skin, kind=wl.list_kind)
     nall = sysm.nall
@@ -446,6 +449,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": wl.name,
+            "atom_order": args.atom_order,
             "atoms": N,
             "ghosts": sysm.nghost,
             "list_entries": lst["entries"],
@@ -465,7 +469,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": pmc_traffic(dom, wl.name if not matrix else f"{wl.name}_matrix"),
+            "traffic": pmc_traffic(dom, wl.name + ("_matrix" if matrix else "")
+                                   + ("_sorted" if args.atom_order == "sorted" else "")),
         },
         "cpu_baseline": cpu,
         "nve": nve,

@@ -14,6 +14,9 @@ The five named workloads:
                    list cutoff rc + 0.3, 96 edges/atom
 
 Random numbers come from numpy's PCG64 (default_rng) with fixed seeds.
+
+Atom order: "lattice" keeps the generator's cell-major order; "sorted" applies the spatial sort
+LAMMPS performs at setup and every 1000 steps by default (atom_modify sort; lammps_sort_order).
 """
 
 from __future__ import annotations
@@ -134,6 +137,20 @@ class Workload:
         return System(self.x, self.types, self.box, self.cutghost)
 
 
+def lammps_sort_order(x: np.ndarray, box, binsize: float) -> np.ndarray:
+    """The permutation of LAMMPS' atom sort (Atom::sort, on by default with atom_modify sort
+    1000 and a bin size of half the neighbour cutoff): the box is cut into
+    nbin = max(1, int(L / binsize)) bins per axis of width L / nbin, atoms are ordered by bin
+    index iz * nby * nbx + iy * nbx + ix (x fastest), and keep their order within a bin."""
+    x = np.asarray(x, dtype=np.float64)
+    box = np.asarray(box, dtype=np.float64)
+    nbin = np.maximum((box / binsize).astype(np.int64), 1)
+    inv = nbin / box
+    idx = np.clip((x * inv).astype(np.int64), 0, nbin - 1)  # positions in [0, box)
+    key = (idx[:, 2] * nbin[1] + idx[:, 1]) * nbin[0] + idx[:, 0]
+    return np.argsort(key, kind="stable")
+
+
 def _species_shuffle(n: int, frac_first: float, seed: int) -> np.ndarray:
     """Exact-count species assignment: round(frac*n) atoms of type 1, the rest type 2."""
     rng = np.random.default_rng(seed)
@@ -148,8 +165,22 @@ def lj_lattice_constant(density: float = LJ_DENSITY) -> float:
     return (4.0 / density) ** (1.0 / 3.0)
 
 
-def make_workload(name: str, *, cells=None, seed: int | None = None) -> Workload:
-    """Builds one of the named workloads; `cells` overrides the lattice size for small tests."""
+def make_workload(name: str, *, cells=None, seed: int | None = None,
+                  order: str = "lattice") -> Workload:
+    """Builds one of the named workloads; `cells` overrides the lattice size for small tests.
+    order: "lattice" (generator order) or "sorted" (LAMMPS' default spatial atom sort, bins of
+    half the neighbour cutoff)."""
+    if order not in ("lattice", "sorted"):
+        raise ValueError(f"unknown atom order {order!r}")
+    wl = _make_workload(name, cells=cells, seed=seed)
+    if order == "sorted":
+        perm = lammps_sort_order(wl.x, wl.box, 0.5 * (wl.cutoff + wl.skin))
+        wl.x = np.ascontiguousarray(wl.x[perm])
+        wl.types = np.ascontiguousarray(wl.types[perm])
+    return wl
+
+
+def _make_workload(name: str, *, cells=None, seed: int | None = None) -> Workload:
     if name == "lj_fcc_1k":
         nx, ny, nz = cells or (8, 8, 4)
         a = lj_lattice_constant()

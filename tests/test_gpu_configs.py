@@ -69,14 +69,19 @@ def _pressure_bar(virial, box) -> float:
     return (virial[0] + virial[1] + virial[2]) / (3.0 * float(np.prod(box))) * NKTV2P_METAL
 
 
-@pytest.mark.parametrize("name", ["lj_fcc_1k", "eam_alloy_8k", "eam_alloy_131k", "eam_alloy_1m",
-                                  "lj_ghost_262k"])
-def test_workload_at_full_size(gpu, name):
-    wl = systems.make_workload(name)
+FULL_SIZE = [(name, "lattice") for name in
+             ("lj_fcc_1k", "eam_alloy_8k", "eam_alloy_131k", "eam_alloy_1m", "lj_ghost_262k")]
+# LAMMPS' default spatial atom sort (atom_modify sort) on the three large workloads
+FULL_SIZE += [(name, "sorted") for name in ("eam_alloy_131k", "eam_alloy_1m", "lj_ghost_262k")]
+
+
+@pytest.mark.parametrize("name,order", FULL_SIZE)
+def test_workload_at_full_size(gpu, name, order):
+    wl = systems.make_workload(name, order=order)
     sysm = wl.system()
     lst = sysm.build_list(wl.cutoff + wl.skin, kind=wl.list_kind)
     pj = PairJax.for_workload(wl, sysm)
-    print(f"full-size case {name}: nlocal={sysm.nlocal} nghost={sysm.nghost} "
+    print(f"full-size case {name} ({order}): nlocal={sysm.nlocal} nghost={sysm.nghost} "
           f"entries={lst['entries']} max_atoms={pj.max_atoms} max_edges={pj.max_edges} "
           f"{wl.accumulation} fp{8 * wl.precision}", flush=True)
     info = pj.compute()
