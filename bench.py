@@ -30,13 +30,16 @@ HBM_PEAK_GBS = 8000.0
 
 
 def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: int,
-                words: int, two_sided: bool = False, matrix: bool = False) -> float:
+                words: int, two_sided: bool = False, matrix: bool = False,
+                records: bool = False) -> float:
     """Algorithmic (compulsory, unique) HBM bytes of one launch of a stage.
 
     R list rows, A = owned + ghost atoms, N owned, E packed edges, entries = list entries read,
     S bytes per model scalar, words = validity words per row; two_sided: the plain / half
     schemes (incidence lists, 2E incident entries); matrix: the neighbour-matrix row models
-    (E = slots inside the cutoff; only the internal receivers are written)."""
+    (E = slots inside the cutoff; only the internal receivers are written); records: the
+    one-sided pack reads x and type and writes the atom records itself (the float64 EAM tile
+    step, no separate record launch)."""
     rec = 4 * S  # atom record: x, y, z, species
     if two_sided:
         # the list-built incidence lists (once per list): E in-entries sorted by atom
@@ -80,9 +83,10 @@ def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: 
     if stage == "forward_fp":
         return (A - N) * (4 + 2 * S)
     if stage == "step_pack":
-        # list + row data, gathered atom records, validity bits and row counts, F' (owned +
-        # ghost images) and rho out, the packed arrays out
-        return (8 * R + 4 * entries + (rec + 4) * A + 4 * R * words + 8 * R + S * A + S * N
+        # list + row data, gathered atom records (or x and type in, records and species out),
+        # validity bits and row counts, F' (owned + ghost images) and rho out, the packed arrays
+        atoms = (28 + rec + 4) * A if records else (rec + 4) * A
+        return (8 * R + 4 * entries + atoms + 4 * R * words + 8 * R + S * A + S * N
                 + (4 if matrix else 9) * E)
     if stage == "step_count":
         # list + row data, x and type of every atom once, atom records and species out,
@@ -406,8 +410,10 @@ def main() -> int:
     matrix = args.layout == "neighbor-matrix"
     if matrix:  # the count reports the widest row; the rows keep the slots inside the cutoff
         E = slots_inside_cutoff(sysm, lst, wl.cutoff)
+    # the float64 EAM tile step writes the atom records in its pack (no pack_atoms stage)
+    records = not two and not matrix and "pack_atoms" not in stage_us
     sb_kw = dict(R=R, A=A, N=N, E=E, entries=lst["entries"], S=S, words=words, two_sided=two,
-                 matrix=matrix)
+                 matrix=matrix, records=records)
     kernel_stages = {k: v for k, v in stage_us.items() if stage_bytes(k, **sb_kw) > 0}
     # the kernel that takes most of a step (once-per-list stages by their share per step)
     dom = max(kernel_stages, key=lambda k: stage_us_step[k])

@@ -215,9 +215,11 @@ int lk_compute(lk_handle *h, void *stream, int nlocal, int nghost, int flags, do
 
 /*
  * One MD step's device work: lk_pack_atoms + lk_pack_edges + lk_compute with the same results.
- * The one-sided scheme runs fused in three launches: the atom records; the pack, which filters
- * the list, sums each row's density while the list slots are in registers and writes the packed
- * arrays; the force sweep over the packed receivers. Other schemes run the three in order.
+ * The one-sided scheme runs fused: the atom records; the pack, which filters the list, sums each
+ * row's density while the list slots are in registers and writes the packed arrays; the force
+ * sweep over the packed receivers. For float64 EAM over an engine list the pack also writes the
+ * atom records (two launches per step between list rebuilds). Other schemes run the three in
+ * order.
  * Replaces the pack/execute/add sequence of PairJaxKokkos::compute (cpp/pair_jax_kokkos.cpp:
  * 1023-1100).
  */

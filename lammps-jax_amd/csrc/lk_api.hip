@@ -569,6 +569,7 @@ int lk_pack_atoms(lk_handle *w, void *stream, const double *x, const int *type, 
 {
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
+  h.pack_ready = false;
   if (nall < 0 || (nall > 0 && (!x || !type))) return fail(h, LK_ERR_ARGUMENT, "invalid atom arrays");
   h.x_last = x;
   h.type_last = type;
@@ -584,6 +585,7 @@ int lk_pack_edges(lk_handle *w, void *stream, const double *x, const int *ilist,
 {
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
+  h.pack_ready = false;
   const lk_contract &c = h.contract;
   if (inum < 0 || gnum < 0 || nlocal < 0) return fail(h, LK_ERR_ARGUMENT, "invalid list sizes");
   const bool multi_hop = c.n_hops > 1;
@@ -659,6 +661,7 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
 {
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
+  h.pack_ready = false;
   if (h.model == 0) return fail(h, LK_ERR_STATE, "LAMMPS-JAX runtime is not initialized");
   if (nlocal < 0 || nghost < 0 || !f) return fail(h, LK_ERR_ARGUMENT, "invalid compute arguments");
   if (static_cast<long>(nlocal) + nghost > h.contract.max_atoms)
@@ -799,6 +802,7 @@ int lk_pack_compute(lk_handle *w, void *stream, const double *x, const int *type
       h.list_duplicate = 0;
       if (int rc = ensure_incidence(h, 2L * rows * mnb)) return rc;
       hipStream_t s = as_stream(stream);
+      h.pack_ready = false;
       lk::FusedPack fp;
       hipError_t e = lk::launch_pack_fused(h, s, x, type, nall, ilist, numneigh, neighbors,
                                            nb_stride, static_cast<int>(rows), mnb, nlocal, &fp);
@@ -977,6 +981,7 @@ int lk_model_density(lk_handle *w, void *stream, int nlocal, int nghost)
 {
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
+  h.pack_ready = false;
   if (int rc = split_check(h, nlocal, nghost)) return rc;
   hipStream_t s = as_stream(stream);
   hipError_t e;
@@ -1016,6 +1021,7 @@ int lk_model_force(lk_handle *w, void *stream, int nlocal, int nghost, int flags
 {
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
+  h.pack_ready = false;
   if (int rc = split_check(h, nlocal, nghost)) return rc;
   if (!f) return fail(h, LK_ERR_ARGUMENT, "invalid compute arguments");
   if (h.split_serial != h.pack_serial || h.split_nall != nlocal + nghost)

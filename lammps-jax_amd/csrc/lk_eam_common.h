@@ -291,6 +291,11 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
       result->ghost_sender = pack.state[kGhostFlag];
       // every block has passed its tail reset (it precedes the done count): the live count moves
       pack.state[kLive] = demand < pack.max_edges ? demand : pack.max_edges;
+      // and the next fused pack may start here, as the atom-record launch would start it: its
+      // tail reset ends at this live count, its claims and ghost flag start from zero
+      pack.state[kPrevLive] = pack.state[kLive];
+      pack.state[kDemand] = 0;
+      pack.state[kGhostFlag] = 0;
     }
     result->seq += 1;
     if (mirror) {

@@ -90,6 +90,9 @@ struct Handle {
   unsigned char *d_rowmark = nullptr;  // [max_atoms] 1: the owned atom is a row of this list
   double *d_nonrow = nullptr;          // [kNonrowBlocks] their embedding energy, per block
   int nonrow_blocks = 0;               // kNonrowBlocks when this step's list misses owned atoms
+  // The last enqueued pack-state user was a fused step whose last block left the state as a new
+  // pack starts it (zero claims, tail bound = live count): the next tile step skips the reset.
+  bool pack_ready = false;
   // block partials: energy and virial, reduced in a fixed order
   void *d_edge_f = nullptr;     // edge-force contracts: per-edge model forces [max_edges][3]
   double *d_partials = nullptr;

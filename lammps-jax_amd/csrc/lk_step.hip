@@ -399,6 +399,18 @@ __global__ void k_clear_state(int *state)
   }
 }
 
+// Starts a fused pack whose atom records another launch writes: what the atom-record launch does
+// to the pack state (the live count of the previous pack bounds this one's tail reset; zero
+// claims, no ghost sender).
+__global__ void k_start_pack(int *state)
+{
+  if (threadIdx.x == 0) {
+    state[kPrevLive] = state[kLive];
+    state[kDemand] = 0;
+    state[kGhostFlag] = 0;
+  }
+}
+
 template <typename S, bool EAM, bool MATRIX>
 static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,
                                 int nall, const int *ilist, const int *numneigh,
@@ -440,27 +452,34 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   p.ghost_list = h.d_ghost_list;
   const int ntiles = (num_rows + kWave - 1) / kWave;
   const int ngroups = ntiles > 0 ? (ntiles + kStepTPB - 1) / kStepTPB : 1;
-  // K0: atom records and species; zeroes the demand counter and the ghost-sender flag (the
-  // records of a separate lk_pack_atoms call are reused when `atoms` is false)
-  if (atoms) {
+  // float64 EAM over an engine list: the pack and density over tile lists (lk_tiles.hip)
+  bool tiled = false;
+  if constexpr (EAM && !MATRIX && sizeof(S) == 8) tiled = tile_step_eligible(h, num_rows, maxneighs);
+  const int records = atoms ? (nall < h.contract.max_atoms ? nall : h.contract.max_atoms) : 0;
+  const bool ready = h.pack_ready;
+  h.pack_ready = false;  // until this step's force sweep is enqueued
+  if (tiled && atoms) {
+    // The tile kernel writes the atom records itself, and the last block of the previous fused
+    // step left the pack state as the record launch would (h.pack_ready); a launch less per step.
+    if (!ready) hipLaunchKernelGGL(k_start_pack, dim3(1), dim3(64), 0, s, h.d_pack_state);
+  } else if (atoms) {
+    // K0: atom records and species; zeroes the demand counter and the ghost-sender flag
     if (hipError_t e0 = launch_pack_atoms(h, s, x, type, nall, h.d_pack_state); e0 != hipSuccess)
       return e0;
   } else {
+    // the records of a separate lk_pack_atoms call
     hipLaunchKernelGGL(k_clear_state, dim3(1), dim3(64), 0, s, h.d_pack_state);
   }
   const bool nonrows = EAM && h.nonrow_blocks > 0;  // the list misses owned atoms
   if (nonrows)
     if (hipError_t e = launch_mark_rows(h, s, ilist, num_rows, nlocal); e != hipSuccess) return e;
-  bool tiled = false;
   if constexpr (EAM && !MATRIX && sizeof(S) == 8) {
-    // float64 EAM over an engine list: the pack and density over tile lists (lk_tiles.hip)
-    if (tile_step_eligible(h, num_rows, maxneighs)) {
+    if (tiled)
       if (hipError_t e1 = launch_step_tiles(h, s, x, type, ilist, numneigh, neighbors, stride,
-                                            num_rows, maxneighs, nlocal, nghost, a);
+                                            num_rows, maxneighs, nlocal, nghost, a,
+                                            tiled && atoms ? records : 0);
           e1 != hipSuccess)
         return e1;
-      tiled = true;
-    }
   }
   if (ntiles > 0 && !tiled) {
     StageTimer timer(h, s, "step_pack");
@@ -481,7 +500,10 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
     if (nonrows)
       if (hipError_t e = launch_embed_nonrows(h, s, nlocal, nghost > 0); e != hipSuccess) return e;
     a.pack = fp;
-    return launch_eam_force(h, s, a, flags);
+    hipError_t e = launch_eam_force(h, s, a, flags);
+    // its last block resets the pack state for the next fused pack (finalize_last_block)
+    h.pack_ready = e == hipSuccess && fp.state != nullptr;
+    return e;
   }
   return launch_lj_onesided(h, s, nlocal, nghost, scale, f, flags, fp);
 }

@@ -30,10 +30,12 @@ struct TileView {
 // in Hilbert order, each 128-row tile's neighbour union staged in LDS. Eligible: float64 EAM,
 // one-sided, sparse edges, an engine list epoch, at most 256 list slots per row. Builds the
 // tile lists when the list changed; writes what the pack kernel of lk_step.hip writes.
+// records > 0: the kernel also writes the atom records and species of atoms [0, records) (the
+// atom-record launch's work; the kernel itself reads x and type, not the records).
 bool tile_step_eligible(const Handle &h, int num_rows, int maxneighs);
 hipError_t launch_step_tiles(Handle &h, hipStream_t s, const double *x, const int *type,
                              const int *ilist, const int *numneigh, const int *neighbors,
                              long stride, int num_rows, int maxneighs, int nlocal, int nghost,
-                             EamArgs<double> &a);
+                             EamArgs<double> &a, int records = 0);
 
 }  // namespace lk

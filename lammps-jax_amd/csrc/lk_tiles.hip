@@ -386,6 +386,9 @@ struct TileStep {
   unsigned char *mask;
   const int *ghost_off;
   const int *ghost_list;
+  Atom4<double> *atoms_out;  // the atom records of [0, records) (PackAtomsFunctor), or null
+  int *species_out;
+  int records;
 };
 
 __global__ __launch_bounds__(kTileW * kTileSub * kWave) __attribute__((amdgpu_waves_per_eu(6)))
@@ -409,6 +412,20 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
   const int sub = wave_in_block() / W;
   const int wave = wave_in_block() % W;
   const int lane = threadIdx.x & (kWave - 1);
+  // The atom records for the force sweep (PackAtomsFunctor, cpp:35-52: x as is, species =
+  // type - 1). Nothing in this kernel reads them: the union and the rows take x and type.
+  if (p.atoms_out)
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < p.records;
+         i += gridDim.x * blockDim.x) {
+      const int sp = p.type[i] - 1;
+      Atom4<double> r;
+      r.x = p.x[3L * i + 0];
+      r.y = p.x[3L * i + 1];
+      r.z = p.x[3L * i + 2];
+      r.w = static_cast<double>(sp);
+      p.atoms_out[i] = r;
+      p.species_out[i] = sp;
+    }
   for (GroupWalk gw = group_walk(t.ntiles); gw.g < gw.g_end; gw.g += gw.step) {
     const int tile = gw.g;
     const int U = t.ucount[tile];
@@ -416,11 +433,10 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
     if (staged) {
       for (int u = threadIdx.x; u < U; u += blockDim.x) {
         const int g = t.uni[static_cast<long>(tile) * kTileUnion + u];
-        const Atom4<double> r = a.atoms[g];
-        ux[u] = r.x;
-        uy[u] = r.y;
-        uz[u] = r.z;
-        usp[u] = static_cast<unsigned char>(clamp_species(static_cast<int>(r.w), a.n_el));
+        ux[u] = p.x[3L * g + 0];
+        uy[u] = p.x[3L * g + 1];
+        uz[u] = p.x[3L * g + 2];
+        usp[u] = static_cast<unsigned char>(clamp_species(p.type[g] - 1, a.n_el));
         ugid[u] = g;
       }
     }
@@ -489,15 +505,14 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
         for (int jj = wd * 32; jj < min(wd * 32 + 32, nn); ++jj) {
           const int j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
           if (j >= p.max_atoms) continue;
-          const Atom4<double> r = a.atoms[j];
-          const double rsq = dist2(r.x, r.y, r.z);
+          const double rsq = dist2(p.x[3L * j + 0], p.x[3L * j + 1], p.x[3L * j + 2]);
           if (rsq > p.cutsq) continue;
           word |= 1u << (jj & 31);
           ++cnt;
           if (rsq < a.cutsq) {
             const double rr = rsq * rsqrt_nr(rsq);
             const Locator<double> L = locate_mul(rr, a.inv_dr, a.nr);
-            rho += cvalue(rcoef(win, a, L.node, clamp_species(static_cast<int>(r.w), a.n_el)),
+            rho += cvalue(rcoef(win, a, L.node, clamp_species(p.type[j] - 1, a.n_el)),
                           L.t);
           }
         }
@@ -716,7 +731,7 @@ bool tile_step_eligible(const Handle &h, int num_rows, int maxneighs)
 hipError_t launch_step_tiles(Handle &h, hipStream_t s, const double *x, const int *type,
                              const int *ilist, const int *numneigh, const int *neighbors,
                              long stride, int num_rows, int maxneighs, int nlocal, int nghost,
-                             EamArgs<double> &a)
+                             EamArgs<double> &a, int records)
 {
   Handle::IncKey key;
   key.epoch = h.list_epoch;
@@ -751,6 +766,9 @@ hipError_t launch_step_tiles(Handle &h, hipStream_t s, const double *x, const in
   p.mask = h.d_mask;
   p.ghost_off = nghost > 0 ? h.d_ghost_off : nullptr;
   p.ghost_list = h.d_ghost_list;
+  p.atoms_out = records > 0 ? static_cast<Atom4<double> *>(h.d_atoms) : nullptr;
+  p.species_out = h.d_species;
+  p.records = records;
   TileView t;
   t.atom = h.tl.atom;
   t.nn = h.tl.nn;

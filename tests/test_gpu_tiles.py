@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lk_testutil import assert_energy, assert_forces, assert_virial
+from lk_testutil import assert_energy, assert_forces, assert_virial, canonical
 from lammps_jax_amd import harness, systems
 from lammps_jax_amd.pair import PairJax
 
@@ -153,3 +153,54 @@ def test_tile_lists_reused_until_the_list_changes(gpu):
     pj.rebind(sysm2)
     print("tile rebuild step", flush=True)
     _check(wl, sysm2, pj, pj.compute(), "after the rebuild")
+
+
+def test_tile_steps_between_split_steps(gpu):
+    """The fused tile step writes the atom records itself and starts from the pack state the
+    previous fused step's last block left. Fused and split steps alternate here, with edge
+    counts rising and falling (positions scaled, the list kept) and two fused steps enqueued
+    without a readback between them: every step's packed set, padding past its count, atom
+    records, energy and forces match the oracle."""
+    import torch
+
+    wl = systems.make_workload("eam_alloy_131k", cells=(5, 5, 5), seed=12)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    pj = PairJax(sysm, ("eam", wl.tables), precision=8, accumulation="onesided")
+    base = pj.x
+    x0 = sysm.x.copy()
+    nl = sysm.nlocal
+
+    def check(scale, info, label):
+        x = x0 * scale
+        pos, sp = O.pack_atoms(x, sysm.type, sysm.nall, pj.max_atoms, 8)
+        s, r, m, count, _ = O.pack_neighbors(x, lst, max_atoms=pj.max_atoms,
+                                             max_edges=pj.max_edges, nlocal=nl, cutoff=wl.cutoff)
+        assert info.edge_count == count and info.edge_overflow == 0, label
+        ds, dr_, dm = pj.edges()
+        np.testing.assert_array_equal(canonical(ds, dr_, dm), canonical(s, r, m))
+        assert not dm[count:].any(), label
+        assert np.all(ds[count:] == pj.max_atoms) and np.all(dr_[count:] == pj.max_atoms), label
+        atoms, species = pj.staging()
+        n = sysm.nall
+        np.testing.assert_array_equal(atoms[:n, :3], pos[:n])
+        np.testing.assert_array_equal(atoms[:n, 3].astype(np.int64), sp[:n])
+        np.testing.assert_array_equal(species[:n], sp[:n])
+        ref = O.eam_compute(wl.tables, pos, sp, ghost_owner=sysm.ghost_owner, nlocal=nl,
+                            nghost=sysm.nghost, senders=s, receivers=r, mask=m, mode=O.ONESIDED,
+                            precision=8)
+        assert_energy(8, info.energy, ref["energy"], nl)
+        assert_forces(8, pj.forces()[:nl], ref["forces"][:nl])
+
+    for k, (scale, fused) in enumerate([(1.0, True), (0.985, False), (1.03, True), (0.985, True),
+                                        (1.03, False), (0.99, True)]):
+        pj.x = (base * scale).contiguous()
+        print(f"interleaved step {k} scale={scale} fused={fused}", flush=True)
+        check(scale, pj.compute(fused=fused), f"step {k}")
+    # two fused steps back to back without a readback: counts rise, then fall below both
+    pj.x = (base * 0.98).contiguous()
+    pj.enqueue(fused=True)
+    pj.x = (base * 1.04).contiguous()
+    pj.enqueue(fused=True)
+    check(1.04, pj.h.step_result(pj.stream()), "back to back")
+    torch.cuda.synchronize()
