@@ -237,50 +237,51 @@ def slots_inside_cutoff(sysm, lst, cutoff: float) -> int:
 
 
 def lean_step(pj, eflag: bool = True, vflag: bool = True, rebuild_every: int = 0):
-    """One engine step as a C++ caller makes it: lk_pack_compute then lk_step_result, with the
-    argument list bound once (ctypes calls, no torch dispatch). The forces add into f without a
-    clear in between: LAMMPS zeroes f in its own force_clear, outside the pair style.
+    """Engine steps as LAMMPS' C++ Verlet loop makes them: lk_pack_compute then lk_step_result
+    per step, called from the harness's C++ loop (lkh_run_steps) with the argument list bound
+    once. The forces add into f without a clear in between: LAMMPS zeroes f in its own
+    force_clear, outside the pair style.
 
     rebuild_every > 0: every that many steps (the first one included) the step is a list-rebuild
     step, as LAMMPS signals it (neighbor->ago == 0; here lk_set_list_epoch): the library redoes
     its once-per-list work (tile lists, incidence lists, matrix copy) inside that step. The list
-    itself is the same one (the engine's rebuild is not the pair style's time)."""
+    itself is the same one (the engine's rebuild is not the pair style's time).
+
+    Returns run(n), which makes n steps and returns the last step's lk_step_info."""
     import ctypes
 
     from lammps_jax_amd import _native as N
+    from lammps_jax_amd import harness
 
+    hl = harness._load()
     lib, h, s = pj.h.lib, pj.h.ptr, pj.system
     lst = s.list
     flags = (N.LK_ENERGY if eflag else 0) | (N.LK_VIRIAL if vflag else 0)
-    vp = ctypes.c_void_p
-    stream = vp(pj.stream())
-    args = (h, stream, vp(pj.x.data_ptr()), vp(pj.type.data_ptr()), ctypes.c_int(s.nall),
-            vp(pj.ilist.data_ptr()), vp(pj.numneigh.data_ptr()), vp(pj.neighbors.data_ptr()),
-            ctypes.c_long(lst["stride"]), ctypes.c_int(lst["inum"]), ctypes.c_int(lst["gnum"]),
-            ctypes.c_int(lst["maxneighs"]), ctypes.c_int(s.nlocal), ctypes.c_int(s.nghost),
-            ctypes.c_int(flags), ctypes.c_double(pj.scale), vp(pj.f.data_ptr()))
+    addr = lambda fn: ctypes.cast(fn, ctypes.c_void_p).value  # noqa: E731
+    fns = harness.StepFns(addr(lib.lk_pack_compute), addr(lib.lk_step_result),
+                          addr(lib.lk_set_list_epoch))
+    args = harness.StepArgs(pj.x.data_ptr(), pj.type.data_ptr(), s.nall, pj.ilist.data_ptr(),
+                            pj.numneigh.data_ptr(), pj.neighbors.data_ptr(), lst["stride"],
+                            lst["inum"], lst["gnum"], lst["maxneighs"], s.nlocal, s.nghost, flags,
+                            pj.scale, pj.f.data_ptr())
     info = N.LkStepInfo()
-    ref = ctypes.byref(info)
-    pack_compute, step_result = lib.lk_pack_compute, lib.lk_step_result
+    epoch, calls, rebuilds = ctypes.c_long(pj.list_epoch), ctypes.c_long(0), ctypes.c_int(0)
+    stream = ctypes.c_void_p(pj.stream())
 
-    set_epoch = lib.lk_set_list_epoch
-    calls = [0]
-
-    def step():
-        if rebuild_every > 0 and calls[0] % rebuild_every == 0:
-            pj.list_epoch += 1
-            if set_epoch(h, ctypes.c_long(pj.list_epoch)) != N.LK_OK:
-                raise N.LammpsJaxError(1, pj.h.error())
-            step.rebuilds += 1
-        calls[0] += 1
-        if pack_compute(*args) != N.LK_OK or step_result(h, stream, ref) != N.LK_OK:
-            raise N.LammpsJaxError(1, pj.h.error())
-        if info.edge_overflow:
+    def run(n: int):
+        rc = hl.lkh_run_steps(ctypes.byref(fns), h, stream, ctypes.byref(args), int(n),
+                              int(rebuild_every), ctypes.byref(epoch), ctypes.byref(calls),
+                              ctypes.byref(rebuilds), ctypes.byref(info))
+        pj.list_epoch = epoch.value
+        run.rebuilds = rebuilds.value
+        if rc == N.LK_ERR_CAPACITY and info.edge_overflow:
             raise N.LammpsJaxError(N.LK_ERR_CAPACITY, "LAMMPS-JAX edge capacity exceeded")
+        if rc != N.LK_OK:
+            raise N.LammpsJaxError(rc, pj.h.error())
         return info
 
-    step.rebuilds = 0
-    return step
+    run.rebuilds = 0
+    return run
 
 
 def main() -> int:
@@ -344,13 +345,11 @@ def main() -> int:
           flush=True)
 
     step = lean_step(pj)
-    for _ in range(args.warmup):
-        info = step()
+    info = step(args.warmup)
     torch.cuda.synchronize(dev)
     step = lean_step(pj, rebuild_every=args.rebuild_every)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        info = step()
+    info = step(args.steps)
     torch.cuda.synchronize(dev)
     elapsed = time.perf_counter() - t0
     rebuilds_timed = step.rebuilds
@@ -369,8 +368,7 @@ def main() -> int:
     pj.h.timing_enable(True)
     step_t = lean_step(pj, rebuild_every=args.rebuild_every)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step_t()
+    step_t(args.steps)
     torch.cuda.synchronize(dev)
     events_ms = 1e3 * (time.perf_counter() - t0) / args.steps
     stages = pj.h.timing()
@@ -379,8 +377,7 @@ def main() -> int:
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
     step_f = lean_step(pj, eflag=False, vflag=False, rebuild_every=args.rebuild_every)
-    for _ in range(args.steps):
-        step_f()
+    step_f(args.steps)
     torch.cuda.synchronize(dev)
     forces_only_ms = 1e3 * (time.perf_counter() - t0) / args.steps
     # packing alone: the separate entry points (lk_pack_atoms, lk_pack_edges) with their timers

@@ -58,7 +58,7 @@ def hip_inputs() -> list[Path]:
 
 
 def harness_inputs() -> list[Path]:
-    return [CSRC / "harness" / "lk_harness.cpp"]
+    return [CSRC / "harness" / "lk_harness.cpp", REPO / "include" / "lk_hip.h"]
 
 
 def _stamp_path(lib: Path) -> Path:
@@ -116,7 +116,7 @@ def build_hip() -> Path:
     return out
 
 
-HARNESS_FLAGS = ["-O3", "-fopenmp", "-fPIC", "-shared", "-std=c++17"]
+HARNESS_FLAGS = ["-O3", "-fopenmp", "-fPIC", "-shared", "-std=c++17", f"-I{REPO / 'include'}"]
 
 
 def build_harness() -> Path:

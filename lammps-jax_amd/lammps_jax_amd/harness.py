@@ -21,6 +21,23 @@ LIST_FULL_GHOST = 2
 _lib = None
 
 
+class StepFns(ctypes.Structure):
+    """The library entry points lkh_run_steps calls (addresses of lk_pack_compute,
+    lk_step_result and lk_set_list_epoch)."""
+    _fields_ = [("pack_compute", ctypes.c_void_p), ("step_result", ctypes.c_void_p),
+                ("set_list_epoch", ctypes.c_void_p)]
+
+
+class StepArgs(ctypes.Structure):
+    """lk_pack_compute's arguments past the handle and stream, as the engine passes them."""
+    _fields_ = [("x", ctypes.c_void_p), ("type", ctypes.c_void_p), ("nall", ctypes.c_int),
+                ("ilist", ctypes.c_void_p), ("numneigh", ctypes.c_void_p),
+                ("neighbors", ctypes.c_void_p), ("stride", ctypes.c_long),
+                ("inum", ctypes.c_int), ("gnum", ctypes.c_int), ("maxneighs", ctypes.c_int),
+                ("nlocal", ctypes.c_int), ("nghost", ctypes.c_int), ("flags", ctypes.c_int),
+                ("scale", ctypes.c_double), ("f", ctypes.c_void_p)]
+
+
 def _load() -> ctypes.CDLL:
     global _lib
     if _lib is not None:
@@ -55,6 +72,10 @@ def _load() -> ctypes.CDLL:
     lib.lkh_nswaps.restype = ip
     lib.lkh_swap.argtypes = [vp, ip, ctypes.POINTER(ip)]
     lib.lkh_swap.restype = ip
+    lib.lkh_run_steps.argtypes = [ctypes.POINTER(StepFns), vp, vp, ctypes.POINTER(StepArgs), ip,
+                                  ip, ctypes.POINTER(lp), ctypes.POINTER(lp),
+                                  ctypes.POINTER(ip), vp]
+    lib.lkh_run_steps.restype = ip
     lib.lkh_swap_sendlist.argtypes = [vp, ip]
     lib.lkh_swap_sendlist.restype = ctypes.POINTER(ctypes.c_int)
     _lib = lib
