@@ -25,6 +25,8 @@
 
 #include <algorithm>
 #include <climits>
+#include <cmath>
+#include <limits>
 
 #include <hipcub/hipcub.hpp>
 
@@ -607,6 +609,8 @@ struct TwoSided {
   int nblk;             // 64-atom tiles over nall
   const uint32_t *inc_bit;  // list-built entries: address of the slot's validity bit
   const uint32_t *bits;     // the pack's validity bits of this step
+  double cutsq_pack;        // the pack's filter: rsq <= cutsq in float64 (cpp:91)
+  float cutsq_lo, cutsq_hi; // cutsq_pack rounded down and up to float
   const int *ghost_flag;    // 1 when a packed edge starts on a ghost row (the pack's flag)
   FusedPack pack;           // a fused pack of this step: tail reset and counts (else unused)
 };
@@ -617,17 +621,11 @@ __device__ __forceinline__ int inc_len(const TwoSided &t, int a, int b)
   return t.len ? t.len[a] : inc_off(t.loc, t.part, a + 1) - b;
 }
 
-// Whether the pack kept an entry's list slot this step (lists built from packed edges: always),
-// split in two so the sweeps can put each load in its round trip: the entry's bit address goes
-// out with the entry itself, the validity word with the neighbour's record.
+// The validity-bit address of an entry's list slot (lists built from packed edges: none), loaded
+// with the entry itself.
 __device__ __forceinline__ uint32_t slot_bit_address(const TwoSided &t, int q)
 {
   return t.inc_bit ? t.inc_bit[q] : 0u;
-}
-
-__device__ __forceinline__ uint32_t slot_word(const TwoSided &t, uint32_t ba)
-{
-  return t.inc_bit ? t.bits[ba >> 5] : ~0u;
 }
 
 __device__ __forceinline__ bool word_has(uint32_t word, uint32_t ba)
@@ -635,8 +633,74 @@ __device__ __forceinline__ bool word_has(uint32_t word, uint32_t ba)
   return ((word >> (ba & 31u)) & 1u) != 0;
 }
 
-// The same two loads with the filter as a template flag (BITS: t.inc_bit is set) rather than a
-// null test, which would put a branch around them, for the force sweep's prefetching walk.
+// Whether the pack kept an entry's list slot this step, decided from the entry's own geometry
+// wherever that decides it, so the sweeps gather no validity word. The pack keeps rsq <= cutsq,
+// rsq formed in float64 from the engine's positions without contraction (cpp:84-91); for a
+// list-built entry that is the whole per-step filter (the list's other filters are applied when
+// the lists are built). Float64 records hold those positions, and r2 is the same sum of the same
+// squared differences (negated or not): the same value, so the same decision.
+// Float32 records hold them rounded to float. With u = 2^-24, l1 = |dx| + |dy| + |dz| and
+// s = l1 + (the 1-norms of both positions), each difference is within
+// b_c = u (|d_c| + |x_a,c| + |x_o,c|) / (1 - u) of the float64 one, so
+// |sum d^2 - sum D^2| <= sum b_c (2|d_c| + b_c) <= u s (2 l1 + u s) / (1 - u)^2, and r2 is within
+// 3u r2 / (1 - 3u) of sum d^2 (float64 rounding adds far less). band = 2u (s (2 l1 + u s) + 4 r2),
+// computed in float, exceeds twice that bound and at least 8u r2, which covers the rounding of
+// r2 +- band against cutsq rounded down (up) to float. Only an r2 inside the band reads the
+// slot's validity bit. Per row, BandRow bounds the band of every entry the model's cutoff lets
+// through (l1 <= sqrt(3) rc_model, and the neighbour's 1-norm <= the row's + l1), so most entries
+// are decided by one comparison with a row threshold. Lists built from packed edges (no bit
+// addresses) hold kept slots only.
+template <typename S>
+struct BandRow {
+  S sa;       // the row atom's 1-norm
+  S fast_lo;  // r2 <= fast_lo: kept
+  S fast_hi;  // r2 > fast_hi: dropped
+};
+
+template <typename S>
+__device__ __forceinline__ BandRow<S> band_row(const TwoSided &t, const Atom4<S> &xa, S cutsq_model)
+{
+  BandRow<S> br{};
+  if constexpr (sizeof(S) == 4) {
+    constexpr float u = 5.9604645e-8f;  // 2^-24
+    br.sa = fabsf(xa.x) + fabsf(xa.y) + fabsf(xa.z);
+    const float l1m = 1.7320509f * sqrtf(cutsq_model) * 1.0001f;
+    const float sm = 2.0f * (br.sa + l1m);
+    const float band = 2.0f * u * (sm * (2.0f * l1m + u * sm) + 4.0f * t.cutsq_hi) * 1.0001f;
+    br.fast_lo = t.cutsq_lo - 1.25f * band;
+    br.fast_hi = t.cutsq_hi + 1.25f * band;
+  }
+  return br;
+}
+
+template <typename S>
+__device__ __forceinline__ bool slot_kept(const TwoSided &t, uint32_t ba, S r2, S dx, S dy, S dz,
+                                          const BandRow<S> &br, const Atom4<S> &xo)
+{
+  if (!t.inc_bit) return true;
+  if constexpr (sizeof(S) == 8) {
+    (void)ba;
+    (void)dx;
+    (void)dy;
+    (void)dz;
+    (void)br;
+    (void)xo;
+    return !(r2 > t.cutsq_pack);
+  } else {
+    if (r2 <= br.fast_lo) return true;
+    if (r2 > br.fast_hi) return false;
+    constexpr float u = 5.9604645e-8f;  // 2^-24
+    const float l1 = fabsf(dx) + fabsf(dy) + fabsf(dz);
+    const float s = l1 + br.sa + (fabsf(xo.x) + fabsf(xo.y) + fabsf(xo.z));
+    const float band = 2.0f * u * (s * (2.0f * l1 + u * s) + 4.0f * r2);
+    if (r2 + band <= t.cutsq_lo) return true;
+    if (r2 - band > t.cutsq_hi) return false;
+    return word_has(t.bits[ba >> 5], ba);
+  }
+}
+
+// The same load with the filter as a template flag (BITS: t.inc_bit is set) rather than a null
+// test, which would put a branch around it, for the force sweep's prefetching walk.
 template <bool BITS>
 __device__ __forceinline__ uint32_t slot_bit_address_of(const TwoSided &t, int q)
 {
@@ -644,16 +708,9 @@ __device__ __forceinline__ uint32_t slot_bit_address_of(const TwoSided &t, int q
   return 0u;
 }
 
-template <bool BITS>
-__device__ __forceinline__ uint32_t slot_word_of(const TwoSided &t, uint32_t ba)
-{
-  if constexpr (BITS) return t.bits[ba >> 5];
-  return ~0u;
-}
-
 // The fp64 force sweep's walk over its atom's incident entries k = gl, gl + 16, ... with the
 // next entry (and its bit address) in flight while the current one is computed. Per entry the
-// sweep issues, in this order: the neighbour's record and F', the validity word, then advance():
+// sweep issues, in this order: the neighbour's record and F', then advance():
 // the next entry's loads go out after this entry's gathers, so waiting for the gathers never
 // waits for them. A skipped entry gathers its own row's record instead (cached), so no branch
 // surrounds a load. (The density and LJ sweeps measured slower with it, also at eight waves per
@@ -713,20 +770,20 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
     S rho = S(0), ep = S(0);
     if (a < t.nall) {
       const Atom4<S> xa = m.atoms[a];
+      const BandRow<S> br = band_row(t, xa, m.cutsq);
       const int za = clamp_species(static_cast<int>(xa.w), m.n_el);
       const int b = inc_off(t.loc, t.part, a);
       const int L = HALF ? inc_off(t.loc, t.part, a + 1) - b : inc_len(t, a, b);  // half: no folds
       // Two entries per lane at a time (k and k + 16): both entries load together, then both
-      // records with their validity words, so a pair of entries costs two memory round trips.
-      // The record gather goes out with the validity word's, not after it (a dropped slot's
-      // record is simply not used); a skipped or missing entry gathers the row's own record.
-      auto dens = [&](uint32_t v, uint32_t ba, const Atom4<S> &xo, uint32_t word) {
+      // records, so a pair of entries costs two memory round trips; a skipped or missing entry
+      // gathers the row's own record.
+      auto dens = [&](uint32_t v, uint32_t ba, const Atom4<S> &xo) {
         const bool in = (v >> 31) != 0;
         if (!HALF && in) return;  // plain: density and pair energy stay on the sender
-        if (!word_has(word, ba)) return;
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
         if (!(r2 < m.cutsq)) return;
+        if (!slot_kept(t, ba, r2, dx, dy, dz, br, xo)) return;
         const S rinv = rsqrt_nr(r2);
         const S rr = r2 * rinv;
         const Locator<S> L2 = locate_mul(rr, m.inv_dr, m.nr);
@@ -746,9 +803,8 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
         const bool s1 = !HALF && (v1 >> 31) != 0, s2 = !two || (!HALF && (v2 >> 31) != 0);
         const Atom4<S> x1 = m.atoms[s1 ? a : static_cast<int>(v1 & kIncAtom)];
         const Atom4<S> x2 = m.atoms[s2 ? a : static_cast<int>(v2 & kIncAtom)];
-        const uint32_t w1 = slot_word(t, ba1), w2 = slot_word(t, ba2);
-        dens(v1, ba1, x1, w1);
-        if (two) dens(v2, ba2, x2, w2);
+        dens(v1, ba1, x1);
+        if (two) dens(v2, ba2, x2);
       }
     }
     rho = group_sum(rho);
@@ -870,18 +926,18 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
     S fx = S(0), fy = S(0), fz = S(0), ep = S(0);
     if (a < t.nall) {
       const Atom4<S> xa = m.atoms[a];
+      const BandRow<S> br = band_row(t, xa, m.cutsq);
       const int za = clamp_species(static_cast<int>(xa.w), m.n_el);
       const S fpa = m.fp[a];
       const int b = inc_off(t.loc, t.part, a);
       const int L = HALF ? inc_off(t.loc, t.part, a + 1) - b : inc_len(t, a, b);  // half: no folds
       // The gathers of an entry: its neighbour's record and F' (the row's own when the entry
-      // is skipped, so no branch surrounds a load) and its validity word.
+      // is skipped, so no branch surrounds a load).
       struct Gathered {
         uint32_t v, ba;
         bool skip;
         Atom4<S> xo;
         S fpo;
-        uint32_t word;
       };
       auto gather = [&](uint32_t v, uint32_t ba, bool present) -> Gathered {
         Gathered e;
@@ -895,11 +951,10 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
         e.skip = !present || (!HALF && (paired ? !(ca || co) : !(in ? co : ca)));
         e.xo = m.atoms[e.skip ? a : o];
         e.fpo = m.fp[(HALF || in || paired) && !e.skip ? o : a];
-        e.word = slot_word_of<BITS>(t, ba);
         return e;
       };
       auto edge = [&](const Gathered &e) {
-        if (e.skip || !word_has(e.word, e.ba)) return;
+        if (e.skip) return;
         const uint32_t v = e.v;
         const Atom4<S> &xo = e.xo;
         const S fpo = e.fpo;
@@ -910,6 +965,7 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
         if (!(r2 < m.cutsq)) return;
+        if (BITS && !slot_kept(t, e.ba, r2, dx, dy, dz, br, xo)) return;
         const S rinv = rsqrt_nr(r2);
         const S rr = r2 * rinv;
         const Locator<S> L2 = locate_mul(rr, m.inv_dr, m.nr);
@@ -1044,6 +1100,7 @@ void k_lj_inc(LjModel<S> m, TwoSided t)
     S en = S(0), fx = S(0), fy = S(0), fz = S(0);
     if (a < t.nall) {
       const Atom4<S> xa = m.atoms[a];
+      const BandRow<S> br = band_row(t, xa, m.cutsq);
       const int b = inc_off(t.loc, t.part, a);
       const int L = inc_len(t, a, b);
       // counted ends of an entry: its sender's row, or both rows of a folded pair (the pair
@@ -1053,11 +1110,12 @@ void k_lj_inc(LjModel<S> m, TwoSided t)
         const int co = static_cast<int>(v & kIncAtom) < erows ? 1 : 0;
         return (in ? 0 : (a < erows ? 1 : 0)) + ((in || (v & kIncPaired)) ? co : 0);
       };
-      auto pair = [&](uint32_t v, uint32_t ba, int w, const Atom4<S> &xo, uint32_t word) {
-        if (w == 0 || !word_has(word, ba)) return;
+      auto pair = [&](uint32_t v, uint32_t ba, int w, const Atom4<S> &xo) {
+        if (w == 0) return;
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
         if (!(r2 > tiny && r2 < m.cutsq)) return;  // export_model.py:22
+        if (!slot_kept(t, ba, r2, dx, dy, dz, br, xo)) return;
         const S inv_r2 = m.sigsq / r2;
         const S inv_r6 = inv_r2 * inv_r2 * inv_r2;
         if (!(v >> 31)) en += m.edge_scale * (m.four_eps * (inv_r6 * inv_r6 - inv_r6));
@@ -1068,8 +1126,7 @@ void k_lj_inc(LjModel<S> m, TwoSided t)
         fz += coef * dz;
       };
       // Two entries per lane at a time (k and k + 16), as in the density sweep: both entries,
-      // then both records with their validity words (an uncounted or missing entry gathers the
-      // row's own record).
+      // then both records (an uncounted or missing entry gathers the row's own record).
       for (int k = gl; k < L; k += 2 * kGroup) {
         const bool two = k + kGroup < L;
         const int q1 = b + k, q2 = b + (two ? k + kGroup : k);
@@ -1079,9 +1136,8 @@ void k_lj_inc(LjModel<S> m, TwoSided t)
         const int w1 = ends(v1), w2 = two ? ends(v2) : 0;
         const Atom4<S> x1 = m.atoms[w1 ? static_cast<int>(v1 & kIncAtom) : a];
         const Atom4<S> x2 = m.atoms[w2 ? static_cast<int>(v2 & kIncAtom) : a];
-        const uint32_t wd1 = slot_word(t, ba1), wd2 = slot_word(t, ba2);
-        pair(v1, ba1, w1, x1, wd1);
-        pair(v2, ba2, w2, x2, wd2);
+        pair(v1, ba1, w1, x1);
+        pair(v2, ba2, w2, x2);
       }
     }
     en = group_sum(en);
@@ -1325,6 +1381,13 @@ static TwoSided two_sided_args(Handle &h, int nlocal, int nghost, const double *
   t.nblk = (t.nall + kRowAtoms - 1) / kRowAtoms;
   t.inc_bit = nullptr;
   t.bits = h.d_bits;
+  t.cutsq_pack = h.contract.cutoff * h.contract.cutoff;
+  t.cutsq_lo = static_cast<float>(t.cutsq_pack);
+  t.cutsq_hi = t.cutsq_lo;
+  if (static_cast<double>(t.cutsq_lo) > t.cutsq_pack)
+    t.cutsq_lo = std::nextafter(t.cutsq_lo, -std::numeric_limits<float>::infinity());
+  if (static_cast<double>(t.cutsq_hi) < t.cutsq_pack)
+    t.cutsq_hi = std::nextafter(t.cutsq_hi, std::numeric_limits<float>::infinity());
   t.ghost_flag = &h.d_result->ghost_sender;
   t.pack = FusedPack{};
   return t;
