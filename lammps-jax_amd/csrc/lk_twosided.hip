@@ -1650,10 +1650,11 @@ __global__ __launch_bounds__(256) void k_lj_edge_force(LjModel<S> m, EdgeOut<S> 
   red[threadIdx.x] = en;
   __syncthreads();
   for (int off = blockDim.x / 2; off >= 1; off >>= 1) {
-    if (threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+    if (static_cast<int>(threadIdx.x) < off) red[threadIdx.x] += red[threadIdx.x + off];
     __syncthreads();
   }
-  if (threadIdx.x == 0 && blockIdx.x < o.ntiles) o.partials[8L * blockIdx.x + 7] = red[0];
+  if (threadIdx.x == 0 && static_cast<int>(blockIdx.x) < o.ntiles)
+    o.partials[8L * blockIdx.x + 7] = red[0];
   edge_tail_and_slots(o, ne);
 }
 
