@@ -198,6 +198,9 @@ struct Handle {
     unsigned long long *box = nullptr;  // [6] bounding box of the rows (ordered-integer doubles)
     int rows_cap = 0, tiles_cap = 0, groups = 0;
     IncKey key;                     // the list (and epoch) they were built from
+    const int *order_ilist = nullptr;  // the ilist and row count the row order was sorted for
+    int order_rows = -1;
+    int order_reuses = 0;              // list rebuilds since that sort that kept its order
   } tl;
 
   size_t scalar_bytes() const { return contract.precision == LK_FLOAT64 ? 8 : 4; }

@@ -681,6 +681,12 @@ hipError_t ensure_tile_list(Handle &h, int rows, int maxneighs)
   return hipSuccess;
 }
 
+// A list rebuild of the same rows (the engine's ilist and row count) keeps the previous build's
+// row order for up to this many rebuilds before sorting the rows again: atoms move little between
+// rebuilds, so the order stays spatially coherent, and any order of the rows gives the same sums
+// per row (only the 64-row energy and virial partials group differently).
+constexpr int kTileOrderReuse = 8;
+
 hipError_t build_tile_list(Handle &h, hipStream_t s, const double *x, const int *ilist,
                            const int *numneigh, const int *neighbors, long stride, int rows,
                            int maxneighs)
@@ -689,18 +695,25 @@ hipError_t build_tile_list(Handle &h, hipStream_t s, const double *x, const int 
   const int tiles = (rows + kTileRows - 1) / kTileRows;
   const int positions = tiles * kTileRows;
   StageTimer timer(h, s, "tile_list");
-  hipLaunchKernelGGL(k_tile_bbox_init, dim3(1), dim3(64), 0, s, T.box);
-  // few blocks (one atomic per component and block), each thread striding over many rows
-  const int bbox_blocks = (rows + 255) / 256 < 64 ? (rows + 255) / 256 : 64;
-  hipLaunchKernelGGL(k_tile_bbox, dim3(bbox_blocks), dim3(256), 0, s, ilist, x, rows,
-                     h.contract.max_atoms, T.box);
-  hipLaunchKernelGGL(k_tile_keys, dim3((rows + 255) / 256), dim3(256), 0, s, ilist, x, rows,
-                     h.contract.max_atoms, T.box, T.keys, T.rows_in);
-  size_t bytes = T.sort_bytes;
-  hipError_t e = hipcub::DeviceRadixSort::SortPairs(T.sort_tmp, bytes, T.keys, T.keys_sorted,
-                                                    T.rows_in, T.order, rows, 0,
-                                                    3 * kTileGridBits, s);
-  if (e != hipSuccess) return e;
+  if (T.order_ilist == ilist && T.order_rows == rows && T.order_reuses < kTileOrderReuse) {
+    ++T.order_reuses;
+  } else {
+    hipLaunchKernelGGL(k_tile_bbox_init, dim3(1), dim3(64), 0, s, T.box);
+    // few blocks (one atomic per component and block), each thread striding over many rows
+    const int bbox_blocks = (rows + 255) / 256 < 64 ? (rows + 255) / 256 : 64;
+    hipLaunchKernelGGL(k_tile_bbox, dim3(bbox_blocks), dim3(256), 0, s, ilist, x, rows,
+                       h.contract.max_atoms, T.box);
+    hipLaunchKernelGGL(k_tile_keys, dim3((rows + 255) / 256), dim3(256), 0, s, ilist, x, rows,
+                       h.contract.max_atoms, T.box, T.keys, T.rows_in);
+    size_t bytes = T.sort_bytes;
+    hipError_t e = hipcub::DeviceRadixSort::SortPairs(T.sort_tmp, bytes, T.keys, T.keys_sorted,
+                                                      T.rows_in, T.order, rows, 0,
+                                                      3 * kTileGridBits, s);
+    if (e != hipSuccess) return e;
+    T.order_ilist = ilist;
+    T.order_rows = rows;
+    T.order_reuses = 0;
+  }
   hipLaunchKernelGGL(k_tile_rows, dim3((positions + 255) / 256), dim3(256), 0, s, T.order, ilist,
                      numneigh, rows, positions, h.contract.max_atoms, maxneighs, T.atom, T.nn);
   TileBuild b;

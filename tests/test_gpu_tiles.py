@@ -3,9 +3,10 @@
 The fused float64 EAM step orders the list rows along a Hilbert curve, cuts them into 128-row
 tiles and stages each tile's neighbour union in LDS; a tile whose union exceeds 1,280 atoms walks
 the engine's list from memory instead. These cases drive both kinds of tile in one step, a list
-handed over in scrambled row order, and steps that reuse the tile lists (positions moved, same
-list) next to steps after a rebuild. Bars: the reference's float64 ones (forces within 1e-11
-absolute, energy within 1e-13 per atom, virial within 1e-12 relative)."""
+handed over in scrambled row order, steps that reuse the tile lists (positions moved, same
+list) next to steps after a rebuild, and rebuilds that keep the previous row order. Bars: the
+reference's float64 ones (forces within 1e-11 absolute, energy within 1e-13 per atom, virial
+within 1e-12 relative)."""
 
 from __future__ import annotations
 
@@ -153,6 +154,32 @@ def test_tile_lists_reused_until_the_list_changes(gpu):
     pj.rebind(sysm2)
     print("tile rebuild step", flush=True)
     _check(wl, sysm2, pj, pj.compute(), "after the rebuild")
+
+
+def test_row_order_across_rebuilds_of_the_same_rows(gpu):
+    """A rebuild of the same rows into the same list arrays keeps the previous rebuild's tile
+    order for up to eight rebuilds before sorting the rows again. Here the rows arrive in a new
+    order at every rebuild, written into the same device arrays, thirteen rebuilds in a row with a
+    list over half of the owned atoms in the middle (a new row count: a fresh sort), and every
+    step matches the oracle over that rebuild's list."""
+    wl = systems.make_workload("eam_alloy_131k", cells=(5, 5, 5), seed=8)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    pj = PairJax(sysm, ("eam", wl.tables), precision=8, accumulation="onesided")
+    ptr = pj.ilist.data_ptr()
+    inum = lst["inum"]
+    rng = np.random.default_rng(4)
+    _check(wl, sysm, pj, pj.compute(), "first build")
+    for k in range(13):
+        rows = inum // 2 if k == 5 else inum
+        ilist = np.ascontiguousarray(lst["ilist"][:inum][rng.permutation(inum)][:rows])
+        sysm.list = dict(lst, ilist=ilist, inum=rows)
+        pj.ilist[:rows].copy_(pj.torch.from_numpy(ilist).to(pj.device))
+        assert pj.ilist.data_ptr() == ptr
+        pj.list_epoch += 1
+        pj.h.set_list_epoch(pj.list_epoch)
+        print(f"row order rebuild {k} rows={rows}", flush=True)
+        _check(wl, sysm, pj, pj.compute(), f"rebuild {k}")
 
 
 def test_tile_steps_between_split_steps(gpu):
