@@ -621,13 +621,6 @@ __device__ __forceinline__ int inc_len(const TwoSided &t, int a, int b)
   return t.len ? t.len[a] : inc_off(t.loc, t.part, a + 1) - b;
 }
 
-// The validity-bit address of an entry's list slot (lists built from packed edges: none), loaded
-// with the entry itself.
-__device__ __forceinline__ uint32_t slot_bit_address(const TwoSided &t, int q)
-{
-  return t.inc_bit ? t.inc_bit[q] : 0u;
-}
-
 __device__ __forceinline__ bool word_has(uint32_t word, uint32_t ba)
 {
   return ((word >> (ba & 31u)) & 1u) != 0;
@@ -645,8 +638,8 @@ __device__ __forceinline__ bool word_has(uint32_t word, uint32_t ba)
 // |sum d^2 - sum D^2| <= sum b_c (2|d_c| + b_c) <= u s (2 l1 + u s) / (1 - u)^2, and r2 is within
 // 3u r2 / (1 - 3u) of sum d^2 (float64 rounding adds far less). band = 2u (s (2 l1 + u s) + 4 r2),
 // computed in float, exceeds twice that bound and at least 8u r2, which covers the rounding of
-// r2 +- band against cutsq rounded down (up) to float. Only an r2 inside the band reads the
-// slot's validity bit. Per row, BandRow bounds the band of every entry the model's cutoff lets
+// r2 +- band against cutsq rounded down (up) to float. Only an r2 inside the band loads the
+// bit address of entry q's slot and then its validity word; no other entry reads either. Per row, BandRow bounds the band of every entry the model's cutoff lets
 // through (l1 <= sqrt(3) rc_model, and the neighbour's 1-norm <= the row's + l1), so most entries
 // are decided by one comparison with a row threshold. Lists built from packed edges (no bit
 // addresses) hold kept slots only.
@@ -674,12 +667,12 @@ __device__ __forceinline__ BandRow<S> band_row(const TwoSided &t, const Atom4<S>
 }
 
 template <typename S>
-__device__ __forceinline__ bool slot_kept(const TwoSided &t, uint32_t ba, S r2, S dx, S dy, S dz,
+__device__ __forceinline__ bool slot_kept(const TwoSided &t, int q, S r2, S dx, S dy, S dz,
                                           const BandRow<S> &br, const Atom4<S> &xo)
 {
   if (!t.inc_bit) return true;
   if constexpr (sizeof(S) == 8) {
-    (void)ba;
+    (void)q;
     (void)dx;
     (void)dy;
     (void)dz;
@@ -695,38 +688,30 @@ __device__ __forceinline__ bool slot_kept(const TwoSided &t, uint32_t ba, S r2, 
     const float band = 2.0f * u * (s * (2.0f * l1 + u * s) + 4.0f * r2);
     if (r2 + band <= t.cutsq_lo) return true;
     if (r2 - band > t.cutsq_hi) return false;
+    const uint32_t ba = t.inc_bit[q];
     return word_has(t.bits[ba >> 5], ba);
   }
 }
 
-// The same load with the filter as a template flag (BITS: t.inc_bit is set) rather than a null
-// test, which would put a branch around it, for the force sweep's prefetching walk.
-template <bool BITS>
-__device__ __forceinline__ uint32_t slot_bit_address_of(const TwoSided &t, int q)
-{
-  if constexpr (BITS) return t.inc_bit[q];
-  return 0u;
-}
-
 // The fp64 force sweep's walk over its atom's incident entries k = gl, gl + 16, ... with the
-// next entry (and its bit address) in flight while the current one is computed. Per entry the
-// sweep issues, in this order: the neighbour's record and F', then advance():
-// the next entry's loads go out after this entry's gathers, so waiting for the gathers never
-// waits for them. A skipped entry gathers its own row's record instead (cached), so no branch
-// surrounds a load. (The density and LJ sweeps measured slower with it, also at eight waves per
-// SIMD: C4 density 404 -> 464 us, C5 LJ 181 -> 183 us; they take two entries at a time instead.)
-template <bool BITS>
+// next entry in flight while the current one is computed. Per entry the sweep issues, in this
+// order: the neighbour's record and F', then advance(): the next entry's load goes out after
+// this entry's gathers, so waiting for the gathers never waits for it. A skipped entry gathers
+// its own row's record instead (cached), so no branch surrounds a load. (The density and LJ
+// sweeps measured slower with it, also at eight waves per SIMD: C4 density 404 -> 464 us, C5 LJ
+// 181 -> 183 us; they take two entries at a time instead.)
 struct IncCursor {
-  uint32_t v = 0, ba = 0;
+  uint32_t v = 0;
+  int q = 0;  // the entry v was loaded from
   int b, last;
   __device__ __forceinline__ IncCursor(const TwoSided &t, int b_, int L, int gl) : b(b_), last(b_ + L - 1)
   {
     if (gl < L) load(t, b + gl);
   }
-  __device__ __forceinline__ void load(const TwoSided &t, int q)
+  __device__ __forceinline__ void load(const TwoSided &t, int q_)
   {
-    v = static_cast<uint32_t>(t.inc[q]);
-    ba = slot_bit_address_of<BITS>(t, q);
+    v = static_cast<uint32_t>(t.inc[q_]);
+    q = q_;
   }
   __device__ __forceinline__ void advance(const TwoSided &t, int k)
   {
@@ -777,13 +762,13 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
       // Two entries per lane at a time (k and k + 16): both entries load together, then both
       // records, so a pair of entries costs two memory round trips; a skipped or missing entry
       // gathers the row's own record.
-      auto dens = [&](uint32_t v, uint32_t ba, const Atom4<S> &xo) {
+      auto dens = [&](uint32_t v, int q, const Atom4<S> &xo) {
         const bool in = (v >> 31) != 0;
         if (!HALF && in) return;  // plain: density and pair energy stay on the sender
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
         if (!(r2 < m.cutsq)) return;
-        if (!slot_kept(t, ba, r2, dx, dy, dz, br, xo)) return;
+        if (!slot_kept(t, q, r2, dx, dy, dz, br, xo)) return;
         const S rinv = rsqrt_nr(r2);
         const S rr = r2 * rinv;
         const Locator<S> L2 = locate_mul(rr, m.inv_dr, m.nr);
@@ -799,12 +784,11 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
         const int q1 = b + k, q2 = b + (two ? k + kGroup : k);
         const uint32_t v1 = static_cast<uint32_t>(t.inc[q1]);
         const uint32_t v2 = static_cast<uint32_t>(t.inc[q2]);
-        const uint32_t ba1 = slot_bit_address(t, q1), ba2 = slot_bit_address(t, q2);
         const bool s1 = !HALF && (v1 >> 31) != 0, s2 = !two || (!HALF && (v2 >> 31) != 0);
         const Atom4<S> x1 = m.atoms[s1 ? a : static_cast<int>(v1 & kIncAtom)];
         const Atom4<S> x2 = m.atoms[s2 ? a : static_cast<int>(v2 & kIncAtom)];
-        dens(v1, ba1, x1);
-        if (two) dens(v2, ba2, x2);
+        dens(v1, q1, x1);
+        if (two) dens(v2, q2, x2);
       }
     }
     rho = group_sum(rho);
@@ -934,15 +918,16 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
       // The gathers of an entry: its neighbour's record and F' (the row's own when the entry
       // is skipped, so no branch surrounds a load).
       struct Gathered {
-        uint32_t v, ba;
+        uint32_t v;
+        int q;  // the entry's index (its slot's bit address is read only near the cutoff)
         bool skip;
         Atom4<S> xo;
         S fpo;
       };
-      auto gather = [&](uint32_t v, uint32_t ba, bool present) -> Gathered {
+      auto gather = [&](uint32_t v, int q, bool present) -> Gathered {
         Gathered e;
         e.v = v;
-        e.ba = ba;
+        e.q = q;
         const bool in = (v >> 31) != 0;
         const int o = static_cast<int>(v & kIncAtom);
         // plain: an uncounted sender gives no gradient; a folded pair counts each counted end
@@ -965,7 +950,7 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
         if (!(r2 < m.cutsq)) return;
-        if (BITS && !slot_kept(t, e.ba, r2, dx, dy, dz, br, xo)) return;
+        if (BITS && !slot_kept(t, e.q, r2, dx, dy, dz, br, xo)) return;
         const S rinv = rsqrt_nr(r2);
         const S rr = r2 * rinv;
         const Locator<S> L2 = locate_mul(rr, m.inv_dr, m.nr);
@@ -1005,27 +990,25 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
       // computed (C4 force sweep 750 -> 739 us). float64 takes one entry at a time with the next
       // in flight (two at a time measured 2% slower there, at 97 VGPRs and four waves per SIMD).
       if constexpr (sizeof(S) == 8) {
-        IncCursor<BITS> cur(t, b, L, gl);
+        IncCursor cur(t, b, L, gl);
         for (int k = gl; k < L; k += kGroup) {
-          const Gathered e = gather(cur.v, cur.ba, true);
+          const Gathered e = gather(cur.v, cur.q, true);
           cur.advance(t, k);
           edge(e);
         }
       } else if (gl < L) {
         const int last = b + L - 1;
-        uint32_t v1 = static_cast<uint32_t>(t.inc[b + gl]);
-        uint32_t ba1 = slot_bit_address_of<BITS>(t, b + gl);
-        uint32_t v2 = static_cast<uint32_t>(t.inc[min(b + gl + kGroup, last)]);
-        uint32_t ba2 = slot_bit_address_of<BITS>(t, min(b + gl + kGroup, last));
+        int q1 = b + gl, q2 = min(b + gl + kGroup, last);
+        uint32_t v1 = static_cast<uint32_t>(t.inc[q1]);
+        uint32_t v2 = static_cast<uint32_t>(t.inc[q2]);
         for (int k = gl; k < L; k += 2 * kGroup) {
-          const Gathered e1 = gather(v1, ba1, true);
-          const Gathered e2 = gather(v2, ba2, k + kGroup < L);
+          const Gathered e1 = gather(v1, q1, true);
+          const Gathered e2 = gather(v2, q2, k + kGroup < L);
           asm volatile("" ::: "memory");  // keep the next entries' loads behind the gathers
-          const int q1 = min(b + k + 2 * kGroup, last), q2 = min(b + k + 3 * kGroup, last);
+          q1 = min(b + k + 2 * kGroup, last);
+          q2 = min(b + k + 3 * kGroup, last);
           v1 = static_cast<uint32_t>(t.inc[q1]);
-          ba1 = slot_bit_address_of<BITS>(t, q1);
           v2 = static_cast<uint32_t>(t.inc[q2]);
-          ba2 = slot_bit_address_of<BITS>(t, q2);
           edge(e1);
           edge(e2);
         }
@@ -1110,12 +1093,12 @@ void k_lj_inc(LjModel<S> m, TwoSided t)
         const int co = static_cast<int>(v & kIncAtom) < erows ? 1 : 0;
         return (in ? 0 : (a < erows ? 1 : 0)) + ((in || (v & kIncPaired)) ? co : 0);
       };
-      auto pair = [&](uint32_t v, uint32_t ba, int w, const Atom4<S> &xo) {
+      auto pair = [&](uint32_t v, int q, int w, const Atom4<S> &xo) {
         if (w == 0) return;
         S dx, dy, dz;
         const S r2 = geometry(xa, xo, dx, dy, dz);
         if (!(r2 > tiny && r2 < m.cutsq)) return;  // export_model.py:22
-        if (!slot_kept(t, ba, r2, dx, dy, dz, br, xo)) return;
+        if (!slot_kept(t, q, r2, dx, dy, dz, br, xo)) return;
         const S inv_r2 = m.sigsq / r2;
         const S inv_r6 = inv_r2 * inv_r2 * inv_r2;
         if (!(v >> 31)) en += m.edge_scale * (m.four_eps * (inv_r6 * inv_r6 - inv_r6));
@@ -1132,12 +1115,11 @@ void k_lj_inc(LjModel<S> m, TwoSided t)
         const int q1 = b + k, q2 = b + (two ? k + kGroup : k);
         const uint32_t v1 = static_cast<uint32_t>(t.inc[q1]);
         const uint32_t v2 = static_cast<uint32_t>(t.inc[q2]);
-        const uint32_t ba1 = slot_bit_address(t, q1), ba2 = slot_bit_address(t, q2);
         const int w1 = ends(v1), w2 = two ? ends(v2) : 0;
         const Atom4<S> x1 = m.atoms[w1 ? static_cast<int>(v1 & kIncAtom) : a];
         const Atom4<S> x2 = m.atoms[w2 ? static_cast<int>(v2 & kIncAtom) : a];
-        pair(v1, ba1, w1, x1);
-        pair(v2, ba2, w2, x2);
+        pair(v1, q1, w1, x1);
+        pair(v2, q2, w2, x2);
       }
     }
     en = group_sum(en);
