@@ -21,6 +21,9 @@
 // follows the atomic claims. Per-row sums never depend on it (each row's edges keep their order
 // inside its tile), so energies, forces and virials are bitwise reproducible.
 
+#include <cmath>
+#include <limits>
+
 #include "lk_eam_common.h"
 #include "lk_pack.h"
 #include "lk_tiles.h"
@@ -40,6 +43,7 @@ struct StepPack {
   int max_atoms;
   int max_edges;
   double cutsq;
+  float cutsq_lo, cutsq_hi;  // cutsq rounded down and up to float
   int pitch;
   uint32_t *bits;
   int *row_count;
@@ -52,6 +56,55 @@ struct StepPack {
   const int *ghost_off;
   const int *ghost_list;
 };
+
+// The pack's filter, rsq <= cutsq with rsq formed in float64 from the engine's x without
+// contraction (cpp:84-91), for float32 contracts, decided from float records where they decide
+// it: xa and xo are the row's and the neighbour's records (x rounded to float), sa = |xa|_1. With
+// u = 2^-24, l1 = |dx| + |dy| + |dz| of the float differences and s = l1 + |xa|_1 + |xo|_1, each
+// float difference is within u (|d_c| + |x_a,c| + |x_o,c|) / (1 - u) of the float64 one, so the
+// float r2 lies within u s (2 l1 + u s) / (1 - u)^2 + 3u r2 / (1 - 3u) of rsq; band, computed in
+// float, is at least twice that and at least 8u r2, which also covers comparing r2 +- band with
+// cutsq rounded down (up) to float. Only a slot inside the band reads the engine's float64
+// position of its neighbour and forms rsq exactly as the float64 filter does.
+__device__ __forceinline__ bool pack_keeps_f32(const StepPack &p, const Atom4<float> &xa,
+                                               float sa, const Atom4<float> &xo, int j,
+                                               double xi0, double xi1, double xi2)
+{
+  constexpr float u = 5.9604645e-8f;  // 2^-24
+  float dx, dy, dz, r2;
+  {
+#pragma clang fp contract(off)
+    dx = xo.x - xa.x;
+    dy = xo.y - xa.y;
+    dz = xo.z - xa.z;
+    r2 = dx * dx + dy * dy + dz * dz;
+  }
+  const float l1 = fabsf(dx) + fabsf(dy) + fabsf(dz);
+  const float s = l1 + sa + (fabsf(xo.x) + fabsf(xo.y) + fabsf(xo.z));
+  const float band = 2.0f * u * (s * (2.0f * l1 + u * s) + 4.0f * r2);
+  if (r2 + band <= p.cutsq_lo) return true;
+  if (r2 - band > p.cutsq_hi) return false;
+  double rsq;
+  {
+#pragma clang fp contract(off)
+    const double ex = xi0 - p.x[3L * j + 0], ey = xi1 - p.x[3L * j + 1];
+    const double ez = xi2 - p.x[3L * j + 2];
+    rsq = ex * ex + ey * ey + ez * ez;
+  }
+  return !(rsq > p.cutsq);
+}
+
+// cutsq and its float bounds for the kernel arguments.
+static void set_pack_cutoff(StepPack &p, double cutoff)
+{
+  p.cutsq = cutoff * cutoff;
+  p.cutsq_lo = static_cast<float>(p.cutsq);
+  p.cutsq_hi = p.cutsq_lo;
+  if (static_cast<double>(p.cutsq_lo) > p.cutsq)
+    p.cutsq_lo = std::nextafter(p.cutsq_lo, -std::numeric_limits<float>::infinity());
+  if (static_cast<double>(p.cutsq_hi) < p.cutsq)
+    p.cutsq_hi = std::nextafter(p.cutsq_hi, std::numeric_limits<float>::infinity());
+}
 
 constexpr int kStepW = 4, kStepTPB = 4;
 constexpr int kStepLds = 3584;     // table window entries: 56 KB (two blocks per CU)
@@ -103,11 +156,14 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
         i = -1;  // cpp:84: rows past max_atoms pack nothing
     }
     double xi0 = 0.0, xi1 = 0.0, xi2 = 0.0;
+    Atom4<float> xa{0.0f, 0.0f, 0.0f, 0.0f};  // float32 pack-only: the row's record
     if (i >= 0) {
       xi0 = p.x[3L * i + 0];
       xi1 = p.x[3L * i + 1];
       xi2 = p.x[3L * i + 2];
+      if constexpr (sizeof(S) == 4 && !EAM) xa = a.atoms[i];
     }
+    const float sa = fabsf(xa.x) + fabsf(xa.y) + fabsf(xa.z);
     const int nn_max = wave_max_int(nn);
     const int nwords = (nn_max + 31) >> 5;
     const bool lds_bits = nwords <= kStepMaxWords;
@@ -179,35 +235,21 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
     };
     // Pack-only kernels (no model in the loop, registers to spare) walk the slots jj0,
     // jj0 + step, ... < jj1 two at a time: both entries are loaded one pair ahead, then both
-    // neighbour positions gathered together, so a pair costs one memory round trip. Every load
-    // is unconditional (slots past the row read element 0 of the list and the record or position
-    // of atom 0, which exist whenever the loop runs, and are unused), so the compiler counts
-    // them exactly and waits for the gathers without waiting for the next pair's entries.
-    auto walk = [&](int jj0, int jj1, int step, auto &&kept) {
-      auto gather = [&](int jj, int entry, double &x0, double &x1, double &x2) {
+    // neighbour records gathered together, so a pair costs one memory round trip. Every load
+    // is unconditional (slots past the row read element 0 of the list and the record of atom 0,
+    // which exist whenever the loop runs, and are unused), so the compiler counts them exactly
+    // and waits for the gathers without waiting for the next pair's entries. The records are
+    // this step's (K0 ran before, or the engine's lk_pack_atoms call): float64 ones hold x
+    // exactly; float32 ones decide the filter through pack_keeps_f32 (one 16-byte gather per
+    // slot instead of three 8-byte ones from x).
+    auto walk32 = [&](int jj0, int jj1, int step, auto &&kept) {
+      auto gather = [&](int jj, int entry) -> Atom4<float> {
         const int j = entry & kNeighMask;
-        const long q = (jj < nn && j < p.max_atoms) ? j : 0;
-        if constexpr (sizeof(S) == 8) {
-          const double2 h = reinterpret_cast<const double2 *>(a.atoms)[2 * q];
-          x0 = h.x;
-          x1 = h.y;
-          x2 = reinterpret_cast<const double *>(a.atoms)[4 * q + 2];
-        } else {
-          x0 = p.x[3 * q + 0];
-          x1 = p.x[3 * q + 1];
-          x2 = p.x[3 * q + 2];
-        }
+        return reinterpret_cast<const Atom4<float> *>(a.atoms)[(jj < nn && j < p.max_atoms) ? j : 0];
       };
-      auto test = [&](int jj, int entry, double x0, double x1, double x2) {
+      auto test = [&](int jj, int entry, const Atom4<float> &xo) {
         const int j = entry & kNeighMask;
-        double rsq;
-        {
-#pragma clang fp contract(off)
-          const double dx = xi0 - x0, dy = xi1 - x1, dz = xi2 - x2;
-          rsq = dx * dx + dy * dy + dz * dz;
-        }
-        // PackNeighborFunctor keeps rsq <= cutsq (cpp:84-101)
-        if (jj < nn && j < p.max_atoms && !(rsq > p.cutsq)) {
+        if (jj < nn && j < p.max_atoms && pack_keeps_f32(p, xa, sa, xo, j, xi0, xi1, xi2)) {
           ++cnt;
           kept(jj);
         }
@@ -215,14 +257,52 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
       int ea = slot_entry(jj0), eb = slot_entry(jj0 + step);
       for (int jj = jj0; jj < jj1; jj += 2 * step) {
         const int jb = jj + step;
-        double a0, a1, a2, b0, b1, b2;
-        gather(jj, ea, a0, a1, a2);
-        gather(jb, eb, b0, b1, b2);
+        const Atom4<float> ra = gather(jj, ea), rb = gather(jb, eb);
         const int na = slot_entry(jj + 2 * step), nb = slot_entry(jj + 3 * step);
-        test(jj, ea, a0, a1, a2);
-        if (jb < jj1) test(jb, eb, b0, b1, b2);
+        test(jj, ea, ra);
+        if (jb < jj1) test(jb, eb, rb);
         ea = na;
         eb = nb;
+      }
+    };
+    auto walk = [&](int jj0, int jj1, int step, auto &&kept) {
+      if constexpr (sizeof(S) == 4) {
+        walk32(jj0, jj1, step, kept);
+      } else {
+        auto gather = [&](int jj, int entry, double &x0, double &x1, double &x2) {
+          const int j = entry & kNeighMask;
+          const long q = (jj < nn && j < p.max_atoms) ? j : 0;
+          const double2 h = reinterpret_cast<const double2 *>(a.atoms)[2 * q];
+          x0 = h.x;
+          x1 = h.y;
+          x2 = reinterpret_cast<const double *>(a.atoms)[4 * q + 2];
+        };
+        auto test = [&](int jj, int entry, double x0, double x1, double x2) {
+          const int j = entry & kNeighMask;
+          double rsq;
+          {
+#pragma clang fp contract(off)
+            const double dx = xi0 - x0, dy = xi1 - x1, dz = xi2 - x2;
+            rsq = dx * dx + dy * dy + dz * dz;
+          }
+          // PackNeighborFunctor keeps rsq <= cutsq (cpp:84-101)
+          if (jj < nn && j < p.max_atoms && !(rsq > p.cutsq)) {
+            ++cnt;
+            kept(jj);
+          }
+        };
+        int ea = slot_entry(jj0), eb = slot_entry(jj0 + step);
+        for (int jj = jj0; jj < jj1; jj += 2 * step) {
+          const int jb = jj + step;
+          double a0, a1, a2, b0, b1, b2;
+          gather(jj, ea, a0, a1, a2);
+          gather(jb, eb, b0, b1, b2);
+          const int na = slot_entry(jj + 2 * step), nb = slot_entry(jj + 3 * step);
+          test(jj, ea, a0, a1, a2);
+          if (jb < jj1) test(jb, eb, b0, b1, b2);
+          ea = na;
+          eb = nb;
+        }
       }
     };
     // Rows of fewer than W words (half lists) would leave waves idle under one word per wave:
@@ -438,7 +518,7 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   p.maxneighs = maxneighs;
   p.max_atoms = h.contract.max_atoms;
   p.max_edges = h.contract.max_edges;
-  p.cutsq = h.contract.cutoff * h.contract.cutoff;
+  set_pack_cutoff(p, h.contract.cutoff);
   p.pitch = h.contract.max_atoms;
   p.bits = h.d_bits;
   p.row_count = h.d_row_count;
@@ -529,7 +609,7 @@ static hipError_t pack_fused(Handle &h, hipStream_t s, const double *x, const in
   p.maxneighs = maxneighs;
   p.max_atoms = h.contract.max_atoms;
   p.max_edges = h.contract.max_edges;
-  p.cutsq = h.contract.cutoff * h.contract.cutoff;
+  set_pack_cutoff(p, h.contract.cutoff);
   p.pitch = h.contract.max_atoms;
   p.bits = h.d_bits;
   p.row_count = h.d_row_count;
