@@ -61,7 +61,7 @@ void free_all(Handle &h)
                   h.tl.keys,     h.tl.keys_sorted, h.tl.rows_in, h.tl.order,  h.tl.sort_tmp,
                   h.tl.atom,     h.tl.nn,       h.tl.uni,        h.tl.ucount,   h.tl.lid,
                   h.tl.box,      h.d_sort_keys, h.d_sort_vals,   h.d_sort_tmp,  h.d_sort_rows,
-                  h.d_sort_pre,  h.d_rowmark,   h.d_nonrow};
+                  h.d_sort_pre,  h.d_rowmark,   h.d_nonrow,      h.d_htab};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -427,6 +427,35 @@ int lk_set_eam(lk_handle *w, const lk_eam_tables *t)
     e = hipMemcpy(h.d_ltab, l.data(), nent * 16, hipMemcpyHostToDevice);
   }
   if (e != hipSuccess) return hip_fail(h, e, "hipMemcpy(ltab)");
+  if (S == 4) {
+    // the force sweep's Hermite rows: per node (s, d) of each density table, then (f, s, d) of
+    // each pair table; s = f(m + 1) - f(m) in float64, the difference the host's c2 and c3 used
+    const int W = 2 * n_el + 3 * npair;
+    std::vector<float> hr(static_cast<size_t>(t->nr) * W);
+    for (int node = 0; node < t->nr; ++node) {
+      auto c = [&](int tab, int k) { return r[(static_cast<size_t>(node) * n_rtab + tab) * 4 + k]; };
+      auto next_f = [&](int tab) {
+        return node + 1 < t->nr ? r[(static_cast<size_t>(node + 1) * n_rtab + tab) * 4] : c(tab, 0);
+      };
+      float *o = &hr[static_cast<size_t>(node) * W];
+      for (int z = 0; z < n_el; ++z) {
+        o[2 * z + 0] = static_cast<float>(next_f(z) - c(z, 0));
+        o[2 * z + 1] = static_cast<float>(c(z, 1));
+      }
+      for (int p = 0; p < npair; ++p) {
+        const int tab = n_el + p;
+        o[2 * n_el + 3 * p + 0] = static_cast<float>(c(tab, 0));
+        o[2 * n_el + 3 * p + 1] = static_cast<float>(next_f(tab) - c(tab, 0));
+        o[2 * n_el + 3 * p + 2] = static_cast<float>(c(tab, 1));
+      }
+    }
+    if ((e = hipMalloc(&h.d_htab, hr.size() * sizeof(float))) != hipSuccess)
+      return hip_fail(h, e, "hipMalloc(htab)");
+    if ((e = hipMemcpy(h.d_htab, hr.data(), hr.size() * sizeof(float), hipMemcpyHostToDevice)) !=
+        hipSuccess)
+      return hip_fail(h, e, "hipMemcpy(htab)");
+    h.htab_w = W;
+  }
   h.n_el = n_el;
   h.nrho = t->nrho;
   h.nr = t->nr;

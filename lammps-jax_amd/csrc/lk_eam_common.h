@@ -58,6 +58,8 @@ struct EamArgs {
   int max_edges;
   const S *rtab;                 // global rows [nr][n_rtab][4]
   const LdsEntry<S> *ltab;       // LDS source [nr][n_rtab]
+  const float *htab;             // float32: Hermite rows [nr][htab_w] (force sweep window)
+  int htab_w;
   int n_rtab;
   int n_el;
   int nr;
@@ -144,6 +146,24 @@ __device__ __forceinline__ Coef<S> rcoef_lds(const Window<S> &w, int m, int tab)
   }
 }
 
+// Any node, without a generic pointer: the lanes below the window load the row from the table in
+// memory (in a branch of their own), then every lane reads the window (a node below it reads the
+// window's first node, unused) and keeps the one that applies. rcoef's two reads in the two arms
+// of one branch compile to a single generic (flat) load through a selected address.
+template <typename S>
+__device__ __forceinline__ Coef<S> rcoef_split(const Window<S> &w, const EamArgs<S> &a, int m,
+                                               int tab)
+{
+  const bool in = m >= w.lo;
+  Coef<S> g{};
+  if (!in) {
+    const S *r = a.rtab + (static_cast<long>(m) * a.n_rtab + tab) * 4;
+    g = Coef<S>{r[0], r[1], r[2], r[3]};
+  }
+  const Coef<S> l = rcoef_lds(w, in ? m : w.lo, tab);
+  return Coef<S>{in ? l.c0 : g.c0, in ? l.c1 : g.c1, in ? l.c2 : g.c2, in ? l.c3 : g.c3};
+}
+
 // float64 intervals in the Hermite basis: the window holds (f, d) per node, so an interval is
 // f0, s = f1 - f0, d0, d1 and value(t) = f0 + s hs + d0 h0 + d1 h1, slope_t = s gs + d0 g0 + d1 g1
 // with basis functions of t alone, shared by every table an edge reads (the same cubic as
@@ -185,6 +205,76 @@ __device__ __forceinline__ double herm_value(const Herm &h, const HermBasis &b)
 __device__ __forceinline__ double herm_slope_t(const Herm &h, const HermBasis &b)
 {
   return h.s * b.gs + h.d0 * b.g0 + h.d1 * b.g1;
+}
+
+// float32 Hermite rows for the force sweep's LDS window: per node, (s, d) of each density table
+// and (f, s, d) of each pair table, with f the node value, d the slope in t and s = f(m+1) - f(m)
+// formed in float64 before narrowing, so an interval needs the next node's d alone. 13 floats
+// per node for two elements: a 64 KB window holds 1,260 nodes, where the narrowed cubic rows
+// (16 bytes per table) hold 819. The same cubic as the coefficient rows, evaluated in float32
+// from differently narrowed data: within a few float32 roundings of the reference's narrowed
+// coefficients, not bit for bit.
+struct HWindow {
+  const float *lds;
+  int W;   // floats per node
+  int lo;  // first node in LDS
+};
+
+__device__ __forceinline__ HWindow fill_hwindow(float *lds, int cap_floats, const float *htab,
+                                                int W, int nr)
+{
+  HWindow w;
+  w.lds = lds;
+  w.W = W;
+  const int cap_nodes = cap_floats / W;
+  w.lo = nr > cap_nodes ? nr - cap_nodes : 0;
+  const int n = (nr - w.lo) * W;
+  const float *src = htab + static_cast<long>(w.lo) * W;
+  for (int q = threadIdx.x; q < n; q += blockDim.x) lds[q] = src[q];
+  __syncthreads();
+  return w;
+}
+
+struct HermBasisF {
+  float hs, h0, h1, gs, g0, g1;
+};
+
+__device__ __forceinline__ HermBasisF herm_basis_f(float t)
+{
+  const float u = 1.0f - t, tt = t * t;
+  HermBasisF b;
+  b.hs = tt * (3.0f - 2.0f * t);
+  b.h0 = t * u * u;
+  b.h1 = -tt * u;
+  b.gs = 6.0f * t * u;
+  b.g0 = u * (1.0f - 3.0f * t);
+  b.g1 = t * (3.0f * t - 2.0f);
+  return b;
+}
+
+// Slope in t of density table z on the interval from node m (m and m + 1 in the window).
+__device__ __forceinline__ float hslope_density(const HWindow &w, int m, int z, const HermBasisF &b)
+{
+  const int q = (m - w.lo) * w.W + 2 * z;
+  return w.lds[q] * b.gs + w.lds[q + 1] * b.g0 + w.lds[q + w.W + 1] * b.g1;
+}
+
+// Value and slope in t of the pair table whose row starts at float `off` of a node.
+__device__ __forceinline__ void hpair(const HWindow &w, int m, int off, const HermBasisF &b,
+                                      float &value, float &slope)
+{
+  const int q = (m - w.lo) * w.W + off;
+  const float f0 = w.lds[q], s = w.lds[q + 1], d0 = w.lds[q + 2], d1 = w.lds[q + w.W + 2];
+  value = f0 + s * b.hs + d0 * b.h0 + d1 * b.h1;
+  slope = s * b.gs + d0 * b.g0 + d1 * b.g1;
+}
+
+// A coefficient row from the table in memory alone.
+template <typename S>
+__device__ __forceinline__ Coef<S> rcoef_global(const EamArgs<S> &a, int m, int tab)
+{
+  const S *r = a.rtab + (static_cast<long>(m) * a.n_rtab + tab) * 4;
+  return Coef<S>{r[0], r[1], r[2], r[3]};
 }
 
 template <typename S>
@@ -327,6 +417,8 @@ inline EamArgs<S> eam_args(Handle &h, int nlocal, double scale, double *f)
   a.max_edges = h.contract.max_edges;
   a.rtab = static_cast<const S *>(h.d_rtab);
   a.ltab = static_cast<const LdsEntry<S> *>(h.d_ltab);
+  a.htab = h.d_htab;
+  a.htab_w = h.htab_w;
   a.n_rtab = h.n_rtab;
   a.n_el = h.n_el;
   a.nr = h.nr;

@@ -59,6 +59,8 @@ struct Handle {
   void *d_rtab = nullptr;
   void *d_etab = nullptr;
   void *d_ltab = nullptr;  // LDS source: [nr][n_rtab] 16-byte entries, see lk_eam.hip
+  float *d_htab = nullptr;  // float32 contracts: Hermite rows of the force sweep, [nr][htab_w]
+  int htab_w = 0;
   int num_cus = 0;
   int n_el = 0, nrho = 0, nr = 0, n_rtab = 0;
   double drho = 0, dr = 0, eam_cutoff = 0;

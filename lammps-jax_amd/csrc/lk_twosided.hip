@@ -906,7 +906,13 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
 {
   __shared__ double vt[6][kRowAtoms];
   __shared__ double et[kRowAtoms];
-  const Window<S> win = fill_window<S>(lds, lds_entries, m, m.n_rtab);
+  // float32: the window holds Hermite rows (more nodes per byte); float64: (f, d) entries
+  Window<S> win{};
+  HWindow hw{};
+  if constexpr (sizeof(S) == 4)
+    hw = fill_hwindow(reinterpret_cast<float *>(lds), lds_entries * 4, m.htab, m.htab_w, m.nr);
+  else
+    win = fill_window<S>(lds, lds_entries, m, m.n_rtab);
   const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
   const int erows = energy_rows(t, HALF);
   for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
@@ -963,20 +969,56 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
         const bool inside = !(L2.t_raw > S(1));
         const int zs = in ? zo : za, zr = in ? za : zo;
         const S fps = in ? fpo : fpa;
-        const S rho_r_p = inside ? cslope_t(rcoef(win, m, L2.node, zr), L2.t) * m.inv_dr : S(0);
-        const Coef<S> cp = rcoef(win, m, L2.node, m.n_el + pair_row(za, zo));
-        const S phi = cvalue(cp, L2.t) * rinv;
+        // Slopes in t of the density tables zr and t3, and the pair table's value and slope:
+        // from the LDS window alone when every active lane's node lies in it (a wave-uniform
+        // branch), else from the tables in memory (or the window, lane by lane), whose loads'
+        // waits also wait for the entries already in flight for the next round.
+        const int tp = m.n_el + pair_row(za, zo);
+        const int t3 = HALF ? zs : za;
+        const bool three = HALF || paired;
+        S sr, z2, z2s, s3 = S(0);
+        if constexpr (sizeof(S) == 4) {
+          if (wave_ballot(L2.node < hw.lo) == 0) {
+            const HermBasisF hb = herm_basis_f(L2.t);
+            sr = hslope_density(hw, L2.node, zr, hb);
+            hpair(hw, L2.node, 2 * m.n_el + 3 * (tp - m.n_el), hb, z2, z2s);
+            if (three) s3 = hslope_density(hw, L2.node, t3, hb);
+          } else {
+            const Coef<S> cp = rcoef_global(m, L2.node, tp);
+            sr = cslope_t(rcoef_global(m, L2.node, zr), L2.t);
+            z2 = cvalue(cp, L2.t);
+            z2s = cslope_t(cp, L2.t);
+            if (three) s3 = cslope_t(rcoef_global(m, L2.node, t3), L2.t);
+          }
+        } else {
+          Coef<S> cr, cp, c3;
+          if (wave_ballot(L2.node < win.lo) == 0) {
+            cr = rcoef_lds(win, L2.node, zr);
+            cp = rcoef_lds(win, L2.node, tp);
+            if (three) c3 = rcoef_lds(win, L2.node, t3);
+          } else {
+            cr = rcoef_split(win, m, L2.node, zr);
+            cp = rcoef_split(win, m, L2.node, tp);
+            if (three) c3 = rcoef_split(win, m, L2.node, t3);
+          }
+          sr = cslope_t(cr, L2.t);
+          z2 = cvalue(cp, L2.t);
+          z2s = cslope_t(cp, L2.t);
+          if (three) s3 = cslope_t(c3, L2.t);
+        }
+        const S rho_r_p = inside ? sr * m.inv_dr : S(0);
+        const S phi = z2 * rinv;
         if (!in) ep += HALF ? phi : S(0.5) * phi;
-        const S z2p = inside ? cslope_t(cp, L2.t) * m.inv_dr : S(0);
+        const S z2p = inside ? z2s * m.inv_dr : S(0);
         const S phip = (z2p - phi) * rinv;
         S coef;
         if (HALF) {
           const S fpr = in ? fpa : fpo;
-          const S rho_s_p = inside ? cslope_t(rcoef(win, m, L2.node, zs), L2.t) * m.inv_dr : S(0);
+          const S rho_s_p = inside ? s3 * m.inv_dr : S(0);
           coef = (fps * rho_r_p + fpr * rho_s_p + phip) * rinv;
         } else if (paired) {
           // both directed edges: a -> o on a's counted row, o -> a on o's
-          const S rho_a_p = inside ? cslope_t(rcoef(win, m, L2.node, za), L2.t) * m.inv_dr : S(0);
+          const S rho_a_p = inside ? s3 * m.inv_dr : S(0);
           const S ga = ca ? fpa * rho_r_p + S(0.5) * phip : S(0);
           const S go = co ? fpo * rho_a_p + S(0.5) * phip : S(0);
           coef = (ga + go) * rinv;
