@@ -106,6 +106,14 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is not built; run `python lammps-jax_amd/build.py` (or "
             "__graft_entry__.build()) first. The hot path has no CPU fallback.")
+    try:
+        # torch ships its own libamdhip64 and libhsa-runtime64 under the same sonames as ROCm's:
+        # loaded first, they serve liblkhip.so too (one HIP runtime per process). Loading
+        # liblkhip.so first binds the process to ROCm's copies, and torch's device
+        # initialisation then reports no GPU.
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(str(LIB_PATH))
     vp, ip, dp = ctypes.c_void_p, ctypes.c_int, ctypes.c_double
     pp = ctypes.POINTER

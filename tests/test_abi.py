@@ -103,3 +103,28 @@ def test_contract_validation_without_device():
                           newton_pair=False)
     with pytest.raises(N.LammpsJaxError, match="n_hops > 1 require newton on"):
         pair.Handle(c)
+
+
+def test_one_hip_runtime_per_process():
+    """torch ships libamdhip64 and libhsa-runtime64 under ROCm's sonames. Loading the library in
+    a fresh process (nothing imported before it) maps one copy of each, torch's, so torch's
+    device initialisation and the library share one HIP runtime."""
+    import sys
+
+    code = (
+        "import json, os, sys\n"
+        f"sys.path.insert(0, {str(REPO / 'lammps-jax_amd')!r})\n"
+        "from lammps_jax_amd import _native\n"
+        "_native.load()\n"
+        "maps = open(f'/proc/{os.getpid()}/maps').read().splitlines()\n"
+        "for name in ('libamdhip64', 'libhsa-runtime64'):\n"
+        "    print(json.dumps([name, sorted({l.split()[-1] for l in maps if name in l})]))\n"
+    )
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    import json
+
+    for line in out.stdout.splitlines():
+        name, paths = json.loads(line)
+        assert len(paths) == 1, (name, paths)
+        assert "torch" in paths[0], (name, paths)
