@@ -773,7 +773,11 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
         const S rr = r2 * rinv;
         const Locator<S> L2 = locate_mul(rr, m.inv_dr, m.nr);
         const int zo = clamp_species(static_cast<int>(xo.w), m.n_el);
-        rho += cvalue(rcoef(win, m, L2.node, zo), L2.t);
+        // the window alone when every active lane's node lies in it (a wave-uniform branch; the
+        // density window usually holds the whole table), so the lookup waits on LDS only
+        const Coef<S> c = wave_ballot(L2.node < win.lo) == 0 ? rcoef_lds(win, L2.node, zo)
+                                                             : rcoef_split(win, m, L2.node, zo);
+        rho += cvalue(c, L2.t);
         if (PAIR && !in) {
           const S phi = cvalue(rcoef(win, m, L2.node, m.n_el + pair_row(za, zo)), L2.t) * rinv;
           ep += HALF ? phi : S(0.5) * phi;  // half: the sender carries both halves
