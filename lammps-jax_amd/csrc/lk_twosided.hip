@@ -639,10 +639,11 @@ __device__ __forceinline__ bool word_has(uint32_t word, uint32_t ba)
 // 3u r2 / (1 - 3u) of sum d^2 (float64 rounding adds far less). band = 2u (s (2 l1 + u s) + 4 r2),
 // computed in float, exceeds twice that bound and at least 8u r2, which covers the rounding of
 // r2 +- band against cutsq rounded down (up) to float. Only an r2 inside the band loads the
-// bit address of entry q's slot and then its validity word; no other entry reads either. Per row, BandRow bounds the band of every entry the model's cutoff lets
-// through (l1 <= sqrt(3) rc_model, and the neighbour's 1-norm <= the row's + l1), so most entries
-// are decided by one comparison with a row threshold. Lists built from packed edges (no bit
-// addresses) hold kept slots only.
+// bit address of entry q's slot and then its validity word; no other entry reads either. Per
+// row, BandRow bounds the band of every entry the model's cutoff lets through (l1 <= sqrt(3)
+// rc_model, and the neighbour's 1-norm <= the row's + l1), so most entries are decided by one
+// comparison with a row threshold. Lists built from packed edges (no bit addresses) hold kept
+// slots only.
 template <typename S>
 struct BandRow {
   S sa;       // the row atom's 1-norm
