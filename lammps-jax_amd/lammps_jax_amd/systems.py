@@ -65,22 +65,24 @@ def _taper(r, rc, h=TAPER_WIDTH):
 
 
 def synthetic_alloy(seed: int = 2024, nr: int = 2000, nrho: int = 2000, cutoff: float = 6.0,
-                    rho_max: float = 40.0, spread: float = 0.2) -> dict:
-    """Per-species constants drawn uniformly within +-spread of the bases; tables sampled on
-    uniform grids with dr = cutoff / (nr - 1), drho = rho_max / (nrho - 1). The cross pair is
-    the mean of the two like-pair functions. Returns the setfl fields (for format_setfl)."""
+                    rho_max: float = 40.0, spread: float = 0.2, base: dict | None = None) -> dict:
+    """Per-species constants drawn uniformly within +-spread of the bases (ALLOY_BASE unless
+    `base` names others, in file order); tables sampled on uniform grids with
+    dr = cutoff / (nr - 1), drho = rho_max / (nrho - 1). A cross pair is the mean of the two
+    like-pair functions. Returns the setfl fields (for format_setfl)."""
     rng = np.random.default_rng(seed)
+    bases = ALLOY_BASE if base is None else base
     consts = {}
-    for el, base in ALLOY_BASE.items():
+    for el, base_c in bases.items():
         c = {}
-        for k, v in base.items():
+        for k, v in base_c.items():
             c[k] = v if k == "mass" else v * (1.0 + spread * (2.0 * rng.random() - 1.0))
         consts[el] = c
     dr = cutoff / (nr - 1)
     drho = rho_max / (nrho - 1)
     r = np.arange(nr) * dr
     rho = np.arange(nrho) * drho
-    elements = list(ALLOY_BASE)
+    elements = list(bases)
     F, dens, phis = [], [], {}
     for el in elements:
         c = consts[el]
@@ -88,7 +90,7 @@ def synthetic_alloy(seed: int = 2024, nr: int = 2000, nrho: int = 2000, cutoff: 
         dens.append(c["fe"] * np.exp(-c["beta"] * (r / c["re"] - 1.0)) * _taper(r, cutoff))
         phis[el] = c["D"] * (np.exp(-2.0 * c["alpha"] * (r - c["r0"]))
                              - 2.0 * np.exp(-c["alpha"] * (r - c["r0"]))) * _taper(r, cutoff)
-    # r*phi for pairs (i, j <= i) in file order: (Cu,Cu), (Zr,Cu), (Zr,Zr)
+    # r*phi for pairs (i, j <= i) in file order: (Cu,Cu), (Zr,Cu), (Zr,Zr) for the default pair
     z2r = []
     for i, ei in enumerate(elements):
         for j in range(i + 1):
