@@ -29,10 +29,19 @@
 #include <limits>
 
 #include <hipcub/hipcub.hpp>
+#include <rocprim/device/device_radix_sort.hpp>
 
 #include "lk_eam_common.h"
 
 namespace lk {
+
+// The in-entry sort of list-built lists: onesweep passes of 11-bit digits, so atom keys of up to
+// 22 bits (4 M atoms) take two passes over the pairs instead of three 8-bit ones.
+using IncSortConfig = rocprim::radix_sort_config<
+    rocprim::default_config, rocprim::default_config,
+    rocprim::radix_sort_onesweep_config<rocprim::kernel_config<1024, 16>,
+                                        rocprim::kernel_config<1024, 16>, 11,
+                                        rocprim::block_radix_rank_algorithm::match>>;
 
 constexpr int kScanThreads = 1024;
 constexpr int kScanItems = 4;
@@ -1290,10 +1299,11 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall, 
       e = hipcub::DeviceScan::ExclusiveSum(nullptr, b_scan_atoms, static_cast<int *>(nullptr),
                                            static_cast<int *>(nullptr), atoms + 2, s);
     if (e == hipSuccess)
-      e = hipcub::DeviceRadixSort::SortPairs(nullptr, b_sort, static_cast<uint32_t *>(nullptr),
-                                             static_cast<uint32_t *>(nullptr),
-                                             static_cast<uint32_t *>(nullptr),
-                                             static_cast<uint32_t *>(nullptr), cap, 0, key_bits, s);
+      e = rocprim::radix_sort_pairs<IncSortConfig>(nullptr, b_sort, static_cast<uint32_t *>(nullptr),
+                                                   static_cast<uint32_t *>(nullptr),
+                                                   static_cast<uint32_t *>(nullptr),
+                                                   static_cast<uint32_t *>(nullptr), cap, 0u,
+                                                   static_cast<unsigned>(key_bits), s);
     if (e != hipSuccess) return e;
     const size_t tmp = std::max(b_sort, std::max(b_scan_rows, b_scan_atoms));
     if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
@@ -1358,8 +1368,10 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall, 
   if (kept > 0) {
     StageTimer timer(h, s, "inc_sort");
     size_t bytes = h.sort_tmp_bytes;
-    if ((e = hipcub::DeviceRadixSort::SortPairs(h.d_sort_tmp, bytes, keys_in, keys_out, vals_in,
-                                                vals_out, kept, 0, key_bits, s)) != hipSuccess)
+    if ((e = rocprim::radix_sort_pairs<IncSortConfig>(h.d_sort_tmp, bytes, keys_in, keys_out,
+                                                      vals_in, vals_out, kept, 0u,
+                                                      static_cast<unsigned>(key_bits), s)) !=
+        hipSuccess)
       return e;
   }
   {
