@@ -461,7 +461,6 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
     for (int wd = wave; wd < nwords; wd += W) {
       uint32_t word = 0;
       if (staged) {
-        // the word's eight four-slot groups: all eight id loads go out first
         // the word's eight four-slot groups; the next group's ids load while one is walked
         const long gbase = static_cast<long>(tile) * t.groups + wd * 8;
         const int gcount = min(8, t.groups - wd * 8);
