@@ -61,10 +61,11 @@ void free_all(Handle &h)
                   h.tl.keys,     h.tl.keys_sorted, h.tl.rows_in, h.tl.order,  h.tl.sort_tmp,
                   h.tl.atom,     h.tl.nn,       h.tl.uni,        h.tl.ucount,   h.tl.lid,
                   h.tl.box,      h.d_sort_keys, h.d_sort_vals,   h.d_sort_tmp,  h.d_sort_rows,
-                  h.d_sort_pre,  h.d_rowmark,   h.d_nonrow,      h.d_htab};
+                  h.d_sort_pre,  h.d_rowmark,   h.d_nonrow,      h.d_htab,      h.tl.ustat};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
+  if (h.tl.h_ustat) (void)hipHostFree(h.tl.h_ustat);
   for (hipEvent_t ev : h.event_pool) (void)hipEventDestroy(ev);
   h.event_pool.clear();
 }

@@ -203,6 +203,10 @@ struct Handle {
     const int *order_ilist = nullptr;  // the ilist and row count the row order was sorted for
     int order_rows = -1;
     int order_reuses = 0;              // list rebuilds since that sort that kept its order
+    unsigned long long *ustat = nullptr;    // device: the summed union sizes of the last build
+    unsigned long long *h_ustat = nullptr;  // pinned copy, read at the next build
+    unsigned long long ustat_at_sort = 0;   // the sum of the build that last sorted the rows
+    bool built = false, last_sorted = false;
   } tl;
 
   size_t scalar_bytes() const { return contract.precision == LK_FLOAT64 ? 8 : 4; }

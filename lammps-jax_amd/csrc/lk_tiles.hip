@@ -202,9 +202,11 @@ __global__ __launch_bounds__(256) void k_tile_rows(const int *__restrict__ order
                                                    const int *__restrict__ ilist,
                                                    const int *__restrict__ numneigh, int rows,
                                                    int positions, int max_atoms, int maxneighs,
-                                                   int *__restrict__ atom, int *__restrict__ nn)
+                                                   int *__restrict__ atom, int *__restrict__ nn,
+                                                   unsigned long long *__restrict__ ustat)
 {
   const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p == 0) *ustat = 0ull;  // for the union kernel that follows
   if (p >= positions) return;
   int a = -1, n = 0;
   if (p < rows) {
@@ -230,6 +232,7 @@ struct TileBuild {
   int *uni;
   int *ucount;
   uint64_t *lid;
+  unsigned long long *ustat;  // sum of the union sizes (zeroed by k_tile_rows)
 };
 
 // One tile per block: the union of the atoms its entries name (hash set in LDS, then a bitonic
@@ -314,6 +317,7 @@ __global__ __launch_bounds__(1024) void k_tile_union(TileBuild b)
   }
   __syncthreads();
   const int U = count;
+  if (tid == 0) atomicAdd(b.ustat, static_cast<unsigned long long>(U));
   if (U > kTileUnion) {  // block-uniform
     if (tid == 0) b.ucount[tile] = -1;
     return;
@@ -651,8 +655,10 @@ hipError_t ensure_tile_list(Handle &h, int rows, int maxneighs)
                   static_cast<void *>(T.rows_in), static_cast<void *>(T.order), T.sort_tmp,
                   static_cast<void *>(T.atom), static_cast<void *>(T.nn),
                   static_cast<void *>(T.uni), static_cast<void *>(T.ucount),
-                  static_cast<void *>(T.lid), static_cast<void *>(T.box)})
+                  static_cast<void *>(T.lid), static_cast<void *>(T.box),
+                  static_cast<void *>(T.ustat)})
     if (q) (void)hipFree(q);
+  if (T.h_ustat) (void)hipHostFree(T.h_ustat);
   T = Handle::TileList{};
   const int rcap = rows > 0 ? rows : 1;
   const int tcap = tiles > 0 ? tiles : 1;
@@ -674,6 +680,11 @@ hipError_t ensure_tile_list(Handle &h, int rows, int maxneighs)
   if ((e = hipMalloc(&T.ucount, tcap * sizeof(int))) != hipSuccess) return e;
   if ((e = hipMalloc(&T.lid, pos * gcap * sizeof(uint64_t))) != hipSuccess) return e;
   if ((e = hipMalloc(&T.box, 6 * sizeof(unsigned long long))) != hipSuccess) return e;
+  if ((e = hipMalloc(&T.ustat, sizeof(unsigned long long))) != hipSuccess) return e;
+  if ((e = hipHostMalloc(reinterpret_cast<void **>(&T.h_ustat), sizeof(unsigned long long))) !=
+      hipSuccess)
+    return e;
+  *T.h_ustat = 0;
   T.rows_cap = rcap;
   T.tiles_cap = tcap;
   T.groups = gcap;
@@ -683,7 +694,12 @@ hipError_t ensure_tile_list(Handle &h, int rows, int maxneighs)
 // A list rebuild of the same rows (the engine's ilist and row count) keeps the previous build's
 // row order for up to this many rebuilds before sorting the rows again: atoms move little between
 // rebuilds, so the order stays spatially coherent, and any order of the rows gives the same sums
-// per row (only the 64-row energy and virial partials group differently).
+// per row (only the 64-row energy and virial partials group differently). The rows are sorted
+// again sooner when the tiles' unions have grown by a quarter since the sort (the engine may have
+// renumbered its atoms, as LAMMPS' periodic atom sort does): the union kernel sums the union
+// sizes of each build, and the next build reads that sum from pinned memory (complete by then,
+// the step results between them having waited for the stream; a sum still in flight only delays
+// the sort).
 constexpr int kTileOrderReuse = 8;
 
 hipError_t build_tile_list(Handle &h, hipStream_t s, const double *x, const int *ilist,
@@ -694,7 +710,18 @@ hipError_t build_tile_list(Handle &h, hipStream_t s, const double *x, const int 
   const int tiles = (rows + kTileRows - 1) / kTileRows;
   const int positions = tiles * kTileRows;
   StageTimer timer(h, s, "tile_list");
-  if (T.order_ilist == ilist && T.order_rows == rows && T.order_reuses < kTileOrderReuse) {
+  bool grown = false;
+  if (T.built) {
+    const unsigned long long last = __atomic_load_n(T.h_ustat, __ATOMIC_ACQUIRE);
+    if (T.last_sorted)
+      T.ustat_at_sort = last;
+    else
+      grown = last > T.ustat_at_sort + T.ustat_at_sort / 4;
+  }
+  T.built = true;
+  T.last_sorted = !(T.order_ilist == ilist && T.order_rows == rows &&
+                    T.order_reuses < kTileOrderReuse && !grown);
+  if (!T.last_sorted) {
     ++T.order_reuses;
   } else {
     hipLaunchKernelGGL(k_tile_bbox_init, dim3(1), dim3(64), 0, s, T.box);
@@ -714,7 +741,8 @@ hipError_t build_tile_list(Handle &h, hipStream_t s, const double *x, const int 
     T.order_reuses = 0;
   }
   hipLaunchKernelGGL(k_tile_rows, dim3((positions + 255) / 256), dim3(256), 0, s, T.order, ilist,
-                     numneigh, rows, positions, h.contract.max_atoms, maxneighs, T.atom, T.nn);
+                     numneigh, rows, positions, h.contract.max_atoms, maxneighs, T.atom, T.nn,
+                     T.ustat);
   TileBuild b;
   b.atom = T.atom;
   b.nn = T.nn;
@@ -727,8 +755,12 @@ hipError_t build_tile_list(Handle &h, hipStream_t s, const double *x, const int 
   b.ucount = T.ucount;
   b.lid = T.lid;
   b.tiles = tiles;
+  b.ustat = T.ustat;
   hipLaunchKernelGGL(k_tile_union, dim3(tile_grid(tiles)), dim3(1024), 0, s, b);
-  return hipGetLastError();
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(T.h_ustat, T.ustat, sizeof(unsigned long long), hipMemcpyDeviceToHost, s);
+  return e;
 }
 
 }  // namespace

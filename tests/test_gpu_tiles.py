@@ -182,6 +182,38 @@ def test_row_order_across_rebuilds_of_the_same_rows(gpu):
         _check(wl, sysm, pj, pj.compute(), f"rebuild {k}")
 
 
+def test_renumbered_atoms_under_kept_row_order(gpu):
+    """The engine renumbers its atoms (as LAMMPS' periodic atom sort does) and rebuilds the list
+    into the same arrays with the same row count: the kept row order then names scattered atoms
+    (tiles past the union cap walk the list from memory) until the union sizes' growth sorts
+    the rows again at a later rebuild. Every step matches the oracle over its list."""
+    wl = systems.make_workload("eam_alloy_131k", cells=(6, 6, 6), seed=9)
+    sysm = wl.system()
+    sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    pj = PairJax(sysm, ("eam", wl.tables), precision=8, accumulation="onesided")
+    _check(wl, sysm, pj, pj.compute(), "first build")
+    nl = sysm.nlocal
+    perm = np.random.default_rng(6).permutation(nl)
+    sysm2 = harness.System(sysm.x[:nl][perm], sysm.type[:nl][perm], wl.box, wl.cutghost)
+    lst2 = sysm2.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    assert sysm2.nall == sysm.nall and lst2["neighbors"].shape == tuple(pj.neighbors.shape)
+    torch = pj.torch
+    ptrs = (pj.ilist.data_ptr(), pj.neighbors.data_ptr())
+    pj.system = sysm2
+    pj.h.set_ghost_map(sysm2.nlocal, sysm2.ghost_owner)
+    pj.x.copy_(torch.from_numpy(np.ascontiguousarray(sysm2.x)).to(pj.device))
+    pj.type.copy_(torch.from_numpy(np.ascontiguousarray(sysm2.type)).to(pj.device))
+    pj.ilist[: len(lst2["ilist"])].copy_(torch.from_numpy(lst2["ilist"]).to(pj.device))
+    pj.numneigh.copy_(torch.from_numpy(lst2["numneigh"]).to(pj.device))
+    pj.neighbors.copy_(torch.from_numpy(lst2["neighbors"]).to(pj.device))
+    assert (pj.ilist.data_ptr(), pj.neighbors.data_ptr()) == ptrs
+    for k in range(3):  # a rebuild that keeps the order, then ones after the growth shows
+        pj.list_epoch += 1
+        pj.h.set_list_epoch(pj.list_epoch)
+        print(f"renumbered rebuild {k}", flush=True)
+        _check(wl, sysm2, pj, pj.compute(), f"renumbered rebuild {k}")
+
+
 def test_tile_steps_between_split_steps(gpu):
     """The fused tile step writes the atom records itself and starts from the pack state the
     previous fused step's last block left. Fused and split steps alternate here, with edge
