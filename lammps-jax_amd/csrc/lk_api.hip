@@ -832,13 +832,14 @@ int lk_pack_compute(lk_handle *w, void *stream, const double *x, const int *type
       h.list_duplicate = 0;
       if (int rc = ensure_incidence(h, 2L * rows * mnb)) return rc;
       hipStream_t s = as_stream(stream);
-      h.pack_ready = false;
       lk::FusedPack fp;
       hipError_t e = lk::launch_pack_fused(h, s, x, type, nall, ilist, numneigh, neighbors,
                                            nb_stride, static_cast<int>(rows), mnb, nlocal, &fp);
       if (e == hipSuccess)
         e = lk::launch_two_sided(h, s, nlocal, nghost, flags, scale, f, x, true, fp);
       if (e != hipSuccess) return hip_fail(h, e, "fused two-sided step");
+      // the sweeps' last block resets the pack state for the next fused pack
+      h.pack_ready = true;
       mark_mirrored(h);
       return LK_OK;
     }

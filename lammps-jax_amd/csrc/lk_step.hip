@@ -55,6 +55,12 @@ struct StepPack {
   unsigned char *mask;
   const int *ghost_off;
   const int *ghost_list;
+  // float64 pack-only kernels of the fused two-sided step: the atom records of [0, records)
+  // (PackAtomsFunctor), written here instead of by a launch of their own, or null; the filter
+  // then reads x, since other blocks' records may not be written yet
+  Atom4<double> *atoms_out;
+  int *species_out;
+  int records;
 };
 
 // The pack's filter, rsq <= cutsq with rsq formed in float64 from the engine's x without
@@ -140,6 +146,21 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
 
   Window<S> win{};
   if constexpr (EAM) win = fill_window<S>(lds, kStepLds, a, a.n_el);
+  if constexpr (!EAM && sizeof(S) == 8) {
+    // the atom records for the sweeps (cpp:35-52: x as is, species = type - 1)
+    if (p.atoms_out)
+      for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < p.records;
+           i += gridDim.x * blockDim.x) {
+        const int sp = p.type[i] - 1;
+        Atom4<double> r;
+        r.x = p.x[3L * i + 0];
+        r.y = p.x[3L * i + 1];
+        r.z = p.x[3L * i + 2];
+        r.w = static_cast<double>(sp);
+        p.atoms_out[i] = r;
+        p.species_out[i] = sp;
+      }
+  }
   const int sub = wave_in_block() / W;
   const int wave = wave_in_block() % W;
   const int lane = threadIdx.x & (kWave - 1);
@@ -272,10 +293,16 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
         auto gather = [&](int jj, int entry, double &x0, double &x1, double &x2) {
           const int j = entry & kNeighMask;
           const long q = (jj < nn && j < p.max_atoms) ? j : 0;
-          const double2 h = reinterpret_cast<const double2 *>(a.atoms)[2 * q];
-          x0 = h.x;
-          x1 = h.y;
-          x2 = reinterpret_cast<const double *>(a.atoms)[4 * q + 2];
+          if (p.atoms_out) {  // this launch writes the records
+            x0 = p.x[3 * q + 0];
+            x1 = p.x[3 * q + 1];
+            x2 = p.x[3 * q + 2];
+          } else {
+            const double2 h = reinterpret_cast<const double2 *>(a.atoms)[2 * q];
+            x0 = h.x;
+            x1 = h.y;
+            x2 = reinterpret_cast<const double *>(a.atoms)[4 * q + 2];
+          }
         };
         auto test = [&](int jj, int entry, double x0, double x1, double x2) {
           const int j = entry & kNeighMask;
@@ -530,6 +557,9 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   p.mask = h.d_mask;
   p.ghost_off = nghost > 0 ? h.d_ghost_off : nullptr;
   p.ghost_list = h.d_ghost_list;
+  p.atoms_out = nullptr;
+  p.species_out = nullptr;
+  p.records = 0;
   const int ntiles = (num_rows + kWave - 1) / kWave;
   const int ngroups = ntiles > 0 ? (ntiles + kStepTPB - 1) / kStepTPB : 1;
   // float64 EAM over an engine list: the pack and density over tile lists (lk_tiles.hip)
@@ -623,8 +653,20 @@ static hipError_t pack_fused(Handle &h, hipStream_t s, const double *x, const in
   p.ghost_list = nullptr;
   const int ntiles = (num_rows + kWave - 1) / kWave;
   const int ngroups = ntiles > 0 ? (ntiles + kStepTPB - 1) / kStepTPB : 1;
-  if (hipError_t e0 = launch_pack_atoms(h, s, x, type, nall, h.d_pack_state); e0 != hipSuccess)
+  // float64: the pack kernel writes the atom records itself, and the previous fused step's last
+  // block left the pack state as the record launch would (h.pack_ready), else one block resets
+  // it. float32 filters from the records (pack_keeps_f32), so they come first.
+  const bool ready = h.pack_ready;
+  h.pack_ready = false;
+  if (sizeof(S) == 8 && ntiles > 0) {
+    if (!ready) hipLaunchKernelGGL(k_start_pack, dim3(1), dim3(64), 0, s, h.d_pack_state);
+    p.atoms_out = static_cast<Atom4<double> *>(h.d_atoms);
+    p.species_out = h.d_species;
+    p.records = nall < h.contract.max_atoms ? nall : h.contract.max_atoms;
+  } else if (hipError_t e0 = launch_pack_atoms(h, s, x, type, nall, h.d_pack_state);
+             e0 != hipSuccess) {
     return e0;
+  }
   if (ntiles > 0) {
     StageTimer timer(h, s, "step_pack");
     const int grid = step_pack_grid<false>(ngroups, h.num_cus);
