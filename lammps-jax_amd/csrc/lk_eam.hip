@@ -27,7 +27,9 @@
 namespace lk {
 
 constexpr int kDensW = 4, kDensTPB = 4, kDensLds = 4096;     // 64 KB table window
-constexpr int kForceW = 4, kForceTPB = 4, kForceLds = 7680;  // 120 KB table window
+// two waves per 64-row tile, eight tiles per block (C3 force rows: 4 x 4 took 77.6 us, 2 x 8
+// 73 us, 8 x 2 91.5 us, 1 x 16 113.5 us)
+constexpr int kForceW = 2, kForceTPB = 8, kForceLds = 7680;  // 120 KB table window
 
 // Density sweep (one-sided): rho_i over the row's own edges, then F(rho_i), F'(rho_i). Owned rows
 // add F(rho_i) to the tile's energy partial.
