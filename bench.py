@@ -27,6 +27,10 @@ sys.path.insert(0, str(REPO / "lammps-jax_amd"))
 
 METRIC = "EAM fp64 atom-steps/s @131k atoms; achieved HBM GB/s (% of peak)"
 HBM_PEAK_GBS = 8000.0
+MEDIAN_STEPS = 50  # per-step wall times for the median: at least this many steps
+REBUILD_SOURCE = ("the 131,072-atom NVE run at 600 K (dt 2 fs, skin 1 A) rebuilds its list 8 "
+                  "times in 100 steps; the synthetic lattice (a = 3.8 A, about -4.8e5 bar) heats "
+                  "from 600 K to about 1,950 K over those steps, so the cadence is the fast end")
 
 
 def stage_bytes(stage: str, *, R: int, A: int, N: int, E: int, entries: int, S: int,
@@ -247,7 +251,8 @@ def lean_step(pj, eflag: bool = True, vflag: bool = True, rebuild_every: int = 0
     its once-per-list work (tile lists, incidence lists, matrix copy) inside that step. The list
     itself is the same one (the engine's rebuild is not the pair style's time).
 
-    Returns run(n), which makes n steps and returns the last step's lk_step_info."""
+    Returns run(n, step_s=None), which makes n steps and returns the last step's lk_step_info;
+    a float64 array of n in step_s receives each step's wall time in seconds."""
     import ctypes
 
     from lammps_jax_amd import _native as N
@@ -268,10 +273,11 @@ def lean_step(pj, eflag: bool = True, vflag: bool = True, rebuild_every: int = 0
     epoch, calls, rebuilds = ctypes.c_long(pj.list_epoch), ctypes.c_long(0), ctypes.c_int(0)
     stream = ctypes.c_void_p(pj.stream())
 
-    def run(n: int):
+    def run(n: int, step_s=None):
+        times = None if step_s is None else step_s.ctypes.data
         rc = hl.lkh_run_steps(ctypes.byref(fns), h, stream, ctypes.byref(args), int(n),
                               int(rebuild_every), ctypes.byref(epoch), ctypes.byref(calls),
-                              ctypes.byref(rebuilds), ctypes.byref(info))
+                              ctypes.byref(rebuilds), ctypes.byref(info), times)
         pj.list_epoch = epoch.value
         run.rebuilds = rebuilds.value
         if rc == N.LK_ERR_CAPACITY and info.edge_overflow:
@@ -355,6 +361,15 @@ def main() -> int:
     rebuilds_timed = step.rebuilds
     print(f"[bench] timed {args.steps} steps ({rebuilds_timed} list-rebuild steps) in "
           f"{elapsed:.4f}s", file=sys.stderr, flush=True)
+    # per-step wall times over at least MEDIAN_STEPS steps at the same rebuild cadence (a pass of
+    # its own, after the timed loop whose count the caller sets)
+    import numpy as np
+
+    n_med = max(args.steps, MEDIAN_STEPS)
+    per_step = np.zeros(n_med)
+    step_m = lean_step(pj, rebuild_every=args.rebuild_every)
+    step_m(n_med, per_step)
+    torch.cuda.synchronize(dev)
     # the same steps through the Python host mirror (PairJax.compute: f cleared by torch each
     # step, result wrapped in Python objects), reported beside the C-caller rate
     torch.cuda.synchronize(dev)
@@ -445,6 +460,11 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms_per_step,
+        "ms_per_step_median": round(1e3 * float(np.median(per_step)), 5),
+        "per_step_sample": {"steps": n_med, "mean_ms": round(1e3 * float(per_step.mean()), 5),
+                            "p10_ms": round(1e3 * float(np.percentile(per_step, 10)), 5),
+                            "p90_ms": round(1e3 * float(np.percentile(per_step, 90)), 5),
+                            "max_ms": round(1e3 * float(per_step.max()), 5)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -464,6 +484,7 @@ def main() -> int:
                     "(lk_pack_compute + lk_step_result; f cleared by the engine, not timed)",
             "list_rebuild_every": args.rebuild_every,
             "list_rebuild_steps_timed": rebuilds_timed,
+            "list_rebuild_source": REBUILD_SOURCE,
         },
         "roofline": {
             "bound": "hbm",

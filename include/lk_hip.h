@@ -352,6 +352,16 @@ int lk_model_buffers(lk_handle *h, void **rho, void **fp);
 int lk_edge_forces(lk_handle *h, void **edge_forces);
 
 /*
+ * Tile lists of the fused one-sided float64 EAM step (built once per list, lk_set_list_epoch):
+ * the number of 128-row tiles of the last build and the device array of their union sizes,
+ * [tiles] int32, the distinct atoms each tile's list entries name, or -1 for a tile whose union
+ * exceeded the staging cap (its rows gather neighbours from memory). ntiles is 0 before the first
+ * build. Diagnostic only (tests, profiling): the LAMMPS step path does not call it; no reference
+ * counterpart.
+ */
+int lk_tile_lists(lk_handle *h, int *ntiles, int **union_count);
+
+/*
  * Neighbour-matrix contracts: the device matrix [max_neighbors][rows] and the per-row counts
  * [rows] the model reads (the reference's d_neighbors / d_num_neighbors views, cpp:369-376).
  * LK_ERR_STATE for sparse-edge contracts.

@@ -14,6 +14,7 @@
 #include "lk_device.h"
 #include "lk_internal.h"
 #include "lk_pack.h"
+#include "lk_tiles.h"
 
 struct lk_handle {
   lk::Handle h;
@@ -907,6 +908,10 @@ int lk_step_result(lk_handle *w, void *stream, lk_step_info *out)
       e = hipMemcpyAsync(h.h_result, h.d_result, sizeof(lk::StepResult), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return hip_fail(h, e, "step result");
+    // With the stream drained the pinned copy holds the device's sequence number: count on from
+    // it, so a pass that failed after enqueuing its last block (and so was never counted) cannot
+    // leave every later poll one behind, spinning out its budget.
+    h.mirror_expected = h.h_result->seq;
   }
   for (const auto &p : h.pending) {
     float ms = 0.0f;
@@ -1000,6 +1005,16 @@ int lk_model_buffers(lk_handle *w, void **rho, void **fp)
   if (!w) return LK_ERR_ARGUMENT;
   if (rho) *rho = w->h.d_rho;
   if (fp) *fp = w->h.d_fp;
+  return LK_OK;
+}
+
+int lk_tile_lists(lk_handle *w, int *ntiles, int **union_count)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  const Handle &h = w->h;
+  const bool built = h.tl.built && h.tl.key.rows > 0;
+  if (ntiles) *ntiles = built ? (h.tl.key.rows + lk::kTileRows - 1) / lk::kTileRows : 0;
+  if (union_count) *union_count = h.tl.ucount;
   return LK_OK;
 }
 

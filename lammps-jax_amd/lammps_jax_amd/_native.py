@@ -37,7 +37,7 @@ EXPORTED = (
     "lk_bundle_contract", "lk_bundle_model", "lk_bundle_unit_style", "lk_pack_edges_noalloc",
     "lk_setfl_parse", "lk_bundle_element", "lk_model_density", "lk_model_comm", "lk_model_force",
     "lk_comm_pack_forward", "lk_comm_unpack_forward", "lk_comm_pack_reverse",
-    "lk_comm_unpack_reverse",
+    "lk_comm_unpack_reverse", "lk_tile_lists",
 )
 
 
@@ -158,6 +158,8 @@ def load() -> ctypes.CDLL:
     lib.lk_edge_forces.restype = ip
     lib.lk_neighbor_matrix.argtypes = [vp, pp(vp), pp(vp)]
     lib.lk_neighbor_matrix.restype = ip
+    lib.lk_tile_lists.argtypes = [vp, pp(ip), pp(vp)]
+    lib.lk_tile_lists.restype = ip
     lib.lk_bundle_load.argtypes = [ctypes.c_char_p, pp(vp), ctypes.c_char_p, ip]
     lib.lk_bundle_load.restype = ip
     lib.lk_bundle_free.argtypes = [vp]

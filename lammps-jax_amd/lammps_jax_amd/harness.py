@@ -74,7 +74,7 @@ def _load() -> ctypes.CDLL:
     lib.lkh_swap.restype = ip
     lib.lkh_run_steps.argtypes = [ctypes.POINTER(StepFns), vp, vp, ctypes.POINTER(StepArgs), ip,
                                   ip, ctypes.POINTER(lp), ctypes.POINTER(lp),
-                                  ctypes.POINTER(ip), vp]
+                                  ctypes.POINTER(ip), vp, vp]
     lib.lkh_run_steps.restype = ip
     lib.lkh_swap_sendlist.argtypes = [vp, ip]
     lib.lkh_swap_sendlist.restype = ctypes.POINTER(ctypes.c_int)

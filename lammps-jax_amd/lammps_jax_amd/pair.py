@@ -521,6 +521,17 @@ class PairJax:
         dt = np.float64 if self.contract.precision == 8 else np.float32
         return read_device(rho_ptr, self.max_atoms, dt), read_device(fp_ptr, self.max_atoms, dt)
 
+    def tile_unions(self) -> np.ndarray:
+        """Union size of each tile of the fused float64 EAM step's last tile-list build (-1: a
+        tile past the staging cap); empty before the first build."""
+        n = ctypes.c_int(0)
+        ptr = ctypes.c_void_p()
+        self.h.check(self.h.lib.lk_tile_lists(self.h.ptr, ctypes.byref(n), ctypes.byref(ptr)))
+        if n.value == 0:
+            return np.zeros(0, np.int32)
+        self.torch.cuda.synchronize(self.device)
+        return read_device(ptr.value, n.value, np.int32)
+
     def forces(self) -> np.ndarray:
         self.torch.cuda.synchronize(self.device)
         return self.f.cpu().numpy()

@@ -141,6 +141,24 @@ Tables<S> make_tables(int n_el, int nrho, double drho, int nr, double dr, double
 }
 
 // ---------------------------------------------------------------------------------------------
+// The pair virial of one edge whose force coef * d goes to the sender and -coef * d to the
+// receiver (d = x_r - x_s), in float64: sum_i x_i (x) F_i over both ends is -coef d (x) d, so
+// the sum over edges equals VirialFDotRFunctor's f.r over every row that takes a force
+// (cpp:227-245) when f holds only this pair style's forces, without f.r's cancellation of
+// |F| |x| sized terms. `w` weighs the edge (one-sided rows: 1/2 per directed edge of a full
+// list, whose reverse edge gives the receiver's half).
+template <typename S>
+void add_pair_virial(double W[6], double w, S coef, const S d[3])
+{
+  const double c = w * static_cast<double>(coef);
+  W[0] -= c * d[0] * d[0];
+  W[1] -= c * d[1] * d[1];
+  W[2] -= c * d[2] * d[2];
+  W[3] -= c * d[0] * d[1];
+  W[4] -= c * d[0] * d[2];
+  W[5] -= c * d[1] * d[2];
+}
+
 // EAM energy and gradient, three accumulation modes.
 //   kPlain    make_setfl_energy(half_edges=False) under wrap_energy_fn: rho and pair energy on the
 //             sender; energy = sum over owned rows, or over all nlocal+nghost rows when a valid
@@ -251,6 +269,7 @@ double eam_compute(const Tables<S> &T, const double *positions_d, const int *spe
         F[3 * s + k] += coef * d[k];
         F[3 * r + k] -= coef * d[k];
       }
+      add_pair_virial(W, 1.0, coef, d);
     } else if (mode == kHalf) {
       const S rhoip = spline_slope(dens + zs * nr4, T.nr, T.dr, rr, false);
       const S coef = (fp[s] * rhojp + fp[r] * rhoip + phip) / rr;
@@ -258,6 +277,7 @@ double eam_compute(const Tables<S> &T, const double *positions_d, const int *spe
         F[3 * s + k] += coef * d[k];
         F[3 * r + k] -= coef * d[k];
       }
+      add_pair_virial(W, 1.0, coef, d);
     } else {  // kOneSided: the row atom takes the whole pair force; ghost rows untouched
       if (s >= nlocal) continue;
       const S rhoip = spline_slope(dens + zs * nr4, T.nr, T.dr, rr, false);
@@ -265,13 +285,7 @@ double eam_compute(const Tables<S> &T, const double *positions_d, const int *spe
       const S coef = psip / rr;
       for (int k = 0; k < 3; ++k) F[3 * s + k] += coef * d[k];
       // Pair virial, half per directed edge of the full list.
-      const double c = 0.5 * static_cast<double>(coef);
-      W[0] -= c * d[0] * d[0];
-      W[1] -= c * d[1] * d[1];
-      W[2] -= c * d[2] * d[2];
-      W[3] -= c * d[0] * d[1];
-      W[4] -= c * d[0] * d[2];
-      W[5] -= c * d[1] * d[2];
+      add_pair_virial(W, 0.5, coef, d);
     }
   }
   for (long k = 0; k < static_cast<long>(max_atoms) * 3; ++k) forces_out[k] = static_cast<double>(F[k]);
@@ -346,17 +360,12 @@ double lj_compute(double epsilon, double sigma, double cutoff, double edge_energ
         F[3 * s + k] += coef * d[k];
         F[3 * r + k] -= coef * d[k];
       }
+      add_pair_virial(W, 1.0, coef, d);
     } else {  // kOneSided: full pair force on the row atom
       if (s >= nlocal) continue;
       const S coef = S(2) * dd;
       for (int k = 0; k < 3; ++k) F[3 * s + k] += coef * d[k];
-      const double c = 0.5 * static_cast<double>(coef);
-      W[0] -= c * d[0] * d[0];
-      W[1] -= c * d[1] * d[1];
-      W[2] -= c * d[2] * d[2];
-      W[3] -= c * d[0] * d[1];
-      W[4] -= c * d[0] * d[2];
-      W[5] -= c * d[1] * d[2];
+      add_pair_virial(W, 0.5, coef, d);
     }
   }
   for (long k = 0; k < static_cast<long>(max_atoms) * 3; ++k) forces_out[k] = static_cast<double>(F[k]);

@@ -190,7 +190,9 @@ def eam_compute(tables, positions, species, *, nlocal, nghost, senders, receiver
                 mode=PLAIN, precision=8, owned_rows_only=False, ghost_owner=None):
     """EAM energy and forces in the reference's semantics (see lk_oracle.cpp for the modes).
 
-    Returns dict(energy, forces [max_atoms,3], rho, fp, virial6 (one-sided pair virial))."""
+    Returns dict(energy, forces [max_atoms,3], rho, fp, virial): the virial is the pair sum
+    -sum_e coef_e d_e (x) d_e in float64 (half per directed edge in the one-sided mode), which
+    equals the f.r virial of the forces over every row that takes one."""
     pos = _c(positions, np.float64)
     max_atoms = pos.shape[0]
     sp = _c(species, np.int32)
@@ -213,6 +215,7 @@ def eam_compute(tables, positions, species, *, nlocal, nghost, senders, receiver
 
 def lj_compute(params, positions, *, nlocal, nghost, senders, receivers, mask, mode=PLAIN,
                precision=8, owned_rows_only=False):
+    """LJ 12-6 energy, forces and pair-sum virial (as eam_compute's)."""
     pos = _c(positions, np.float64)
     max_atoms = pos.shape[0]
     s, r, m = _c(senders, np.int32), _c(receivers, np.int32), _c(mask, np.uint8)

@@ -58,12 +58,21 @@ def fold_ghosts(forces: np.ndarray, nlocal: int, ghost_owner: np.ndarray) -> np.
 
 
 # Parity bars. Float64: the reference's own (tests/test_lammps.py:49-51): forces within 1e-11
-# absolute, energy within 1e-13 per atom; the virial within 1e-12 relative (normwise). Float32:
-# 1e-5 relative.
+# absolute, energy within 1e-13 per atom; the virial within 1e-12 relative (normwise). Forces
+# above 100 (near-contact LJ pairs reach 4e5) round at float64 by more than 1e-11, so there the
+# force bar is 1e-13 normwise relative (max|dF| / max|F|), still a thousandth of the 1e-10
+# relative the path is specified to. Float32: 1e-5 relative.
 F64_FORCE_ABS = 1.0e-11
+F64_FORCE_REL = 1.0e-13
 F64_ENERGY_PER_ATOM = 1.0e-13
 F64_VIRIAL_REL = 1.0e-12
 F32_REL = 1.0e-5
+
+
+def f64_force_bar(ref) -> float:
+    """The float64 force bar for reference forces `ref`: 1e-11 absolute, or 1e-13 of max|F|."""
+    scale = float(np.max(np.abs(ref))) if np.size(ref) else 0.0
+    return max(F64_FORCE_ABS, F64_FORCE_REL * scale)
 
 
 def assert_energy(precision: int, energy: float, ref: float, natoms: int, scale: float = 1.0):
@@ -76,7 +85,7 @@ def assert_energy(precision: int, energy: float, ref: float, natoms: int, scale:
 def assert_forces(precision: int, f, ref):
     if precision == 8:
         err = float(np.max(np.abs(np.asarray(f, np.float64) - ref))) if np.size(f) else 0.0
-        assert err <= F64_FORCE_ABS, err
+        assert err <= f64_force_bar(ref), err
     else:
         assert rel_err(f, ref) < F32_REL
 

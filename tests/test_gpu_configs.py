@@ -32,6 +32,7 @@ import oracle as O
 from lk_testutil import canonical, fold_ghosts, rel_err
 from lammps_jax_amd import systems
 from lammps_jax_amd.pair import PairJax
+from test_gpu_tiles import union_sizes
 
 pytestmark = pytest.mark.gpu
 
@@ -117,6 +118,9 @@ def test_workload_at_full_size(gpu, name, order):
         assert abs(info.energy - ref["energy"]) / nl <= F32_ENERGY_PER_ATOM
         assert rel_err(f[:rows], f_ref) < F32_REL
         assert rel_err(info.virial, vir_ref) < F32_REL
+    if name == "eam_alloy_131k":
+        # the fused step's tile lists staged every tile's neighbour union in LDS
+        np.testing.assert_array_equal(pj.tile_unions(), union_sizes(sysm, lst))
     if wl.model == "eam":
         rho, fp = pj.model_rows()
         tol = 1e-13 if wl.precision == 8 else F32_REL

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lk_testutil import assert_energy, assert_forces, assert_virial
+from lk_testutil import assert_energy, assert_forces, assert_virial, canonical, rel_err
 from lammps_jax_amd import systems
 from lammps_jax_amd.md import Nve
 
@@ -57,3 +57,35 @@ def test_nve_reneighbors_and_keeps_parity(gpu):
     assert_forces(8, f[:nl], ref["forces"][:nl])
     assert_virial(8, info.virial, ref["virial"])
     assert np.all(f[nl:] == 0.0)
+
+
+def test_nve_full_size_131k_keeps_parity(gpu):
+    """The 131,072-atom alloy's NVE run (600 K, dt 2 fs) through at least one list rebuild; the
+    last step's packed edges, energy, forces, virial and F' rows against the oracle at the
+    reference's float64 bar."""
+    wl = systems.make_workload("eam_alloy_131k")
+    md = Nve(wl, temperature=600.0, dt=0.002)
+    print("nve case eam_alloy_131k full size dt=0.002 steps=24", flush=True)
+    rep = md.run(24).summary()
+    print(f"  rebuilds {rep['rebuilds']} drift {rep['etot_max_rel_drift']:.2e}", flush=True)
+    assert rep["rebuilds"] >= 1
+    assert rep["etot_max_rel_drift"] < 1e-4
+    pj, sysm = md.pj, md.pj.system
+    x = pj.x.cpu().numpy()
+    info = pj.compute()
+    f = pj.forces().copy()
+    nl, nall = sysm.nlocal, sysm.nall
+    pos, sp = O.pack_atoms(x, sysm.type, nall, pj.max_atoms, 8)
+    s, r, m, count, _ = O.pack_neighbors(x, sysm.list, max_atoms=pj.max_atoms,
+                                         max_edges=pj.max_edges, nlocal=nl, cutoff=wl.cutoff)
+    ref = O.eam_compute(wl.tables, pos, sp, nlocal=nl, nghost=sysm.nghost, senders=s,
+                        receivers=r, mask=m, mode=O.ONESIDED, ghost_owner=sysm.ghost_owner)
+    assert info.edge_count == count and info.edge_overflow == 0
+    ds, dr_, dm = pj.edges()
+    np.testing.assert_array_equal(canonical(ds, dr_, dm), canonical(s, r, m))
+    assert_energy(8, info.energy, ref["energy"], nl)
+    assert_forces(8, f[:nl], ref["forces"][:nl])
+    assert_virial(8, info.virial, ref["virial"])
+    assert np.all(f[nl:nall] == 0.0)
+    _, fp = pj.model_rows()
+    assert rel_err(fp[:nall], ref["fp"][:nall]) < 1e-13

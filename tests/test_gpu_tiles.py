@@ -126,6 +126,9 @@ def test_tiles_over_and_under_the_union_cap(gpu, scramble):
     pj = PairJax(sysm, ("eam", wl.tables), precision=8, accumulation="onesided",
                  edges_per_atom=256)
     _check(wl, sysm, pj, pj.compute(), "first step")
+    # the library staged exactly the tiles whose union fits, each with the union size counted
+    # here, and sent the others to the gather from memory
+    np.testing.assert_array_equal(pj.tile_unions(), np.where(sizes <= UNION_CAP, sizes, -1))
 
 
 def test_tile_lists_reused_until_the_list_changes(gpu):

@@ -280,6 +280,45 @@ def test_eam_virial_pair_sum_equals_fdotr_with_ghost_rows():
                         mode=O.ONESIDED, ghost_owner=sysm.ghost_owner)
     assert rel_err(one["virial"], w_fdotr) < 1e-11
     assert abs(w_fdotr[0]) > 1e-3  # a real signal
+    # the two-sided schemes' pair sums equal f.r of their own forces over every row
+    assert rel_err(plain["virial"], w_fdotr) < 1e-11
+    lst_h = sysm.build_list(wl.cutoff + wl.skin, kind=1)
+    hs, hr, hm, _, _ = O.pack_neighbors(sysm.x, lst_h, max_atoms=nall, max_edges=200 * nall,
+                                        nlocal=nlocal, cutoff=wl.cutoff)
+    half = O.eam_compute(t, pos, sp, nlocal=nlocal, nghost=nghost, senders=hs, receivers=hr,
+                         mask=hm, mode=O.HALF, ghost_owner=sysm.ghost_owner)
+    assert rel_err(half["virial"], O.virial_fdotr(half["forces"][:nall], sysm.x, nall)) < 1e-11
+    assert rel_err(half["virial"], w_fdotr) < 1e-11
+
+
+def test_eam_float32_virial_rounding_floor():
+    """A near-zero virial (a 3^3-cell half-list alloy at |W| ~ 2.4) is ill-conditioned in the
+    float32 contract itself: narrowing the positions to float32 (PackAtomsFunctor, cpp:35-52)
+    and nothing else already moves the float64 virial by more than 1e-5 relative, so no float32
+    evaluation can sit within 1e-5 of float64 there. The float32 pair sum and f.r of the float32
+    forces land equally far from float64: the error is the float32 model's, not f.r's."""
+    from sweep_cases import sweep_case
+
+    c = sweep_case(2, 113)
+    sysm, lst = c.build()
+    t = c.model_spec()[1]
+    nlocal, nghost = sysm.nlocal, sysm.nghost
+    nall = nlocal + nghost
+    s, r, m, _, _ = O.pack_neighbors(sysm.x, lst, max_atoms=nall, max_edges=200 * nall,
+                                     nlocal=nlocal, cutoff=c.cutoff)
+    kw = dict(nlocal=nlocal, nghost=nghost, senders=s, receivers=r, mask=m, mode=O.HALF,
+              ghost_owner=sysm.ghost_owner)
+    pos64, sp = O.pack_atoms(sysm.x, sysm.type, nall, nall, 8)
+    pos32, _ = O.pack_atoms(sysm.x, sysm.type, nall, nall, 4)
+    v64 = O.eam_compute(t, pos64, sp, precision=8, **kw)["virial"]
+    assert np.max(np.abs(v64)) < 5.0
+    v_rounded_x = O.eam_compute(t, pos32.astype(np.float64), sp, precision=8, **kw)["virial"]
+    assert rel_err(v_rounded_x, v64) > 1e-5
+    out32 = O.eam_compute(t, pos32, sp, precision=4, **kw)
+    err_pair = rel_err(out32["virial"], v64)
+    err_fdotr = rel_err(O.virial_fdotr(out32["forces"][:nall], sysm.x, nall), v64)
+    assert 1e-5 < err_pair < 1e-4 and 1e-5 < err_fdotr < 1e-4
+    assert 0.5 < err_pair / err_fdotr < 2.0
 
 
 def test_eam_translation_invariance_and_momentum():
@@ -367,6 +406,7 @@ def test_lj_periodic_matches_dense_and_virial():
     assert rel_err(one["forces"][:nlocal], f_d) < 1e-12
     f = O.add_forces(np.zeros((nall, 3)), plain["forces"][:nall], nall)
     assert rel_err(one["virial"], O.virial_fdotr(f, sysm.x, nall)) < 1e-11
+    assert rel_err(plain["virial"], O.virial_fdotr(f, sysm.x, nall)) < 1e-11
 
 
 # --------------------------------------------------------------------------------------------

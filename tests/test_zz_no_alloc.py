@@ -4,7 +4,8 @@ Two packs in a row, the second on a smaller system into the same caller-owned ar
 previous count bounding the tail reset): after each, the caller's senders, receivers and mask,
 the demand count and the overflow flag equal, bit for bit, what lk_pack_edges writes into a
 handle's arrays for the same two calls (the same kernels, so the same packed order, padding
-included). Also: a call past the fixed working memory's row limit is refused before any launch.
+included); the second call leaves the device's free memory (hipMemGetInfo) as it found it.
+Also: a call past the fixed working memory's row limit is refused before any launch.
 """
 
 from __future__ import annotations
@@ -67,6 +68,8 @@ def test_noalloc_pack_matches_lk_pack_edges_twice_in_a_row(gpu):
                      d["neighbors"].data_ptr(), lst["stride"], lst["inum"], lst["gnum"],
                      lst["maxneighs"], sysm.nlocal)
         info = h.step_result(stream)
+        torch.cuda.synchronize(dev)
+        free_before = torch.cuda.mem_get_info(dev)[0]
         rc = lib.lk_pack_edges_noalloc(
             ctypes.byref(contract), stream, d["x"].data_ptr(), d["ilist"].data_ptr(),
             d["numneigh"].data_ptr(), d["neighbors"].data_ptr(), lst["stride"], lst["inum"],
@@ -74,6 +77,8 @@ def test_noalloc_pack_matches_lk_pack_edges_twice_in_a_row(gpu):
             mask.data_ptr(), counts.data_ptr(), prev, err, len(err))
         assert rc == N.LK_OK, err.value.decode()
         torch.cuda.synchronize(dev)
+        if seen:  # past the first call on this device: the call took no device memory
+            assert torch.cuda.mem_get_info(dev)[0] == free_before
         c = counts.cpu().numpy()
         assert int(c[0]) == info.edge_count and int(c[1]) == info.edge_overflow == 0
         assert info.edge_count > 0
