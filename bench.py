@@ -290,6 +290,62 @@ def lean_step(pj, eflag: bool = True, vflag: bool = True, rebuild_every: int = 0
     return run
 
 
+def split_step(pj, eflag: bool = True, vflag: bool = True, rebuild_every: int = 0):
+    """Engine steps with the model pass split at its exchange, as a multi-rank LAMMPS run makes
+    them: lk_pack_density, the forward exchange of rho over the ghost swaps through the comm
+    buffer calls (lk_comm_pack_forward / lk_comm_unpack_forward, the pair style's Kokkos comm
+    hooks; on one rank each swap's buffer goes straight from pack to unpack), lk_model_force,
+    lk_step_result; from the harness's C++ loop (lkh_run_split_steps). Same rebuild signal and
+    return value as lean_step."""
+    import ctypes
+
+    from lammps_jax_amd import _native as N
+    from lammps_jax_amd import harness
+    from lammps_jax_amd.pair import DeviceComm
+
+    hl = harness._load()
+    lib, h, s = pj.h.lib, pj.h.ptr, pj.system
+    lst = s.list
+    flags = (N.LK_ENERGY if eflag else 0) | (N.LK_VIRIAL if vflag else 0)
+    addr = lambda fn: ctypes.cast(fn, ctypes.c_void_p).value  # noqa: E731
+    fns = harness.SplitFns(*(addr(getattr(lib, name)) for name in (
+        "lk_pack_density", "lk_model_comm", "lk_comm_pack_forward", "lk_comm_unpack_forward",
+        "lk_comm_pack_reverse", "lk_comm_unpack_reverse", "lk_model_force", "lk_step_result",
+        "lk_set_list_epoch")))
+    args = harness.StepArgs(pj.x.data_ptr(), pj.type.data_ptr(), s.nall, pj.ilist.data_ptr(),
+                            pj.numneigh.data_ptr(), pj.neighbors.data_ptr(), lst["stride"],
+                            lst["inum"], lst["gnum"], lst["maxneighs"], s.nlocal, s.nghost, flags,
+                            pj.scale, pj.f.data_ptr())
+    comm = DeviceComm(pj, s)
+    n = len(comm.swaps)
+    n_max = max((c for _, _, c in comm.swaps), default=1)
+    sendlists = (ctypes.c_void_p * max(n, 1))(*[sl.data_ptr() for sl, _, _ in comm.swaps])
+    firsts = (ctypes.c_int * max(n, 1))(*[first for _, first, _ in comm.swaps])
+    counts = (ctypes.c_int * max(n, 1))(*[c for _, _, c in comm.swaps])
+    swaps = harness.Swaps(n, sendlists, firsts, counts, comm._buffer(n_max, 3))
+    info = N.LkStepInfo()
+    epoch, calls, rebuilds = ctypes.c_long(pj.list_epoch), ctypes.c_long(0), ctypes.c_int(0)
+    stream = ctypes.c_void_p(pj.stream())
+
+    def run(n_steps: int, step_s=None):
+        times = None if step_s is None else step_s.ctypes.data
+        rc = hl.lkh_run_split_steps(ctypes.byref(fns), h, stream, ctypes.byref(args),
+                                    ctypes.byref(swaps), int(n_steps), int(rebuild_every),
+                                    ctypes.byref(epoch), ctypes.byref(calls),
+                                    ctypes.byref(rebuilds), ctypes.byref(info), times)
+        pj.list_epoch = epoch.value
+        run.rebuilds = rebuilds.value
+        if rc == N.LK_ERR_CAPACITY and info.edge_overflow:
+            raise N.LammpsJaxError(N.LK_ERR_CAPACITY, "LAMMPS-JAX edge capacity exceeded")
+        if rc != N.LK_OK:
+            raise N.LammpsJaxError(rc, pj.h.error())
+        return info
+
+    run.rebuilds = 0
+    run.keep = (comm, sendlists, firsts, counts, swaps, fns, args)  # alive while run is
+    return run
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -306,6 +362,10 @@ def main() -> int:
                     help="a list-rebuild step every STEPS steps in the timed loops (the 131k-atom "
                          "NVE run at 600 K rebuilds its list 8 times in 100 steps); the library's "
                          "once-per-list work runs inside those steps. 0: the list never changes")
+    ap.add_argument("--split", action="store_true",
+                    help="time the step split at the model's exchange (lk_pack_density, the "
+                         "forward exchange of rho over the ghost swaps, lk_model_force) as the "
+                         "headline; EAM one-sided sparse-edge workloads")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--split-steps", type=int, default=20,
@@ -350,10 +410,16 @@ def main() -> int:
           f"max_atoms={max_atoms} max_edges={pj.max_edges} setup {setup_s:.1f}s", file=sys.stderr,
           flush=True)
 
-    step = lean_step(pj)
+    splittable = wl.model == "eam" and wl.accumulation == "onesided" and args.layout == "sparse-edge"
+    if args.split and not splittable:
+        print("bench.py --split: the split step is timed for one-sided EAM sparse-edge workloads",
+              file=sys.stderr)
+        return 2
+    stepper = split_step if args.split else lean_step
+    step = stepper(pj)
     info = step(args.warmup)
     torch.cuda.synchronize(dev)
-    step = lean_step(pj, rebuild_every=args.rebuild_every)
+    step = stepper(pj, rebuild_every=args.rebuild_every)
     t0 = time.perf_counter()
     info = step(args.steps)
     torch.cuda.synchronize(dev)
@@ -367,9 +433,21 @@ def main() -> int:
 
     n_med = max(args.steps, MEDIAN_STEPS)
     per_step = np.zeros(n_med)
-    step_m = lean_step(pj, rebuild_every=args.rebuild_every)
+    step_m = stepper(pj, rebuild_every=args.rebuild_every)
     step_m(n_med, per_step)
     torch.cuda.synchronize(dev)
+    # the other form of the step (fused, or split at the exchange), per step, for comparison
+    other = None
+    if splittable:
+        other_stepper = lean_step if args.split else split_step
+        other_times = np.zeros(n_med)
+        other_stepper(pj)(args.warmup)
+        other_stepper(pj, rebuild_every=args.rebuild_every)(n_med, other_times)
+        torch.cuda.synchronize(dev)
+        other = {"step": "fused (lk_pack_compute)" if args.split else
+                         "split at the exchange (lk_pack_density, forward rho, lk_model_force)",
+                 "steps": n_med, "ms_per_step_mean": round(1e3 * float(other_times.mean()), 5),
+                 "ms_per_step_median": round(1e3 * float(np.median(other_times)), 5)}
     # the same steps through the Python host mirror (PairJax.compute: f cleared by torch each
     # step, result wrapped in Python objects), reported beside the C-caller rate
     torch.cuda.synchronize(dev)
@@ -381,7 +459,7 @@ def main() -> int:
     # stage timing: the same steps again with HIP events recorded around every launch on the
     # launch stream (lk_timing_*); kept out of the timed loop above, whose rate they would slow
     pj.h.timing_enable(True)
-    step_t = lean_step(pj, rebuild_every=args.rebuild_every)
+    step_t = stepper(pj, rebuild_every=args.rebuild_every)
     t0 = time.perf_counter()
     step_t(args.steps)
     torch.cuda.synchronize(dev)
@@ -391,7 +469,7 @@ def main() -> int:
     # forces-only steps (eflag = vflag = 0), as most MD steps run between thermo outputs
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
-    step_f = lean_step(pj, eflag=False, vflag=False, rebuild_every=args.rebuild_every)
+    step_f = stepper(pj, eflag=False, vflag=False, rebuild_every=args.rebuild_every)
     step_f(args.steps)
     torch.cuda.synchronize(dev)
     forces_only_ms = 1e3 * (time.perf_counter() - t0) / args.steps
@@ -480,8 +558,12 @@ def main() -> int:
             "edge_capacity_per_atom": wl.edges_per_atom,
             "accumulation": wl.accumulation,
             "layout": args.layout,
-            "step": "pack_atoms + pack_edges + model E/F/virial + f add + host readback "
-                    "(lk_pack_compute + lk_step_result; f cleared by the engine, not timed)",
+            "step": ("pack_atoms + pack_edges + density (lk_pack_density), forward exchange of "
+                     "rho over the ghost swaps (lk_comm_pack/unpack_forward), F' of the ghost "
+                     "rows + force/virial + f add (lk_model_force) + host readback "
+                     "(lk_step_result); f cleared by the engine, not timed" if args.split else
+                     "pack_atoms + pack_edges + model E/F/virial + f add + host readback "
+                     "(lk_pack_compute + lk_step_result; f cleared by the engine, not timed)"),
             "list_rebuild_every": args.rebuild_every,
             "list_rebuild_steps_timed": rebuilds_timed,
             "list_rebuild_source": REBUILD_SOURCE,
@@ -497,6 +579,7 @@ def main() -> int:
                                    + ("_sorted" if args.atom_order == "sorted" else "")),
         },
         "cpu_baseline": cpu,
+        "other_step_form": other,
         "nve": nve,
         "stages_us": {k: round(v, 2) for k, v in sorted(stage_us.items())},
         "stages_us_per_step": {k: round(v, 2) for k, v in sorted(stage_us_step.items())},

@@ -249,7 +249,20 @@ int lk_pack_compute(lk_handle *h, void *stream, const double *x, const int *type
  * The exchanges are the reference's (eam.py:316-317 for the half scheme: reverse, then forward;
  * eam_pallas.py:337 for complete rows: forward). No ghost map is needed. lk_model_force takes
  * the same nlocal and nghost as the density pass of the same pack (LK_ERR_STATE otherwise).
+ *
+ * lk_pack_density is the first three calls in one, as lk_pack_compute is the step's: the step of
+ * PairJaxKokkos::compute up to the model's first exchange (cpp/pair_jax_kokkos.cpp:1023-1055,
+ * then service_model_comm at cpp:444-469). Its arguments are lk_pack_compute's less the force
+ * ones. In the one-sided scheme the pack and the owned rows' densities, F and F' run fused (over
+ * the tile lists for float64 with a list epoch), as in lk_pack_compute, but without a ghost map:
+ * the ghost rows' F' come from the exchanged densities in lk_model_force, whose force sweep also
+ * finishes the pack (the tail reset past this step's count, the edge count and overflow flag of
+ * lk_step_result). The half scheme runs lk_pack_atoms, lk_pack_edges, lk_model_density. Read the
+ * step result after lk_model_force.
  */
+int lk_pack_density(lk_handle *h, void *stream, const double *x, const int *type, int nall,
+                    const int *ilist, const int *numneigh, const int *neighbors, long nb_stride,
+                    int inum, int gnum, int maxneighs, int nlocal, int nghost);
 int lk_model_density(lk_handle *h, void *stream, int nlocal, int nghost);
 int lk_model_comm(lk_handle *h, int site, int *forward, void **rows, int *width);
 int lk_model_force(lk_handle *h, void *stream, int nlocal, int nghost, int flags, double scale,

@@ -601,6 +601,7 @@ int lk_pack_atoms(lk_handle *w, void *stream, const double *x, const int *type, 
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
   h.pack_ready = false;
+  h.split_pack = lk::FusedPack{};  // a fused split pack is finished only by its own force pass
   if (nall < 0 || (nall > 0 && (!x || !type))) return fail(h, LK_ERR_ARGUMENT, "invalid atom arrays");
   h.x_last = x;
   h.type_last = type;
@@ -617,6 +618,7 @@ int lk_pack_edges(lk_handle *w, void *stream, const double *x, const int *ilist,
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
   h.pack_ready = false;
+  h.split_pack = lk::FusedPack{};  // a fused split pack is finished only by its own force pass
   const lk_contract &c = h.contract;
   if (inum < 0 || gnum < 0 || nlocal < 0) return fail(h, LK_ERR_ARGUMENT, "invalid list sizes");
   const bool multi_hop = c.n_hops > 1;
@@ -693,6 +695,7 @@ int lk_compute(lk_handle *w, void *stream, int nlocal, int nghost, int flags, do
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
   h.pack_ready = false;
+  h.split_pack = lk::FusedPack{};  // a fused split pack is finished only by its own force pass
   if (h.model == 0) return fail(h, LK_ERR_STATE, "LAMMPS-JAX runtime is not initialized");
   if (nlocal < 0 || nghost < 0 || !f) return fail(h, LK_ERR_ARGUMENT, "invalid compute arguments");
   if (static_cast<long>(nlocal) + nghost > h.contract.max_atoms)
@@ -1028,6 +1031,7 @@ int lk_model_density(lk_handle *w, void *stream, int nlocal, int nghost)
   if (!w) return LK_ERR_ARGUMENT;
   Handle &h = w->h;
   h.pack_ready = false;
+  h.split_pack = lk::FusedPack{};  // a fused split pack is finished only by its own force pass
   if (int rc = split_check(h, nlocal, nghost)) return rc;
   hipStream_t s = as_stream(stream);
   hipError_t e;
@@ -1041,6 +1045,50 @@ int lk_model_density(lk_handle *w, void *stream, int nlocal, int nghost)
                              lk::FusedPack{}, lk::kPhaseDensity);
   }
   if (e != hipSuccess) return hip_fail(h, e, "model density");
+  h.split_serial = h.pack_serial;
+  h.split_nall = nlocal + nghost;
+  h.result_mirrored = false;
+  return LK_OK;
+}
+
+int lk_pack_density(lk_handle *w, void *stream, const double *x, const int *type, int nall,
+                    const int *ilist, const int *numneigh, const int *neighbors, long nb_stride,
+                    int inum, int gnum, int maxneighs, int nlocal, int nghost)
+{
+  if (!w) return LK_ERR_ARGUMENT;
+  Handle &h = w->h;
+  if (int rc = split_check(h, nlocal, nghost)) return rc;
+  if (h.accum != LK_ACCUM_ONESIDED) {
+    // the half scheme's density needs the packed edges: the three calls in order
+    int rc = lk_pack_atoms(w, stream, x, type, nall);
+    if (rc == LK_OK) rc = lk_pack_edges(w, stream, x, ilist, numneigh, neighbors, nb_stride, inum,
+                                        gnum, maxneighs, nlocal);
+    if (rc == LK_OK) rc = lk_model_density(w, stream, nlocal, nghost);
+    return rc;
+  }
+  const lk_contract &c = h.contract;
+  if (nall < 0 || inum < 0 || gnum < 0) return fail(h, LK_ERR_ARGUMENT, "invalid step arguments");
+  long rows = static_cast<long>(inum) + (c.n_hops > 1 ? gnum : 0);
+  if (rows > c.max_atoms) rows = c.max_atoms;
+  const int max_neighbors_per_atom = maxneighs > 1 ? maxneighs : 1;
+  if (rows * max_neighbors_per_atom > static_cast<long>(INT_MAX))
+    return fail(h, LK_ERR_CAPACITY,
+                "LAMMPS-JAX neighbor pack index overflows int; reduce the bundle max_atoms or the "
+                "neigh_modify one setting");
+  if ((rows > 0 || nall > 0) && (!x || !type || !ilist || !numneigh || !neighbors))
+    return fail(h, LK_ERR_ARGUMENT, "invalid atom or neighbor list arrays");
+  if (int rc = ensure_bits(h, max_neighbors_per_atom)) return rc;
+  if (int rc = prepare_nonrows(h, inum, nlocal)) return rc;
+  h.split_pack = lk::FusedPack{};
+  hipError_t e = lk::launch_step_density(h, as_stream(stream), x, type, nall, ilist, numneigh,
+                                         neighbors, nb_stride, static_cast<int>(rows),
+                                         max_neighbors_per_atom, nlocal, nghost);
+  if (e != hipSuccess) {
+    h.split_pack = lk::FusedPack{};
+    return hip_fail(h, e, "fused pack and density");
+  }
+  h.x_last = x;
+  h.type_last = type;
   h.split_serial = h.pack_serial;
   h.split_nall = nlocal + nghost;
   h.result_mirrored = false;

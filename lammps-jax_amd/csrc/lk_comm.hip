@@ -102,6 +102,7 @@ hipError_t launch_comm_pack_forward(Handle &h, hipStream_t s, const void *rows, 
 {
   if (n <= 0) return hipSuccess;
   const int words = width * static_cast<int>(h.scalar_bytes() / 4);
+  StageTimer timer(h, s, "comm_pack_forward");
   hipLaunchKernelGGL(k_comm_pack_list, comm_grid(n, words), dim3(kCommBlock), 0, s,
                      static_cast<const uint32_t *>(rows), list, n, words, comm_slots(h, width),
                      h.contract.max_atoms, reinterpret_cast<uint32_t *>(buf));
@@ -113,6 +114,7 @@ hipError_t launch_comm_unpack_forward(Handle &h, hipStream_t s, void *rows, int 
 {
   if (n <= 0) return hipSuccess;
   const int words = width * static_cast<int>(h.scalar_bytes() / 4);
+  StageTimer timer(h, s, "comm_unpack_forward");
   hipLaunchKernelGGL(k_comm_unpack_at, comm_grid(n, words), dim3(kCommBlock), 0, s,
                      static_cast<uint32_t *>(rows), first, n, words, comm_slots(h, width),
                      reinterpret_cast<const uint32_t *>(buf));
@@ -124,6 +126,7 @@ hipError_t launch_comm_pack_reverse(Handle &h, hipStream_t s, const void *rows, 
 {
   if (n <= 0) return hipSuccess;
   const int words = width * static_cast<int>(h.scalar_bytes() / 4);
+  StageTimer timer(h, s, "comm_pack_reverse");
   hipLaunchKernelGGL(k_comm_pack_at, comm_grid(n, words), dim3(kCommBlock), 0, s,
                      static_cast<const uint32_t *>(rows), first, n, words, comm_slots(h, width),
                      reinterpret_cast<uint32_t *>(buf));
@@ -135,6 +138,7 @@ hipError_t launch_comm_unpack_reverse(Handle &h, hipStream_t s, void *rows, int 
 {
   if (n <= 0) return hipSuccess;
   const int slots = comm_slots(h, width);
+  StageTimer timer(h, s, "comm_unpack_reverse");
   if (h.contract.precision == LK_FLOAT64)
     hipLaunchKernelGGL(k_comm_add_list<double>, comm_grid(n, width), dim3(kCommBlock), 0, s,
                        static_cast<double *>(rows), list, n, width, slots, h.contract.max_atoms,

@@ -83,16 +83,16 @@ __device__ __forceinline__ Locator<S> locate(S x, S delta, int n)
 }
 
 // Interval and fraction with a multiply by 1/delta (per-edge lookups; the division's result can
-// differ in the last bit, which moves t by one ulp at most).
+// differ in the last bit, which moves t by one ulp at most). The node is idx clamped to
+// [0, n-2] (fmax maps NaN to 0) and then truncated: for a non-negative value truncation is the
+// floor, so this is locate's floor-then-clip node in fewer operations.
 template <typename S>
 __device__ __forceinline__ Locator<S> locate_mul(S x, S inv_delta, int n)
 {
   Locator<S> L;
   const S idx = x * inv_delta;
-  S fl = floor(idx);
-  fl = fl >= S(0) ? fl : S(0);
-  fl = fl <= S(n - 2) ? fl : S(n - 2);
-  L.node = static_cast<int>(fl);
+  const S c = fmin(fmax(idx, S(0)), static_cast<S>(n - 2));
+  L.node = static_cast<int>(c);
   L.t_raw = idx - static_cast<S>(L.node);
   L.t = L.t_raw < S(1) ? L.t_raw : S(1);
   return L;

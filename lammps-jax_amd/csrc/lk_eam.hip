@@ -231,10 +231,14 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
             r2 = dx * dx + dy * dy + dz * dz;
           }
           if (!(r2 < a.cutsq)) return;
+          // the species conversion stays here: hoisted into the gather, its wait for the record
+          // held back the F' load behind it
+          S wj = r.at.w;
+          asm volatile("" : "+v"(wj));
           const S rinv = rsqrt_nr(r2);
           const S rr = r2 * rinv;
           const Locator<S> L = locate_mul(rr, a.inv_dr, a.nr);
-          const int zj = clamp_species(static_cast<int>(r.at.w), a.n_el);
+          const int zj = clamp_species(static_cast<int>(wj), a.n_el);
           const int tp = a.n_el + pair_row(zi, zj);
           S sj, si, z2, z2s;  // slopes in t of rho_j, rho_i and z2r, and z2r itself
           if (sizeof(S) == 8 && wave_ballot(L.node < win.lo) == 0) {
@@ -264,13 +268,11 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
             z2s = cslope_t(cp, L.t);
           }
           // Past the table the non-extrapolated lookups saturate: autodiff slope 0 (eam.py:150).
-          const bool inside = !(L.t_raw > S(1));
-          const S rhojp = inside ? sj * a.inv_dr : S(0);
-          const S rhoip = inside ? si * a.inv_dr : S(0);
-          const S z2p = inside ? z2s * a.inv_dr : S(0);
+          // The slopes in t become slopes in r through one factor (1/dr inside, 0 past).
+          const S kin = L.t_raw > S(1) ? S(0) : a.inv_dr;
           const S phi = z2 * rinv;
-          const S phip = (z2p - phi) * rinv;
-          const S psip = fpi * rhojp + r.fp * rhoip + phip;
+          const S phip = (z2s * kin - phi) * rinv;
+          const S psip = (fpi * sj + r.fp * si) * kin + phip;
           const S coef = psip * rinv;
           ep += S(0.5) * phi;
           const S gx = coef * dx, gy = coef * dy, gz = coef * dz;
@@ -366,7 +368,13 @@ static hipError_t eam_onesided(Handle &h, hipStream_t s, int nlocal, int nghost,
       hipLaunchKernelGGL(k_embed_rows<S>, dim3((nghost + 255) / 256), dim3(256), 0, s, a, nlocal,
                          nlocal + nghost);
     }
-    return launch_eam_force(h, s, a, flags);
+    // after lk_pack_density the force pass finishes its pack (tail reset, counts) and leaves
+    // the pack state ready for the next fused pack
+    a.pack = h.split_pack;
+    h.split_pack = FusedPack{};
+    const hipError_t e = launch_eam_force(h, s, a, flags);
+    h.pack_ready = e == hipSuccess && a.pack.state != nullptr;
+    return e;
   }
   if (ntiles > 0) {
     const int ngroups = (ntiles + kDensTPB - 1) / kDensTPB;

@@ -82,6 +82,7 @@ struct Handle {
   int packed_rows = 0;          // list rows of the last pack
   int pack_serial = 0;
   int split_serial = -1;        // pack_serial of the last lk_model_density (split model pass)
+  FusedPack split_pack;         // lk_pack_density's pack state for the force pass to finish
   int split_nall = -1;          // its nlocal + nghost
 
   // per-atom model state
@@ -296,5 +297,13 @@ hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const
                                 const int *neighbors, long stride, int num_rows, int maxneighs,
                                 int nlocal, int nghost, int flags, double scale, double *f,
                                 bool matrix = false, bool atoms = true);
+// The one-sided EAM step up to its exchange (lk_pack_density): the atom records, the pack with
+// the owned rows' density, F and F' (no F' to ghost images: the engine's forward exchange of rho
+// fills the ghost rows), and the energy partials. h.split_pack receives the pack state the force
+// pass finishes (tail reset, counts).
+hipError_t launch_step_density(Handle &h, hipStream_t s, const double *x, const int *type,
+                               int nall, const int *ilist, const int *numneigh,
+                               const int *neighbors, long stride, int num_rows, int maxneighs,
+                               int nlocal, int nghost);
 
 }  // namespace lk

@@ -523,7 +523,7 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
                                 int nall, const int *ilist, const int *numneigh,
                                 const int *neighbors, long stride, int num_rows, int maxneighs,
                                 int nlocal, int nghost, int flags, double scale, double *f,
-                                bool atoms)
+                                bool atoms, bool split = false)
 {
   h.packed_rows = num_rows;
   EamArgs<S> a{};
@@ -555,7 +555,8 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   p.senders = h.d_senders;
   p.receivers = h.d_receivers;
   p.mask = h.d_mask;
-  p.ghost_off = nghost > 0 ? h.d_ghost_off : nullptr;
+  // split: the engine's exchange of rho between the passes gives the ghost rows their F'
+  p.ghost_off = nghost > 0 && !split ? h.d_ghost_off : nullptr;
   p.ghost_list = h.d_ghost_list;
   p.atoms_out = nullptr;
   p.species_out = nullptr;
@@ -587,7 +588,7 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
     if (tiled)
       if (hipError_t e1 = launch_step_tiles(h, s, x, type, ilist, numneigh, neighbors, stride,
                                             num_rows, maxneighs, nlocal, nghost, a,
-                                            tiled && atoms ? records : 0);
+                                            tiled && atoms ? records : 0, !split);
           e1 != hipSuccess)
         return e1;
   }
@@ -608,7 +609,13 @@ static hipError_t step_onesided(Handle &h, hipStream_t s, const double *x, const
   fp.pad = h.contract.max_atoms;
   if constexpr (EAM) {
     if (nonrows)
-      if (hipError_t e = launch_embed_nonrows(h, s, nlocal, nghost > 0); e != hipSuccess) return e;
+      if (hipError_t e = launch_embed_nonrows(h, s, nlocal, nghost > 0 && !split);
+          e != hipSuccess)
+        return e;
+    if (split) {  // the force pass (lk_model_force) finishes the pack
+      h.split_pack = fp;
+      return hipGetLastError();
+    }
     a.pack = fp;
     hipError_t e = launch_eam_force(h, s, a, flags);
     // its last block resets the pack state for the next fused pack (finalize_last_block)
@@ -693,6 +700,20 @@ hipError_t launch_pack_fused(Handle &h, hipStream_t s, const double *x, const in
                               maxneighs, nlocal, out);
   return pack_fused<float>(h, s, x, type, nall, ilist, numneigh, neighbors, stride, num_rows,
                            maxneighs, nlocal, out);
+}
+
+hipError_t launch_step_density(Handle &h, hipStream_t s, const double *x, const int *type,
+                               int nall, const int *ilist, const int *numneigh,
+                               const int *neighbors, long stride, int num_rows, int maxneighs,
+                               int nlocal, int nghost)
+{
+  if (h.contract.precision == LK_FLOAT64)
+    return step_onesided<double, true, false>(h, s, x, type, nall, ilist, numneigh, neighbors,
+                                              stride, num_rows, maxneighs, nlocal, nghost, 0, 1.0,
+                                              nullptr, true, true);
+  return step_onesided<float, true, false>(h, s, x, type, nall, ilist, numneigh, neighbors,
+                                           stride, num_rows, maxneighs, nlocal, nghost, 0, 1.0,
+                                           nullptr, true, true);
 }
 
 hipError_t launch_step_onesided(Handle &h, hipStream_t s, const double *x, const int *type,

@@ -32,10 +32,12 @@ struct TileView {
 // tile lists when the list changed; writes what the pack kernel of lk_step.hip writes.
 // records > 0: the kernel also writes the atom records and species of atoms [0, records) (the
 // atom-record launch's work; the kernel itself reads x and type, not the records).
+// forward_fp: F' also goes to the owned rows' ghost images through the handle's ghost map (the
+// one-rank forward exchange); false when the engine exchanges rho between the passes.
 bool tile_step_eligible(const Handle &h, int num_rows, int maxneighs);
 hipError_t launch_step_tiles(Handle &h, hipStream_t s, const double *x, const int *type,
                              const int *ilist, const int *numneigh, const int *neighbors,
                              long stride, int num_rows, int maxneighs, int nlocal, int nghost,
-                             EamArgs<double> &a, int records = 0);
+                             EamArgs<double> &a, int records = 0, bool forward_fp = true);
 
 }  // namespace lk

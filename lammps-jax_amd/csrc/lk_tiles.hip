@@ -775,7 +775,7 @@ bool tile_step_eligible(const Handle &h, int num_rows, int maxneighs)
 hipError_t launch_step_tiles(Handle &h, hipStream_t s, const double *x, const int *type,
                              const int *ilist, const int *numneigh, const int *neighbors,
                              long stride, int num_rows, int maxneighs, int nlocal, int nghost,
-                             EamArgs<double> &a, int records)
+                             EamArgs<double> &a, int records, bool forward_fp)
 {
   Handle::IncKey key;
   key.epoch = h.list_epoch;
@@ -808,7 +808,7 @@ hipError_t launch_step_tiles(Handle &h, hipStream_t s, const double *x, const in
   p.senders = h.d_senders;
   p.receivers = h.d_receivers;
   p.mask = h.d_mask;
-  p.ghost_off = nghost > 0 ? h.d_ghost_off : nullptr;
+  p.ghost_off = forward_fp && nghost > 0 ? h.d_ghost_off : nullptr;
   p.ghost_list = h.d_ghost_list;
   p.atoms_out = records > 0 ? static_cast<Atom4<double> *>(h.d_atoms) : nullptr;
   p.species_out = h.d_species;

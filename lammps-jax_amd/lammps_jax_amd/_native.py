@@ -37,7 +37,7 @@ EXPORTED = (
     "lk_bundle_contract", "lk_bundle_model", "lk_bundle_unit_style", "lk_pack_edges_noalloc",
     "lk_setfl_parse", "lk_bundle_element", "lk_model_density", "lk_model_comm", "lk_model_force",
     "lk_comm_pack_forward", "lk_comm_unpack_forward", "lk_comm_pack_reverse",
-    "lk_comm_unpack_reverse", "lk_tile_lists",
+    "lk_comm_unpack_reverse", "lk_tile_lists", "lk_pack_density",
 )
 
 
@@ -177,6 +177,9 @@ def load() -> ctypes.CDLL:
     lib.lk_bundle_element.restype = ip
     lib.lk_model_density.argtypes = [vp, vp, ip, ip]
     lib.lk_model_density.restype = ip
+    lib.lk_pack_density.argtypes = [vp, vp, vp, vp, ip, vp, vp, vp, ctypes.c_long, ip, ip, ip,
+                                    ip, ip]
+    lib.lk_pack_density.restype = ip
     lib.lk_model_comm.argtypes = [vp, ip, pp(ip), pp(vp), pp(ip)]
     lib.lk_model_comm.restype = ip
     lib.lk_model_force.argtypes = [vp, vp, ip, ip, ip, dp, vp]

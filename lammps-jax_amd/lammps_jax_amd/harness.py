@@ -28,6 +28,21 @@ class StepFns(ctypes.Structure):
                 ("set_list_epoch", ctypes.c_void_p)]
 
 
+class SplitFns(ctypes.Structure):
+    """The library entry points lkh_run_split_steps calls."""
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "pack_density", "model_comm", "pack_forward", "unpack_forward", "pack_reverse",
+        "unpack_reverse", "model_force", "step_result", "set_list_epoch")]
+
+
+class Swaps(ctypes.Structure):
+    """The ghost swaps of the split loop: device send lists, first ghost rows, counts, and the
+    device buffer."""
+    _fields_ = [("n", ctypes.c_int), ("sendlist", ctypes.POINTER(ctypes.c_void_p)),
+                ("first", ctypes.POINTER(ctypes.c_int)), ("count", ctypes.POINTER(ctypes.c_int)),
+                ("buf", ctypes.c_void_p)]
+
+
 class StepArgs(ctypes.Structure):
     """lk_pack_compute's arguments past the handle and stream, as the engine passes them."""
     _fields_ = [("x", ctypes.c_void_p), ("type", ctypes.c_void_p), ("nall", ctypes.c_int),
@@ -76,6 +91,10 @@ def _load() -> ctypes.CDLL:
                                   ip, ctypes.POINTER(lp), ctypes.POINTER(lp),
                                   ctypes.POINTER(ip), vp, vp]
     lib.lkh_run_steps.restype = ip
+    lib.lkh_run_split_steps.argtypes = [ctypes.POINTER(SplitFns), vp, vp, ctypes.POINTER(StepArgs),
+                                        ctypes.POINTER(Swaps), ip, ip, ctypes.POINTER(lp),
+                                        ctypes.POINTER(lp), ctypes.POINTER(ip), vp, vp]
+    lib.lkh_run_split_steps.restype = ip
     lib.lkh_swap_sendlist.argtypes = [vp, ip]
     lib.lkh_swap_sendlist.restype = ctypes.POINTER(ctypes.c_int)
     _lib = lib

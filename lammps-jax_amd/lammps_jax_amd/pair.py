@@ -436,20 +436,28 @@ class PairJax:
                           lst["maxneighs"], nlocal)
         self.h.compute(st, nlocal, nghost, flags, self.scale, self.f.data_ptr())
 
-    def compute_split(self, comm, eflag=True, vflag=True) -> StepInfo:
+    def compute_split(self, comm, eflag=True, vflag=True, fused=False) -> StepInfo:
         """The model pass with the engine's exchanges between its phases (lk_model_density,
         then every exchange lk_model_comm names through `comm` (a DeviceComm or anything with
-        forward(rows, width) / reverse(rows, width)), then lk_model_force) after the pack."""
+        forward(rows, width) / reverse(rows, width)), then lk_model_force) after the pack.
+        fused: the pack and the density pass as one call (lk_pack_density) instead of
+        lk_pack_atoms, lk_pack_edges, lk_model_density."""
         s, lst = self.system, self.system.list
         st = self.stream()
         lib, h = self.h.lib, self.h.ptr
         self.f.zero_()
         flags = (N.LK_ENERGY if eflag else 0) | (N.LK_VIRIAL if vflag else 0)
-        self.h.pack_atoms(st, self.x.data_ptr(), self.type.data_ptr(), s.nall)
-        self.h.pack_edges(st, self.x.data_ptr(), self.ilist.data_ptr(), self.numneigh.data_ptr(),
-                          self.neighbors.data_ptr(), lst["stride"], lst["inum"], lst["gnum"],
-                          lst["maxneighs"], s.nlocal)
-        self.h.check(lib.lk_model_density(h, st, s.nlocal, s.nghost))
+        if fused:
+            self.h.check(lib.lk_pack_density(
+                h, st, self.x.data_ptr(), self.type.data_ptr(), s.nall, self.ilist.data_ptr(),
+                self.numneigh.data_ptr(), self.neighbors.data_ptr(), lst["stride"], lst["inum"],
+                lst["gnum"], lst["maxneighs"], s.nlocal, s.nghost))
+        else:
+            self.h.pack_atoms(st, self.x.data_ptr(), self.type.data_ptr(), s.nall)
+            self.h.pack_edges(st, self.x.data_ptr(), self.ilist.data_ptr(),
+                              self.numneigh.data_ptr(), self.neighbors.data_ptr(), lst["stride"],
+                              lst["inum"], lst["gnum"], lst["maxneighs"], s.nlocal)
+            self.h.check(lib.lk_model_density(h, st, s.nlocal, s.nghost))
         site = 0
         forward, rows, width = ctypes.c_int(), ctypes.c_void_p(), ctypes.c_int()
         while lib.lk_model_comm(h, site, ctypes.byref(forward), ctypes.byref(rows),

@@ -22,7 +22,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from lk_testutil import assert_energy, assert_forces, assert_virial, rel_err
+from lk_testutil import assert_energy, assert_forces, assert_virial, canonical, rel_err
 from lammps_jax_amd import _native as N
 from lammps_jax_amd import harness, systems
 from lammps_jax_amd.pair import DeviceComm, PairJax
@@ -95,12 +95,15 @@ def test_comm_buffers_move_rows_exactly(gpu, precision, width):
                                     buf.data_ptr(), None) == N.LK_ERR_ARGUMENT
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("precision", [8, 4])
 @pytest.mark.parametrize("accumulation,kind,mode", [
     ("onesided", harness.LIST_FULL, O.ONESIDED),
     ("half", harness.LIST_HALF, O.HALF),
 ])
-def test_split_pass_with_engine_exchange(gpu, precision, accumulation, kind, mode):
+def test_split_pass_with_engine_exchange(gpu, precision, accumulation, kind, mode, fused):
+    """fused: the pack and the density pass as one call (lk_pack_density; for the one-sided
+    scheme the fused pack kernel, over tile lists in float64) instead of three."""
     wl, sysm, lst, pj = _pair(precision, accumulation, kind)
     # the handle has no ghost map for this step: the engine's exchange is the only path
     pj.h.set_ghost_map(sysm.nlocal, np.zeros(0, np.int32))
@@ -112,9 +115,9 @@ def test_split_pass_with_engine_exchange(gpu, precision, accumulation, kind, mod
         sites.append(("forward" if fwd.value else "reverse", width.value))
     assert sites == ([("reverse", 1), ("forward", 1)] if accumulation == "half"
                      else [("forward", 1)])
-    print(f"split case {accumulation} precision={precision} nall={sysm.nall} "
+    print(f"split case {accumulation} precision={precision} fused={fused} nall={sysm.nall} "
           f"swaps={len(comm.swaps)}", flush=True)
-    info = pj.compute_split(comm)
+    info = pj.compute_split(comm, fused=fused)
     f = pj.forces()
     pos, sp = O.pack_atoms(sysm.x, sysm.type, sysm.nall, pj.max_atoms, precision)
     s, r, m, _, _ = O.pack_neighbors(sysm.x, lst, max_atoms=pj.max_atoms, max_edges=pj.max_edges,
@@ -138,6 +141,56 @@ def test_split_pass_with_engine_exchange(gpu, precision, accumulation, kind, mod
     np.testing.assert_array_equal(rho[nl:nall], rho[sysm.ghost_owner])
     np.testing.assert_array_equal(fp[nl:nall], fp[sysm.ghost_owner])
     assert rel_err(fp[:nall], ref["fp"][:nall]) < tol
+    # the packed arrays the step leaves, and a second step bitwise the same
+    ds, dr_, dm = pj.edges()
+    np.testing.assert_array_equal(canonical(ds, dr_, dm), canonical(s, r, m))
+    info2 = pj.compute_split(comm, fused=fused)
+    np.testing.assert_array_equal(pj.forces(), f)
+    assert info2.energy == info.energy and list(info2.virial) == list(info.virial)
+    assert info2.edge_count == info.edge_count
+
+
+def test_fused_split_steps_interleave_with_fused_steps(gpu):
+    """lk_pack_density leaves the pack state for its force pass to finish (tail reset, counts);
+    fused full steps (lk_pack_compute), fused split steps and split steps through the three
+    calls can follow each other in any order. The fused forms give the same results bit for bit
+    (the same pack and density kernel; a ghost row's F' is its owner's either way); the three
+    calls' density pass groups each row's partial sums differently, so they agree to rounding.
+    Then positions that keep fewer pairs: the slots past the new count return to padding."""
+    wl, sysm, lst, pj = _pair(8, "onesided", harness.LIST_FULL, cells=(4, 4, 4), seed=6)
+    comm = DeviceComm(pj, sysm)
+    ref_info = pj.compute(fused=True)
+    ref_f = pj.forces().copy()
+    ref_edges = canonical(*pj.edges())
+    for label, run in (("fused split", lambda: pj.compute_split(comm, fused=True)),
+                       ("fused", lambda: pj.compute(fused=True)),
+                       ("fused split", lambda: pj.compute_split(comm, fused=True)),
+                       ("split", lambda: pj.compute_split(comm, fused=False)),
+                       ("fused split", lambda: pj.compute_split(comm, fused=True))):
+        print(f"interleave step: {label}", flush=True)
+        info = run()
+        assert info.edge_count == ref_info.edge_count and info.edge_overflow == 0, label
+        if label == "split":
+            assert rel_err(pj.forces(), ref_f) < 1e-13
+            assert abs(info.energy - ref_info.energy) <= 1e-13 * abs(ref_info.energy)
+        else:
+            np.testing.assert_array_equal(pj.forces(), ref_f)
+            assert info.energy == ref_info.energy, label
+        ds, dr_, dm = pj.edges()
+        np.testing.assert_array_equal(canonical(ds, dr_, dm), ref_edges)
+        assert not dm[info.edge_count:].any()
+    # expanded positions (the same list, fewer kept pairs): the fused split step's force pass
+    # returns the slots past the new count to the padding
+    import torch
+
+    pj.x = torch.from_numpy(sysm.x * 1.04).to(pj.device)
+    comm = DeviceComm(pj, sysm)
+    info = pj.compute_split(comm, fused=True)
+    assert 0 < info.edge_count < ref_info.edge_count
+    ds, dr_, dm = pj.edges()
+    c = info.edge_count
+    assert np.all(dm[:c] == 1) and not dm[c:].any()
+    assert np.all(ds[c:] == pj.max_atoms) and np.all(dr_[c:] == pj.max_atoms)
 
 
 def test_split_pass_state_and_scheme_errors(gpu):

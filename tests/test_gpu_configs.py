@@ -169,12 +169,14 @@ def test_neighbor_matrix_layout_at_full_size(gpu):
     assert np.all(f[sysm.nlocal:sysm.nall] == 0.0)
 
 
-@pytest.mark.parametrize("name", ["eam_alloy_8k", "eam_alloy_131k"])
-def test_split_pass_at_full_size(gpu, name):
+@pytest.mark.parametrize("name,fused", [("eam_alloy_8k", False), ("eam_alloy_131k", False),
+                                        ("eam_alloy_131k", True)])
+def test_split_pass_at_full_size(gpu, name, fused):
     """The model pass split at its exchanges (lk_model_density, the engine's exchanges through
     the lk_comm_* buffer calls over the harness's ghost swaps, lk_model_force) at full size, with
     no ghost map on the handle: the half scheme of the 8k workload and the one-sided scheme of the
-    131k workload against the oracle."""
+    131k workload against the oracle. fused: lk_pack_density (the tile-list pack and density of
+    the fused step, stopping at the exchange) in place of the pack calls and the density pass."""
     from lammps_jax_amd.pair import DeviceComm
 
     wl = systems.make_workload(name)
@@ -182,8 +184,9 @@ def test_split_pass_at_full_size(gpu, name):
     lst = sysm.build_list(wl.cutoff + wl.skin, kind=wl.list_kind)
     pj = PairJax.for_workload(wl, sysm, fused=False)
     pj.h.set_ghost_map(sysm.nlocal, np.zeros(0, np.int32))
-    print(f"full-size split case {name}: nlocal={sysm.nlocal} nghost={sysm.nghost}", flush=True)
-    info = pj.compute_split(DeviceComm(pj, sysm))
+    print(f"full-size split case {name} fused={fused}: nlocal={sysm.nlocal} "
+          f"nghost={sysm.nghost}", flush=True)
+    info = pj.compute_split(DeviceComm(pj, sysm), fused=fused)
     f = pj.forces().copy()
     ref, _ = _oracle(wl, sysm, lst, pj)
     assert info.edge_overflow == 0
@@ -197,3 +200,11 @@ def test_split_pass_at_full_size(gpu, name):
     rho, fp = pj.model_rows()
     assert rel_err(rho[:sysm.nlocal], ref["rho"][:sysm.nlocal]) < 1e-13
     assert rel_err(fp[:sysm.nall], ref["fp"][:sysm.nall]) < 1e-13
+    if fused:
+        # the pack ran in the fused kernel over the tile lists: the packed set, and every tile
+        # staged its union
+        _, (s, r, m, count, _) = _oracle(wl, sysm, lst, pj)
+        assert info.edge_count == count
+        np.testing.assert_array_equal(canonical(*pj.edges()), canonical(s, r, m))
+        u = pj.tile_unions()
+        assert len(u) > 0 and np.all(u >= 0)
