@@ -46,9 +46,15 @@ using IncSortConfig = rocprim::radix_sort_config<
 constexpr int kScanThreads = 1024;
 constexpr int kScanItems = 4;
 constexpr int kScanChunk = kScanThreads * kScanItems;
-constexpr int kGroup = 16;                     // lanes per atom in the row sweeps
 constexpr int kRowBlock = 1024;                // threads per row-sweep block
-constexpr int kRowAtoms = kRowBlock / kGroup;  // 64 atoms per block = one partial tile
+constexpr int kRowAtoms = 64;                  // atoms per partial tile (energy, virial slots)
+// Lanes per atom in the row sweeps: a block holds kRowBlock / G atoms, kRowBlock / G / kRowAtoms
+// partial tiles. Sixteen lanes for float64, eight for float32, whose lists of 50 to 100 entries
+// leave fewer lanes idle that way (C4 force sweep 498 -> 404 us, density 239 -> 216 us, C5 LJ
+// sweep 146 -> 122 us); the float64 steps of the small systems lost with eight (C2 0.097 ->
+// 0.104 ms/step).
+template <typename S>
+constexpr int kLanesPerAtom = sizeof(S) == 4 ? 8 : 16;
 constexpr int kIncLds = 7680;                  // 120 KB table window
 constexpr int kIncDensLds = 4096;              // 64 KB density-table window (two blocks per CU)
 // Force sweep two blocks per CU with the density-sized window: fp32 (fp64 would spill).
@@ -593,11 +599,11 @@ __global__ __launch_bounds__(256) void k_inc_list_fold_sorted(ListArgs L, int na
   if (have && gl == 0) L.len[atom] = out + kept;
 }
 
-template <typename T>
+template <int G, typename T>
 __device__ __forceinline__ T group_sum(T v)
 {
 #pragma unroll
-  for (int m = kGroup / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  for (int m = G / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
   return v;
 }
 
@@ -615,7 +621,7 @@ struct TwoSided {
   const double *x;      // engine positions for the virial
   const int *ghost_off;
   const int *ghost_list;
-  int nblk;             // 64-atom tiles over nall
+  int nblk;             // 64-atom partial tiles over nall
   const uint32_t *inc_bit;  // list-built entries: address of the slot's validity bit
   const uint32_t *bits;     // the pack's validity bits of this step
   double cutsq_pack;        // the pack's filter: rsq <= cutsq in float64 (cpp:91)
@@ -710,6 +716,7 @@ __device__ __forceinline__ bool slot_kept(const TwoSided &t, int q, S r2, S dx, 
 // its own row's record instead (cached), so no branch surrounds a load. (The density and LJ
 // sweeps measured slower with it, also at eight waves per SIMD: C4 density 404 -> 464 us, C5 LJ
 // 181 -> 183 us; they take two entries at a time instead.)
+template <int G>
 struct IncCursor {
   uint32_t v = 0;
   int q = 0;  // the entry v was loaded from
@@ -726,7 +733,7 @@ struct IncCursor {
   __device__ __forceinline__ void advance(const TwoSided &t, int k)
   {
     asm volatile("" ::: "memory");  // keep these loads behind the current entry's gathers
-    load(t, min(b + k + kGroup, last));
+    load(t, min(b + k + G, last));
   }
 };
 
@@ -750,18 +757,20 @@ __device__ __forceinline__ S geometry(const Atom4<S> &xa, const Atom4<S> &xo, S 
 // Density per row (eam.py:298-314); PAIR: also the row's pair energy (the edge-force path, whose
 // edge sweep keeps no per-row energy). Without it the window holds the density tables only, so
 // two blocks fit on a CU; the force sweep then sums the pair energy.
-template <typename S, bool HALF, bool PAIR>
+template <typename S, bool HALF, bool PAIR, int G>
 __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, TwoSided t,
                                                                S *__restrict__ rho_part,
                                                                S *__restrict__ epair)
 {
   constexpr int kLds = PAIR ? kIncLds : kIncDensLds;
+  constexpr int APB = kRowBlock / G;  // atoms per block
   __shared__ LdsEntry<S> lds[kLds];
   fused_tail_reset(t.pack);
   const Window<S> win = fill_window<S>(lds, kLds, m, PAIR ? m.n_rtab : m.n_el);
-  const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
-  for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
-    const int a = blk * kRowAtoms + g;
+  const int g = threadIdx.x / G, gl = threadIdx.x % G;
+  const int nsb = (t.nall + APB - 1) / APB;
+  for (int blk = blockIdx.x; blk < nsb; blk += gridDim.x) {
+    const int a = blk * APB + g;
     S rho = S(0), ep = S(0);
     if (a < t.nall) {
       const Atom4<S> xa = m.atoms[a];
@@ -769,7 +778,7 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
       const int za = clamp_species(static_cast<int>(xa.w), m.n_el);
       const int b = inc_off(t.loc, t.part, a);
       const int L = HALF ? inc_off(t.loc, t.part, a + 1) - b : inc_len(t, a, b);  // half: no folds
-      // Two entries per lane at a time (k and k + 16): both entries load together, then both
+      // Two entries per lane at a time (k and k + G): both entries load together, then both
       // records, so a pair of entries costs two memory round trips; a skipped or missing entry
       // gathers the row's own record.
       auto dens = [&](uint32_t v, int q, const Atom4<S> &xo) {
@@ -793,9 +802,9 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
           ep += HALF ? phi : S(0.5) * phi;  // half: the sender carries both halves
         }
       };
-      for (int k = gl; k < L; k += 2 * kGroup) {
-        const bool two = k + kGroup < L;
-        const int q1 = b + k, q2 = b + (two ? k + kGroup : k);
+      for (int k = gl; k < L; k += 2 * G) {
+        const bool two = k + G < L;
+        const int q1 = b + k, q2 = b + (two ? k + G : k);
         uint32_t v1 = static_cast<uint32_t>(t.inc[q1]);
         uint32_t v2 = static_cast<uint32_t>(t.inc[q2]);
         // both entries in flight before either is used: without this the compiler moves the
@@ -809,8 +818,8 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
         if (two) dens(v2, q2, x2);
       }
     }
-    rho = group_sum(rho);
-    if (PAIR) ep = group_sum(ep);
+    rho = group_sum<G>(rho);
+    if (PAIR) ep = group_sum<G>(ep);
     if (gl == 0 && a < t.nall) {
       rho_part[a] = rho;
       if (PAIR) epair[a] = ep;
@@ -858,13 +867,13 @@ __global__ __launch_bounds__(kWave) void k_eam_embed_inc(EamArgs<S> m, TwoSided 
   if (threadIdx.x == 0 && tile < t.nblk) m.partials[8L * tile] = esum;
 }
 
-// Per-row f.r virial of the total f after the add, summed over the 64 rows of the tile in a fixed
-// order by the first wave, which alone stores partials (finalize_last_block's contract).
-template <bool VIRIAL>
+// Per-row f.r virial of the total f after the add, summed over the 64 rows of each partial tile
+// in a fixed order by the first wave, which alone stores partials (finalize_last_block's
+// contract). vt is [6][APB], one column per atom of the block.
+template <bool VIRIAL, int APB>
 __device__ __forceinline__ void add_row_force(double *f, const double *x, int a, int nadd,
                                               int nall, int fdotr, double scale, double fx,
-                                              double fy, double fz, double (*vt)[kRowAtoms],
-                                              int g)
+                                              double fy, double fz, double (*vt)[APB], int g)
 {
   double w[6] = {0, 0, 0, 0, 0, 0};
   if (a < nall) {
@@ -892,34 +901,43 @@ __device__ __forceinline__ void add_row_force(double *f, const double *x, int a,
     for (int c = 0; c < 6; ++c) vt[c][g] = w[c];
 }
 
-template <bool VIRIAL>
-__device__ __forceinline__ void store_tile_virial(double *partials, int blk,
-                                                  double (*vt)[kRowAtoms], double e_tile,
-                                                  bool write_energy, double e_pair = 0.0)
+// The partials of the block's tiles, from columns [64 q, 64 q + 64) of vt and et for its tile
+// q (the atoms blk * APB + 64 q ...): called by the first wave only, after a barrier. The pair
+// energy goes to slot 7; write_energy: et holds the rows' whole energy, into slot 0.
+template <bool VIRIAL, int APB>
+__device__ __forceinline__ void store_block_partials(double *partials, int blk, int nall,
+                                                     double (*vt)[APB], const double *et,
+                                                     bool write_energy)
 {
-  // called by the first wave only, after a barrier
   const int lane = threadIdx.x;
-  if (VIRIAL) {
-    for (int c = 0; c < 6; ++c) {
-      const double v = wave_sum(vt[c][lane]);
-      if (lane == 0) partials[8L * blk + 1 + c] = v;
+#pragma unroll
+  for (int q = 0; q < APB / kRowAtoms; ++q) {
+    const int tile = blk * (APB / kRowAtoms) + q;
+    if (tile * kRowAtoms >= nall) break;  // uniform over the wave
+    if (VIRIAL) {
+      for (int c = 0; c < 6; ++c) {
+        const double v = wave_sum(vt[c][q * kRowAtoms + lane]);
+        if (lane == 0) partials[8L * tile + 1 + c] = v;
+      }
     }
-  }
-  if (lane == 0) {
-    partials[8L * blk + 7] = e_pair;
-    if (write_energy) partials[8L * blk] = e_tile;
+    const double e = wave_sum(et[q * kRowAtoms + lane]);
+    if (lane == 0) {
+      partials[8L * tile + 7] = write_energy ? 0.0 : e;
+      if (write_energy) partials[8L * tile] = e;
+    }
   }
 }
 
 // Force sweep (eam.py:336-409 closed form; export.py:197-204 autodiff convention), and the pair
 // energy of the counted rows (eam.py:300-307) from the phi it evaluates anyway: on the sender,
 // both halves in the half scheme, half per directed edge in the plain one.
-template <typename S, bool HALF, bool VIRIAL, bool BITS>
+template <typename S, bool HALF, bool VIRIAL, bool BITS, int G>
 __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const TwoSided &t,
                                                    LdsEntry<S> *lds, int lds_entries)
 {
-  __shared__ double vt[6][kRowAtoms];
-  __shared__ double et[kRowAtoms];
+  constexpr int APB = kRowBlock / G;  // atoms per block
+  __shared__ double vt[6][APB];
+  __shared__ double et[APB];
   // float32: the window holds Hermite rows (more nodes per byte); float64: (f, d) entries
   Window<S> win{};
   HWindow hw{};
@@ -927,10 +945,11 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
     hw = fill_hwindow(reinterpret_cast<float *>(lds), lds_entries * 4, m.htab, m.htab_w, m.nr);
   else
     win = fill_window<S>(lds, lds_entries, m, m.n_rtab);
-  const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
+  const int g = threadIdx.x / G, gl = threadIdx.x % G;
   const int erows = energy_rows(t, HALF);
-  for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
-    const int a = blk * kRowAtoms + g;
+  const int nsb = (t.nall + APB - 1) / APB;
+  for (int blk = blockIdx.x; blk < nsb; blk += gridDim.x) {
+    const int a = blk * APB + g;
     S fx = S(0), fy = S(0), fz = S(0), ep = S(0);
     if (a < t.nall) {
       const Atom4<S> xa = m.atoms[a];
@@ -1044,29 +1063,29 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
         fy += coef * dy;
         fz += coef * dz;
       };
-      // float32: entries k and k + 16 of this lane at a time: both gathers go out together,
+      // float32: entries k and k + G of this lane at a time: both gathers go out together,
       // then the next pair's entries (clamped to the list's last entry, so every load is
       // unconditional and waiting for the gathers never waits for them), then both edges are
       // computed (C4 force sweep 750 -> 739 us). float64 takes one entry at a time with the next
       // in flight (two at a time measured 2% slower there, at 97 VGPRs and four waves per SIMD).
       if constexpr (sizeof(S) == 8) {
-        IncCursor cur(t, b, L, gl);
-        for (int k = gl; k < L; k += kGroup) {
+        IncCursor<G> cur(t, b, L, gl);
+        for (int k = gl; k < L; k += G) {
           const Gathered e = gather(cur.v, cur.q, true);
           cur.advance(t, k);
           edge(e);
         }
       } else if (gl < L) {
         const int last = b + L - 1;
-        int q1 = b + gl, q2 = min(b + gl + kGroup, last);
+        int q1 = b + gl, q2 = min(b + gl + G, last);
         uint32_t v1 = static_cast<uint32_t>(t.inc[q1]);
         uint32_t v2 = static_cast<uint32_t>(t.inc[q2]);
-        for (int k = gl; k < L; k += 2 * kGroup) {
+        for (int k = gl; k < L; k += 2 * G) {
           const Gathered e1 = gather(v1, q1, true);
-          const Gathered e2 = gather(v2, q2, k + kGroup < L);
+          const Gathered e2 = gather(v2, q2, k + G < L);
           asm volatile("" ::: "memory");  // keep the next entries' loads behind the gathers
-          q1 = min(b + k + 2 * kGroup, last);
-          q2 = min(b + k + 3 * kGroup, last);
+          q1 = min(b + k + 2 * G, last);
+          q2 = min(b + k + 3 * G, last);
           v1 = static_cast<uint32_t>(t.inc[q1]);
           v2 = static_cast<uint32_t>(t.inc[q2]);
           edge(e1);
@@ -1074,19 +1093,19 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
         }
       }
     }
-    fx = group_sum(fx);
-    fy = group_sum(fy);
-    fz = group_sum(fz);
-    ep = group_sum(ep);
+    fx = group_sum<G>(fx);
+    fy = group_sum<G>(fy);
+    fz = group_sum<G>(fz);
+    ep = group_sum<G>(ep);
     if (gl == 0) {
-      add_row_force<VIRIAL>(m.f, t.x, a, t.nadd, t.nall, t.fdotr, m.scale,
-                            static_cast<double>(fx), static_cast<double>(fy),
-                            static_cast<double>(fz), vt, g);
+      add_row_force<VIRIAL, APB>(m.f, t.x, a, t.nadd, t.nall, t.fdotr, m.scale,
+                                 static_cast<double>(fx), static_cast<double>(fy),
+                                 static_cast<double>(fz), vt, g);
       et[g] = a < erows ? static_cast<double>(ep) : 0.0;
     }
     __syncthreads();
-    if (threadIdx.x < kWave && blk * kRowAtoms < t.nall)
-      store_tile_virial<VIRIAL>(m.partials, blk, vt, 0.0, false, wave_sum(et[threadIdx.x]));
+    if (threadIdx.x < kWave)
+      store_block_partials<VIRIAL, APB>(m.partials, blk, t.nall, vt, et, false);
     __syncthreads();
   }
   finalize_last_block(m.partials, t.nblk, m.scale, 1.0, m.flags, m.result, m.done,
@@ -1094,22 +1113,22 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
 }
 
 // One block per CU: the 120 KB table window (all of a 2000-node r-grid of two elements).
-template <typename S, bool HALF, bool VIRIAL, bool BITS>
+template <typename S, bool HALF, bool VIRIAL, bool BITS, int G>
 __global__ __launch_bounds__(kRowBlock) void k_eam_force_inc(EamArgs<S> m, TwoSided t)
 {
   __shared__ LdsEntry<S> lds[kIncLds];
-  eam_force_inc_rows<S, HALF, VIRIAL, BITS>(m, t, lds, kIncLds);
+  eam_force_inc_rows<S, HALF, VIRIAL, BITS, G>(m, t, lds, kIncLds);
 }
 
 // Two blocks per CU (eight waves per SIMD) with the 64 KB window: twice the gathers in flight for
 // more lookups below the window (L2-resident). The fp32 sweep fits 64 VGPRs without spills
 // (C4 force sweep 814 -> 748 us); the fp64 one would spill.
-template <typename S, bool HALF, bool VIRIAL, bool BITS>
+template <typename S, bool HALF, bool VIRIAL, bool BITS, int G>
 __global__ __launch_bounds__(kRowBlock) __attribute__((amdgpu_waves_per_eu(8))) LK_EIGHT_WAVES
 void k_eam_force_inc_2b(EamArgs<S> m, TwoSided t)
 {
   __shared__ LdsEntry<S> lds[kIncDensLds];
-  eam_force_inc_rows<S, HALF, VIRIAL, BITS>(m, t, lds, kIncDensLds);
+  eam_force_inc_rows<S, HALF, VIRIAL, BITS, G>(m, t, lds, kIncDensLds);
 }
 
 template <typename S>
@@ -1127,19 +1146,21 @@ struct LjModel {
 
 // LJ 12-6 plain (examples/export_model.py:16-50): e per edge on the sender row, g = 2 de/d(r^2) d
 // (times edge_energy_scale) to the sender and minus it to the receiver.
-template <typename S, bool VIRIAL>
+template <typename S, bool VIRIAL, int G>
 __global__ __launch_bounds__(kRowBlock) __attribute__((amdgpu_waves_per_eu(8))) LK_EIGHT_WAVES
 void k_lj_inc(LjModel<S> m, TwoSided t)
 {
-  __shared__ double vt[6][kRowAtoms];
-  __shared__ double et[kRowAtoms];
+  constexpr int APB = kRowBlock / G;  // atoms per block
+  __shared__ double vt[6][APB];
+  __shared__ double et[APB];
   __shared__ double scratch[7 * kRowBlock];
   fused_tail_reset(t.pack);
-  const int g = threadIdx.x / kGroup, gl = threadIdx.x % kGroup;
+  const int g = threadIdx.x / G, gl = threadIdx.x % G;
   const int erows = energy_rows(t, false);
   const S tiny = static_cast<S>(1.0e-12);
-  for (int blk = blockIdx.x; blk < t.nblk; blk += gridDim.x) {
-    const int a = blk * kRowAtoms + g;
+  const int nsb = (t.nall + APB - 1) / APB;
+  for (int blk = blockIdx.x; blk < nsb; blk += gridDim.x) {
+    const int a = blk * APB + g;
     S en = S(0), fx = S(0), fy = S(0), fz = S(0);
     if (a < t.nall) {
       const Atom4<S> xa = m.atoms[a];
@@ -1168,11 +1189,11 @@ void k_lj_inc(LjModel<S> m, TwoSided t)
         fy += coef * dy;
         fz += coef * dz;
       };
-      // Two entries per lane at a time (k and k + 16), as in the density sweep: both entries,
+      // Two entries per lane at a time (k and k + G), as in the density sweep: both entries,
       // then both records (an uncounted or missing entry gathers the row's own record).
-      for (int k = gl; k < L; k += 2 * kGroup) {
-        const bool two = k + kGroup < L;
-        const int q1 = b + k, q2 = b + (two ? k + kGroup : k);
+      for (int k = gl; k < L; k += 2 * G) {
+        const bool two = k + G < L;
+        const int q1 = b + k, q2 = b + (two ? k + G : k);
         const uint32_t v1 = static_cast<uint32_t>(t.inc[q1]);
         const uint32_t v2 = static_cast<uint32_t>(t.inc[q2]);
         const int w1 = ends(v1), w2 = two ? ends(v2) : 0;
@@ -1182,21 +1203,19 @@ void k_lj_inc(LjModel<S> m, TwoSided t)
         pair(v2, q2, w2, x2);
       }
     }
-    en = group_sum(en);
-    fx = group_sum(fx);
-    fy = group_sum(fy);
-    fz = group_sum(fz);
+    en = group_sum<G>(en);
+    fx = group_sum<G>(fx);
+    fy = group_sum<G>(fy);
+    fz = group_sum<G>(fz);
     if (gl == 0) {
       et[g] = a < erows ? static_cast<double>(en) : 0.0;
-      add_row_force<VIRIAL>(m.f, t.x, a, t.nadd, t.nall, t.fdotr, m.scale,
-                            static_cast<double>(fx), static_cast<double>(fy),
-                            static_cast<double>(fz), vt, g);
+      add_row_force<VIRIAL, APB>(m.f, t.x, a, t.nadd, t.nall, t.fdotr, m.scale,
+                                 static_cast<double>(fx), static_cast<double>(fy),
+                                 static_cast<double>(fz), vt, g);
     }
     __syncthreads();
-    if (threadIdx.x < kWave && blk * kRowAtoms < t.nall) {
-      const double e_tile = wave_sum(et[threadIdx.x]);
-      store_tile_virial<VIRIAL>(m.partials, blk, vt, e_tile, true);
-    }
+    if (threadIdx.x < kWave)
+      store_block_partials<VIRIAL, APB>(m.partials, blk, t.nall, vt, et, true);
     __syncthreads();
   }
   finalize_last_block(m.partials, t.nblk, m.scale, 1.0, m.flags, m.result, m.done, scratch,
@@ -1466,11 +1485,12 @@ static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost
     t.ghost_off = nullptr;
     t.owned_rows_only = 1;
   }
-  const int nblk = t.nblk > 0 ? t.nblk : 1;
-  const int grid = grid_for(h, nblk, 1, 1);
+  constexpr int G = kLanesPerAtom<S>;
+  const int nsb = t.nall > 0 ? (t.nall + kRowBlock / G - 1) / (kRowBlock / G) : 1;
+  const int grid = grid_for(h, nsb, 1, 1);
   if (t.nblk > 0 && phase != kPhaseForce) {
     StageTimer timer(h, s, "eam_density");
-    hipLaunchKernelGGL((k_eam_density_inc<S, HALF, false>), dim3(grid_for(h, nblk, 1, 2)),
+    hipLaunchKernelGGL((k_eam_density_inc<S, HALF, false, G>), dim3(grid_for(h, nsb, 1, 2)),
                        dim3(kRowBlock), 0, s, m, t, rho_part, static_cast<S *>(nullptr));
   }
   if (phase == kPhaseDensity) return hipGetLastError();
@@ -1487,24 +1507,24 @@ static hipError_t eam_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost
   StageTimer timer(h, s, "eam_force");
   const bool vir = (flags & LK_VIRIAL) != 0;
   if constexpr (kForceTwoBlocks<S>) {
-    const int grid2 = grid_for(h, nblk, 1, 2);
+    const int grid2 = grid_for(h, nsb, 1, 2);
     if (vir && t.inc_bit)
-      hipLaunchKernelGGL((k_eam_force_inc_2b<S, HALF, true, true>), dim3(grid2), dim3(kRowBlock), 0, s, m, t);
+      hipLaunchKernelGGL((k_eam_force_inc_2b<S, HALF, true, true, G>), dim3(grid2), dim3(kRowBlock), 0, s, m, t);
     else if (vir)
-      hipLaunchKernelGGL((k_eam_force_inc_2b<S, HALF, true, false>), dim3(grid2), dim3(kRowBlock), 0, s, m, t);
+      hipLaunchKernelGGL((k_eam_force_inc_2b<S, HALF, true, false, G>), dim3(grid2), dim3(kRowBlock), 0, s, m, t);
     else if (t.inc_bit)
-      hipLaunchKernelGGL((k_eam_force_inc_2b<S, HALF, false, true>), dim3(grid2), dim3(kRowBlock), 0, s, m, t);
+      hipLaunchKernelGGL((k_eam_force_inc_2b<S, HALF, false, true, G>), dim3(grid2), dim3(kRowBlock), 0, s, m, t);
     else
-      hipLaunchKernelGGL((k_eam_force_inc_2b<S, HALF, false, false>), dim3(grid2), dim3(kRowBlock), 0, s, m, t);
+      hipLaunchKernelGGL((k_eam_force_inc_2b<S, HALF, false, false, G>), dim3(grid2), dim3(kRowBlock), 0, s, m, t);
   } else {
     if (vir && t.inc_bit)
-      hipLaunchKernelGGL((k_eam_force_inc<S, HALF, true, true>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+      hipLaunchKernelGGL((k_eam_force_inc<S, HALF, true, true, G>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
     else if (vir)
-      hipLaunchKernelGGL((k_eam_force_inc<S, HALF, true, false>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+      hipLaunchKernelGGL((k_eam_force_inc<S, HALF, true, false, G>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
     else if (t.inc_bit)
-      hipLaunchKernelGGL((k_eam_force_inc<S, HALF, false, true>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+      hipLaunchKernelGGL((k_eam_force_inc<S, HALF, false, true, G>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
     else
-      hipLaunchKernelGGL((k_eam_force_inc<S, HALF, false, false>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+      hipLaunchKernelGGL((k_eam_force_inc<S, HALF, false, false, G>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
   }
   return hipGetLastError();
 }
@@ -1530,12 +1550,14 @@ static hipError_t lj_two_sided(Handle &h, hipStream_t s, int nlocal, int nghost,
   TwoSided t = two_sided_args(h, nlocal, nghost, x);
   use_pack(t, pack);
   if (from_list && h.list_bits_filter) t.inc_bit = h.d_inc_bit;
-  const int grid = grid_for(h, t.nblk > 0 ? t.nblk : 1, 1, 2);
+  constexpr int G = kLanesPerAtom<S>;
+  const int nsb = t.nall > 0 ? (t.nall + kRowBlock / G - 1) / (kRowBlock / G) : 1;
+  const int grid = grid_for(h, nsb, 1, 2);
   StageTimer timer(h, s, "lj_rows");
   if (flags & LK_VIRIAL)
-    hipLaunchKernelGGL((k_lj_inc<S, true>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+    hipLaunchKernelGGL((k_lj_inc<S, true, G>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
   else
-    hipLaunchKernelGGL((k_lj_inc<S, false>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
+    hipLaunchKernelGGL((k_lj_inc<S, false, G>), dim3(grid), dim3(kRowBlock), 0, s, m, t);
   return hipGetLastError();
 }
 
@@ -1807,7 +1829,8 @@ static hipError_t eam_edge_force(Handle &h, hipStream_t s, int nlocal, int nghos
   S *epair = static_cast<S *>(h.d_epair);
   if (t.nblk > 0) {
     StageTimer timer(h, s, "eam_density");
-    hipLaunchKernelGGL((k_eam_density_inc<S, true, true>), dim3(grid_for(h, t.nblk, 1, 1)),
+    hipLaunchKernelGGL((k_eam_density_inc<S, true, true, 16>),
+                       dim3(grid_for(h, (t.nall + kRowBlock / 16 - 1) / (kRowBlock / 16), 1, 1)),
                        dim3(kRowBlock), 0, s, m, t, rho_part, epair);
   }
   if (t.nblk > 0) {
