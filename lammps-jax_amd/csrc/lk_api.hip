@@ -62,7 +62,7 @@ void free_all(Handle &h)
                   h.tl.keys,     h.tl.keys_sorted, h.tl.rows_in, h.tl.order,  h.tl.sort_tmp,
                   h.tl.atom,     h.tl.nn,       h.tl.uni,        h.tl.ucount,   h.tl.lid,
                   h.tl.box,      h.d_sort_keys, h.d_sort_vals,   h.d_sort_tmp,  h.d_sort_rows,
-                  h.d_sort_pre,  h.d_rowmark,   h.d_nonrow,      h.d_htab,      h.tl.ustat};
+                  h.d_sort_pre,  h.d_rowmark,   h.d_nonrow,      h.d_htab,      h.tl.ustat, h.d_dtab};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (h.h_result) (void)hipHostFree(h.h_result);
@@ -429,6 +429,19 @@ int lk_set_eam(lk_handle *w, const lk_eam_tables *t)
     e = hipMemcpy(h.d_ltab, l.data(), nent * 16, hipMemcpyHostToDevice);
   }
   if (e != hipSuccess) return hip_fail(h, e, "hipMemcpy(ltab)");
+  if (S == 8) {
+    // the density tables alone, (f, d) per node and element, for the tile pack's density
+    std::vector<double> dt(static_cast<size_t>(t->nr) * n_el * 2);
+    for (int node = 0; node < t->nr; ++node)
+      for (int z = 0; z < n_el; ++z)
+        for (int c = 0; c < 2; ++c)
+          dt[(static_cast<size_t>(node) * n_el + z) * 2 + c] =
+              r[(static_cast<size_t>(node) * n_rtab + z) * 4 + c];
+    if ((e = hipMalloc(&h.d_dtab, dt.size() * 8)) != hipSuccess)
+      return hip_fail(h, e, "hipMalloc(dtab)");
+    if ((e = hipMemcpy(h.d_dtab, dt.data(), dt.size() * 8, hipMemcpyHostToDevice)) != hipSuccess)
+      return hip_fail(h, e, "hipMemcpy(dtab)");
+  }
   if (S == 4) {
     // the force sweep's Hermite rows: per node (s, d) of each density table, then (f, s, d) of
     // each pair table; s = f(m + 1) - f(m) in float64, the difference the host's c2 and c3 used

@@ -58,6 +58,7 @@ struct EamArgs {
   int max_edges;
   const S *rtab;                 // global rows [nr][n_rtab][4]
   const LdsEntry<S> *ltab;       // LDS source [nr][n_rtab]
+  const double *dtab;            // float64: (f, d) of the density tables [nr][n_el] (tile pack)
   const float *htab;             // float32: Hermite rows [nr][htab_w] (force sweep window)
   int htab_w;
   int n_rtab;
@@ -162,6 +163,15 @@ __device__ __forceinline__ Coef<S> rcoef_split(const Window<S> &w, const EamArgs
   }
   const Coef<S> l = rcoef_lds(w, in ? m : w.lo, tab);
   return Coef<S>{in ? l.c0 : g.c0, in ? l.c1 : g.c1, in ? l.c2 : g.c2, in ? l.c3 : g.c3};
+}
+
+// Density coefficients of interval m of element z from the density-only (f, d) table: 16 bytes
+// per node and element, so the density rows of a 2000-node binary alloy take 64 KB (the
+// node-major table of every r-table takes 160 bytes per node).
+__device__ __forceinline__ Coef<double> dens_coef(const EamArgs<double> &a, int m, int z)
+{
+  const double2 *q = reinterpret_cast<const double2 *>(a.dtab) + static_cast<long>(m) * a.n_el + z;
+  return coef_from(q[0], q[a.n_el]);
 }
 
 // float64 intervals in the Hermite basis: the window holds (f, d) per node, so an interval is
@@ -419,6 +429,7 @@ inline EamArgs<S> eam_args(Handle &h, int nlocal, double scale, double *f)
   a.ltab = static_cast<const LdsEntry<S> *>(h.d_ltab);
   a.htab = h.d_htab;
   a.htab_w = h.htab_w;
+  a.dtab = h.d_dtab;
   a.n_rtab = h.n_rtab;
   a.n_el = h.n_el;
   a.nr = h.nr;

@@ -59,6 +59,7 @@ struct Handle {
   void *d_rtab = nullptr;
   void *d_etab = nullptr;
   void *d_ltab = nullptr;  // LDS source: [nr][n_rtab] 16-byte entries, see lk_eam.hip
+  double *d_dtab = nullptr;  // float64: (f, d) of the density tables, [nr][n_el] (tile pack)
   float *d_htab = nullptr;  // float32 contracts: Hermite rows of the force sweep, [nr][htab_w]
   int htab_w = 0;
   int num_cus = 0;

@@ -408,11 +408,7 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
   __shared__ int scnt[SUB][kWave];
   __shared__ int sbase[SUB];
 
-  // the density coefficient rows are read from memory (no LDS window)
-  Window<double> win;
-  win.lds = nullptr;
-  win.T = a.n_el;
-  win.lo = a.nr;
+  // the density intervals are read from the density-only (f, d) table in memory (no LDS window)
   const int sub = wave_in_block() / W;
   const int wave = wave_in_block() % W;
   const int lane = threadIdx.x & (kWave - 1);
@@ -498,7 +494,7 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
               const double s = dens[k] ? rsq : 1.0;
               const Locator<double> L = locate_mul(s * rsqrt_nr(s), a.inv_dr, a.nr);
               tq[k] = L.t;
-              c[k] = rcoef(win, a, dens[k] ? L.node : 0, usp[u]);
+              c[k] = dens_coef(a, dens[k] ? L.node : 0, usp[u]);
             }
 #pragma unroll
             for (int k = 0; k < 2; ++k) rho = dens[k] ? rho + cvalue(c[k], tq[k]) : rho;
@@ -515,8 +511,7 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
           if (rsq < a.cutsq) {
             const double rr = rsq * rsqrt_nr(rsq);
             const Locator<double> L = locate_mul(rr, a.inv_dr, a.nr);
-            rho += cvalue(rcoef(win, a, L.node, clamp_species(p.type[j] - 1, a.n_el)),
-                          L.t);
+            rho += cvalue(dens_coef(a, L.node, clamp_species(p.type[j] - 1, a.n_el)), L.t);
           }
         }
       }
