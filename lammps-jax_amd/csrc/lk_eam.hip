@@ -93,7 +93,7 @@ __global__ __launch_bounds__(W * TPB * 64) LK_EIGHT_WAVES void k_eam_density_row
         if (i < a.nlocal) e_own = static_cast<double>(F);
       }
       const double esum = wave_sum(e_own);
-      if (lane == 0 && tile * kWave < a.num_rows) a.partials[8L * tile + 0] = esum;
+      if (lane == 0 && tile * kWave < a.num_rows) put_partial(a.partials + 8L * tile + 0, esum);
     }
     __syncthreads();
   }
@@ -341,13 +341,13 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
       }
     }
     __syncthreads();
-    // The block's first wave stores the partials of the group's tiles (the only wave that
-    // writes partials, see finalize_last_block); tpart is next written after the next barrier.
+    // The block's first wave stores the partials of the group's tiles; tpart is next written
+    // after the next barrier.
     if (threadIdx.x < TPB * 7) {
       const int q = threadIdx.x / 7, c = threadIdx.x % 7;
       const int t = gw.g * TPB + q;
       if (t * kWave < a.num_rows && (c == 0 || VIRIAL))
-        a.partials[8L * t + (c == 0 ? 7 : c)] = tpart[q][c];
+        put_partial(a.partials + 8L * t + (c == 0 ? 7 : c), tpart[q][c]);
     }
   }
   finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done,

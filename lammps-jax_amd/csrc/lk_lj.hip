@@ -133,13 +133,13 @@ __global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
   }
   const double esum = wave_sum(e_own);
   if (has_rows && lane == 0) {
-    a.partials[8L * tile] = esum;
-    a.partials[8L * tile + 7] = 0.0;
+    put_partial(a.partials + 8L * tile, esum);
+    put_partial(a.partials + 8L * tile + 7, 0.0);
   }
   if (has_rows && VIRIAL && lane < 6) {
     double v = vir[lane][0];
     for (int w = 1; w < W; ++w) v += vir[lane][w];
-    a.partials[8L * tile + 1 + lane] = v;
+    put_partial(a.partials + 8L * tile + 1 + lane, v);
   }
   }
   finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done, scratch,

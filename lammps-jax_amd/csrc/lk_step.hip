@@ -411,7 +411,7 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
         sbase[sub] = base;
         p.tile_base[tile] = base;
         if (gmask != 0) atomicOr(&p.state[kGhostFlag], 1);
-        a.partials[8L * tile + 0] = esum;
+        put_partial(a.partials + 8L * tile + 0, esum);
       }
     }
     __syncthreads();

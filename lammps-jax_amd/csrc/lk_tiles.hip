@@ -39,9 +39,10 @@ namespace lk {
 
 constexpr int kTileSortN = 2048;      // bitonic sort width of the union build (>= kTileUnion)
 constexpr int kTileHash = 8192;       // hash slots of the union build
-constexpr int kTileW = 4;             // waves per sub-tile
+constexpr int kTileW = 6;             // waves per sub-tile
 constexpr int kTileSub = kTileRows / kWave;
-constexpr int kTileBlocksPerCu = 3;   // 47.9 KB of LDS per block
+constexpr int kTileBlocksPerCu = 2;   // 79.5 KB of LDS per block
+constexpr int kTileIdGroups = 40;     // slot groups per row whose ids the walk keeps in LDS
 constexpr int kTileGridBits = 5;      // Hilbert grid of 2^5 cells per axis over the bounding box
 
 __device__ __forceinline__ uint32_t tile_hash(int j)
@@ -400,13 +401,18 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
 {
   constexpr int W = kTileW, SUB = kTileSub;
   __shared__ double ux[kTileUnion], uy[kTileUnion], uz[kTileUnion];
-  __shared__ int ugid[kTileUnion];
-  __shared__ unsigned char usp[kTileUnion];
-  __shared__ int cpart[SUB][W][kWave];
-  __shared__ double rpart[SUB][W][kWave];
+  __shared__ uint32_t ugid[kTileUnion];  // atom id | species << 24
   __shared__ uint32_t sbits[SUB][kTileMaxSlots / 32][kWave];
   __shared__ int scnt[SUB][kWave];
   __shared__ int sbase[SUB];
+  // the ids of the walked slot groups, for the compacted write (groups past kTileIdGroups are
+  // read again from the tile list)
+  __shared__ uint64_t sids[kTileIdGroups][kTileRows];
+  // the walk's partial counts and densities reuse ux once every wave has left the walk
+  int(*cpart)[W][kWave] = reinterpret_cast<int(*)[W][kWave]>(ux);
+  double(*rpart)[W][kWave] = reinterpret_cast<double(*)[W][kWave]>(ux + SUB * W * kWave / 2);
+  static_assert(SUB * W * kWave * 3 <= 2 * kTileUnion, "the partials fit in ux");
+  constexpr int kBitWords = SUB * (kTileMaxSlots / 32) * kWave;
 
   // the density intervals are read from the density-only (f, d) table in memory (no LDS window)
   const int sub = wave_in_block() / W;
@@ -436,10 +442,11 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
         ux[u] = p.x[3L * g + 0];
         uy[u] = p.x[3L * g + 1];
         uz[u] = p.x[3L * g + 2];
-        usp[u] = static_cast<unsigned char>(clamp_species(p.type[g] - 1, a.n_el));
-        ugid[u] = g;
+        ugid[u] = static_cast<uint32_t>(g) |
+                  static_cast<uint32_t>(clamp_species(p.type[g] - 1, a.n_el)) << 24;
       }
     }
+    for (int k = threadIdx.x; k < kBitWords; k += blockDim.x) (&sbits[0][0][0])[k] = 0u;
     __syncthreads();
     const int pos = tile * kTileRows + sub * kWave + lane;
     const int i = t.atom[pos];
@@ -450,7 +457,7 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
       xi1 = p.x[3L * i + 1];
       xi2 = p.x[3L * i + 2];
     }
-    const int nwords = (wave_max_int(nn) + 31) >> 5;
+    const int nmax = wave_max_int(nn);  // the sub-tile's longest row
     int cnt = 0;
     double rho = 0.0;
     auto dist2 = [&](double xj0, double xj1, double xj2) -> double {
@@ -458,49 +465,62 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
       const double dx = xi0 - xj0, dy = xi1 - xj1, dz = xi2 - xj2;
       return dx * dx + dy * dy + dz * dz;
     };
-    for (int wd = wave; wd < nwords; wd += W) {
+    if (staged) {
+      // The sub-tile's four-slot groups dealt round the W waves (group g to wave g mod W), up to
+      // the longest row; the next group's ids load while one is walked. A wave gathers the kept
+      // bits of its groups in one bit word and ORs it into LDS when it moves to another word.
+      const int ngroups = (nmax + 3) >> 2;
+      const uint64_t *lidp =
+          t.lid + static_cast<long>(tile) * t.groups * kTileRows + sub * kWave + lane;
+      uint64_t ids = wave < ngroups ? lidp[static_cast<long>(wave) * kTileRows] : 0;
       uint32_t word = 0;
-      if (staged) {
-        // the word's eight four-slot groups; the next group's ids load while one is walked
-        const long gbase = static_cast<long>(tile) * t.groups + wd * 8;
-        const int gcount = min(8, t.groups - wd * 8);
-        const uint64_t *lidp = t.lid + gbase * kTileRows + sub * kWave + lane;
-        uint64_t ids = lidp[0];
-        // Each group's slots two at a time without a branch between them: both positions from
-        // LDS, both filter decisions, both coefficient rows in flight together (a slot with no
-        // density reads row 0 of its table, unused), then the densities added in slot order.
+      int wd = wave >> 3;
 #pragma unroll 1
-        for (int g = 0; g < gcount; ++g) {
-          const uint64_t cur = ids;
-          if (g + 1 < gcount) ids = lidp[static_cast<long>(g + 1) * kTileRows];
-#pragma unroll
-          for (int h = 0; h < 4; h += 2) {
-            double tq[2];
-            bool dens[2];
-            Coef<double> c[2];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-              const int q = h + k;
-              const uint32_t id = static_cast<uint32_t>(cur >> (16 * q)) & 0xFFFFu;
-              const bool has = id != kNoId;
-              const uint32_t u = has ? id : 0u;
-              const double rsq = dist2(ux[u], uy[u], uz[u]);
-              // PackNeighborFunctor keeps rsq <= cutsq (cpp:91)
-              const bool kept = has && !(rsq > p.cutsq);
-              word |= kept ? 1u << (g * 4 + q) : 0u;
-              cnt += kept ? 1 : 0;
-              // valid = mask & r_sq < cutoff_sq (eam.py:288)
-              dens[k] = kept && rsq < a.cutsq;
-              const double s = dens[k] ? rsq : 1.0;
-              const Locator<double> L = locate_mul(s * rsqrt_nr(s), a.inv_dr, a.nr);
-              tq[k] = L.t;
-              c[k] = dens_coef(a, dens[k] ? L.node : 0, usp[u]);
-            }
-#pragma unroll
-            for (int k = 0; k < 2; ++k) rho = dens[k] ? rho + cvalue(c[k], tq[k]) : rho;
-          }
+      for (int g = wave; g < ngroups; g += W) {
+        const uint64_t cur = ids;
+        if (g + W < ngroups) ids = lidp[static_cast<long>(g + W) * kTileRows];
+        if (g < kTileIdGroups) sids[g][sub * kWave + lane] = cur;
+        if ((g >> 3) != wd) {
+          atomicOr(&sbits[sub][wd][lane], word);
+          word = 0;
+          wd = g >> 3;
         }
-      } else {
+        const int sh = (g & 7) * 4;
+        // two slots at a time without a branch between them: both positions from LDS, both
+        // filter decisions, both coefficient rows in flight together (a slot with no density
+        // reads row 0 of its table, unused), then the densities added in slot order
+#pragma unroll
+        for (int h = 0; h < 4; h += 2) {
+          double tq[2];
+          bool dens[2];
+          Coef<double> c[2];
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const int q = h + k;
+            const uint32_t id = static_cast<uint32_t>(cur >> (16 * q)) & 0xFFFFu;
+            const bool has = id != kNoId;
+            const uint32_t u = has ? id : 0u;
+            const double rsq = dist2(ux[u], uy[u], uz[u]);
+            // PackNeighborFunctor keeps rsq <= cutsq (cpp:91)
+            const bool kept = has && !(rsq > p.cutsq);
+            word |= kept ? 1u << (sh + q) : 0u;
+            cnt += kept ? 1 : 0;
+            // valid = mask & r_sq < cutoff_sq (eam.py:288)
+            dens[k] = kept && rsq < a.cutsq;
+            const double s = dens[k] ? rsq : 1.0;
+            const Locator<double> L = locate_mul(s * rsqrt_nr(s), a.inv_dr, a.nr);
+            tq[k] = L.t;
+            c[k] = dens_coef(a, dens[k] ? L.node : 0, static_cast<int>(ugid[u] >> 24));
+          }
+#pragma unroll
+          for (int k = 0; k < 2; ++k) rho = dens[k] ? rho + cvalue(c[k], tq[k]) : rho;
+        }
+      }
+      if (wave < ngroups) atomicOr(&sbits[sub][wd][lane], word);
+    } else {
+      // the engine's list, one 32-slot word per wave in turn
+      for (int wd = wave; wd < (nmax + 31) >> 5; wd += W) {
+        uint32_t word = 0;
         for (int jj = wd * 32; jj < min(wd * 32 + 32, nn); ++jj) {
           const int j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
           if (j >= p.max_atoms) continue;
@@ -514,9 +534,10 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
             rho += cvalue(dens_coef(a, L.node, clamp_species(p.type[j] - 1, a.n_el)), L.t);
           }
         }
+        sbits[sub][wd][lane] = word;
       }
-      sbits[sub][wd][lane] = word;
     }
+    __syncthreads();  // every wave has left the walk: ux takes the partials
     cpart[sub][wave][lane] = cnt;
     rpart[sub][wave][lane] = rho;
     __syncthreads();
@@ -556,7 +577,7 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
         sbase[sub] = base;
         p.tile_base[subtile] = base;
         if (gmask != 0) atomicOr(&p.state[kGhostFlag], 1);
-        a.partials[8L * subtile + 0] = esum;
+        put_partial(a.partials + 8L * subtile + 0, esum);
       }
     }
     __syncthreads();
@@ -608,9 +629,12 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
           if (active) {
             if (staged) {
               const uint64_t w4 =
-                  t.lid[((static_cast<long>(tile) * t.groups + (jj >> 2)) * kTileRows) +
-                        sub * kWave + lane];
-              j = ugid[static_cast<uint32_t>(w4 >> (16 * (jj & 3))) & 0xFFFFu];
+                  (jj >> 2) < kTileIdGroups
+                      ? sids[jj >> 2][sub * kWave + lane]
+                      : t.lid[((static_cast<long>(tile) * t.groups + (jj >> 2)) * kTileRows) +
+                              sub * kWave + lane];
+              j = static_cast<int>(ugid[static_cast<uint32_t>(w4 >> (16 * (jj & 3))) & 0xFFFFu] &
+                                   0xFFFFFFu);
             } else {
               j = p.neighbors[static_cast<long>(jj) * p.stride + i] & kNeighMask;
             }
@@ -764,7 +788,7 @@ bool tile_step_eligible(const Handle &h, int num_rows, int maxneighs)
 {
   return h.model == 1 && h.contract.precision == LK_FLOAT64 && !h.matrix &&
          h.accum == LK_ACCUM_ONESIDED && h.list_epoch >= 0 && num_rows > 0 &&
-         maxneighs <= kTileMaxSlots && h.n_el <= 255;
+         maxneighs <= kTileMaxSlots && h.n_el <= 255 && h.contract.max_atoms <= (1 << 24);
 }
 
 hipError_t launch_step_tiles(Handle &h, hipStream_t s, const double *x, const int *type,

@@ -864,12 +864,12 @@ __global__ __launch_bounds__(kWave) void k_eam_embed_inc(EamArgs<S> m, TwoSided 
     if (a < erows) e_row = static_cast<double>(epair ? epair[a] + F : F);
   }
   const double esum = wave_sum(e_row);
-  if (threadIdx.x == 0 && tile < t.nblk) m.partials[8L * tile] = esum;
+  if (threadIdx.x == 0 && tile < t.nblk) put_partial(m.partials + 8L * tile, esum);
 }
 
 // Per-row f.r virial of the total f after the add, summed over the 64 rows of each partial tile
-// in a fixed order by the first wave, which alone stores partials (finalize_last_block's
-// contract). vt is [6][APB], one column per atom of the block.
+// in a fixed order by the first wave, which stores the partials. vt is [6][APB], one column per
+// atom of the block.
 template <bool VIRIAL, int APB>
 __device__ __forceinline__ void add_row_force(double *f, const double *x, int a, int nadd,
                                               int nall, int fdotr, double scale, double fx,
@@ -917,13 +917,13 @@ __device__ __forceinline__ void store_block_partials(double *partials, int blk, 
     if (VIRIAL) {
       for (int c = 0; c < 6; ++c) {
         const double v = wave_sum(vt[c][q * kRowAtoms + lane]);
-        if (lane == 0) partials[8L * tile + 1 + c] = v;
+        if (lane == 0) put_partial(partials + 8L * tile + 1 + c, v);
       }
     }
     const double e = wave_sum(et[q * kRowAtoms + lane]);
     if (lane == 0) {
-      partials[8L * tile + 7] = write_energy ? 0.0 : e;
-      if (write_energy) partials[8L * tile] = e;
+      put_partial(partials + 8L * tile + 7, write_energy ? 0.0 : e);
+      if (write_energy) put_partial(partials + 8L * tile, e);
     }
   }
 }
@@ -1635,8 +1635,8 @@ __device__ __forceinline__ void edge_tail_and_slots(const EdgeOut<S> &o, long ne
     q[2] = S(0);
   }
   for (long t = tid; t < o.ntiles; t += stride) {
-    if (!o.block_energy || t >= gridDim.x) o.partials[8 * t + 7] = 0.0;
-    if (t >= o.slot0_from) o.partials[8 * t] = 0.0;
+    if (!o.block_energy || t >= gridDim.x) put_partial(o.partials + 8L * t + 7, 0.0);
+    if (t >= o.slot0_from) put_partial(o.partials + 8L * t, 0.0);
   }
 }
 
@@ -1721,7 +1721,7 @@ __global__ __launch_bounds__(256) void k_lj_edge_force(LjModel<S> m, EdgeOut<S> 
     __syncthreads();
   }
   if (threadIdx.x == 0 && static_cast<int>(blockIdx.x) < o.ntiles)
-    o.partials[8L * blockIdx.x + 7] = red[0];
+    put_partial(o.partials + 8L * blockIdx.x + 7, red[0]);
   edge_tail_and_slots(o, ne);
 }
 
@@ -1745,8 +1745,8 @@ __global__ __launch_bounds__(256) void k_fdotr_rows(const double *__restrict__ f
     const int c = result->edge_count;
     state[kEdgeForceLive] = c < max_edges ? c : max_edges;
   }
-  // Each wave sums one tile; the first wave alone stores the block's tiles (finalize_last_block
-  // releases the first wave's stores only). The loop bounds are the block's, for the barriers.
+  // Each wave sums one tile; the first wave stores the block's tiles. The loop bounds are the
+  // block's, for the barriers.
   for (int t0 = blockIdx.x * kWaves; t0 < ntiles; t0 += static_cast<int>(gridDim.x) * kWaves) {
     const int t = t0 + wave;
     const int a = t * kWave + lane;
@@ -1769,7 +1769,7 @@ __global__ __launch_bounds__(256) void k_fdotr_rows(const double *__restrict__ f
     __syncthreads();
     if (threadIdx.x < kWaves * 6) {
       const int q = threadIdx.x / 6, c = threadIdx.x % 6;
-      if (t0 + q < ntiles) partials[8L * (t0 + q) + 1 + c] = tp[q][c];
+      if (t0 + q < ntiles) put_partial(partials + 8L * (t0 + q) + 1 + c, tp[q][c]);
     }
     __syncthreads();
   }

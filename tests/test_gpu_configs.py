@@ -7,9 +7,9 @@ calls (lk_pack_compute, then lk_step_result), with the capacities the benchmark 
   eam_alloy_1m    EAM/alloy fp32, fcc 64^3 (1,048,576 atoms), half list, half scheme, 96/atom
   lj_ghost_262k   LJ fp32, 262,144 owned atoms, n_hops = 2 (ghost rows packed), plain, 96/atom
 
-At these sizes the launch geometry of the benchmark runs: the persistent force sweep walks more
-tile groups than it has blocks, its last-block reduction spans every block, the packs claim
-thousands of tiles. Each case is compared with the oracle on the same inputs:
+At these sizes the launch geometry of the benchmark runs: the persistent kernels walk their
+groups over every CU, the last-block reductions span every block, the packs claim thousands of
+tiles. Each case is compared with the oracle on the same inputs:
 
   * the packed arrays bit for bit after canonical ordering, with the count, the overflow flag
     and the padding above the count;
@@ -148,6 +148,33 @@ def _model_checks(wl, sysm, info, f, ref, rows):
     else:
         assert abs(info.energy - ref["energy"]) / nl <= F32_ENERGY_PER_ATOM
         assert rel_err(f[:rows], f_ref) < F32_REL
+
+
+@pytest.mark.parametrize("precision", [8, 4])
+def test_force_sweep_walking_several_groups(gpu, precision):
+    """One-sided EAM on 157,216 atoms (fcc 34^3): 308 groups of 512 rows, more than the force
+    sweep's blocks (one per CU), so blocks walk two groups and publish their partials through the
+    release fence (the 131,072-atom workload has one group per block, whose partials go out as
+    agent-scope stores). Forces, energy and virial against the oracle, and a second step gives
+    bitwise the same results."""
+    import dataclasses
+
+    wl = dataclasses.replace(systems.make_workload("eam_alloy_131k", cells=(34, 34, 34)),
+                             precision=precision)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=wl.list_kind)
+    pj = PairJax.for_workload(wl, sysm)
+    print(f"multi-group force sweep case: nlocal={sysm.nlocal} fp{8 * precision}", flush=True)
+    info = pj.compute()
+    f = pj.forces().copy()
+    ref, (_, _, _, count, ovf) = _oracle(wl, sysm, lst, pj)
+    assert info.edge_count == count and info.edge_overflow == ovf == 0
+    _model_checks(wl, sysm, info, f, ref, sysm.nlocal)
+    assert rel_err(info.virial, ref["virial"]) < (1e-12 if precision == 8 else F32_REL)
+    again = pj.compute()
+    assert again.energy == info.energy
+    np.testing.assert_array_equal(again.virial, info.virial)
+    np.testing.assert_array_equal(pj.forces(), f)
 
 
 def test_neighbor_matrix_layout_at_full_size(gpu):
