@@ -374,6 +374,12 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
   if (!last_block) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   const int t = threadIdx.x, nt = blockDim.x;
+  // the pack's counts, loaded while the partials are
+  int demand = 0, ghost_flag = 0;
+  if (t == 0 && pack.state) {
+    demand = pack.state[kDemand];
+    ghost_flag = pack.state[kGhostFlag];
+  }
   double acc[7] = {0, 0, 0, 0, 0, 0, 0};
   for (int k = t; k < ntiles; k += nt) {
     const double *q = partials + 8L * k;
@@ -382,22 +388,36 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
   }
   if (t == 0)
     for (int k = 0; k < nextra; ++k) acc[0] += extra[k];
+  // fixed order: a tree of fan-in 16 over the threads' sums, each node adding its inputs in order
   for (int c = 0; c < 7; ++c) scratch[c * nt + t] = acc[c];
   __syncthreads();
-  for (int off = nt / 2; off >= 1; off >>= 1) {
-    if (t < off)
-      for (int c = 0; c < 7; ++c) scratch[c * nt + t] += scratch[c * nt + t + off];
+  for (int n = nt; n > 1;) {
+    const int m = (n + 15) / 16;
+    double part = 0.0;
+    if (t < 7 * m) {
+      const int j = t % m, cnt = min(16, n - 16 * j);
+      const double *v = scratch + (t / m) * nt + 16 * j;
+      double x[16];
+#pragma unroll
+      for (int l = 0; l < 16; ++l) x[l] = l < cnt ? v[l] : 0.0;
+      part = x[0];
+#pragma unroll
+      for (int l = 1; l < 16; ++l) part += x[l];
+    }
     __syncthreads();
+    if (t < 7 * m) scratch[(t / m) * nt + t % m] = part;
+    __syncthreads();
+    n = m;
   }
   if (t == 0) {
-    result->energy = (flags & LK_ENERGY) ? escale * scratch[0] : 0.0;
-    for (int c = 0; c < 6; ++c)
-      result->virial[c] = (flags & LK_VIRIAL) ? vscale * scratch[(c + 1) * nt] : 0.0;
+    double tot[7];
+    for (int c = 0; c < 7; ++c) tot[c] = scratch[c * nt];
+    result->energy = (flags & LK_ENERGY) ? escale * tot[0] : 0.0;
+    for (int c = 0; c < 6; ++c) result->virial[c] = (flags & LK_VIRIAL) ? vscale * tot[c + 1] : 0.0;
     if (pack.state) {
-      const int demand = pack.state[kDemand];
       result->edge_count = demand;
       result->edge_overflow = demand > pack.max_edges ? 1 : 0;
-      result->ghost_sender = pack.state[kGhostFlag];
+      result->ghost_sender = ghost_flag;
       // every block has passed its tail reset (it precedes the done count): the live count moves
       pack.state[kLive] = demand < pack.max_edges ? demand : pack.max_edges;
       // and the next fused pack may start here, as the atom-record launch would start it: its
@@ -408,14 +428,22 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
     }
     result->seq += 1;
     if (mirror) {
-      // the host's pinned copy, no separate readback: every field, a system-scope fence, then
-      // the sequence number the host waits for
-      StepResult copy = *result;
-      const int seq = copy.seq;
-      copy.seq = mirror->seq;
-      *mirror = copy;
-      __threadfence_system();
-      __hip_atomic_store(&mirror->seq, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+      // The host's pinned copy, no separate readback: every field stored through to host memory
+      // (system scope), a wait for those stores, then the sequence number the host waits for.
+      // No system-scope fence: it would write back the XCD's whole L2 (2 us here).
+      const StepResult copy = *result;
+      __hip_atomic_store(&mirror->energy, copy.energy, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      for (int c = 0; c < 6; ++c)
+        __hip_atomic_store(&mirror->virial[c], copy.virial[c], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(&mirror->edge_count, copy.edge_count, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(&mirror->edge_overflow, copy.edge_overflow, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(&mirror->ghost_sender, copy.ghost_sender, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+      __builtin_amdgcn_s_waitcnt(0);
+      __hip_atomic_store(&mirror->seq, copy.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     *done = 0;  // ready for the next launch
   }
