@@ -341,17 +341,24 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
       }
     }
     __syncthreads();
-    // The block's first wave stores the partials of the group's tiles; tpart is next written
-    // after the next barrier.
-    if (threadIdx.x < TPB * 7) {
-      const int q = threadIdx.x / 7, c = threadIdx.x % 7;
-      const int t = gw.g * TPB + q;
-      if (t * kWave < a.num_rows && (c == 0 || VIRIAL))
-        put_partial(a.partials + 8L * t + (c == 0 ? 7 : c), tpart[q][c]);
+    // The group's sums over its tiles in tile order, the density pass's embedding energy of
+    // each tile (slot 0 of its partials, from an earlier launch) added to its pair energy,
+    // stored over the partials of the group's first tile: the last block reads one entry per
+    // group. tpart is next written after the next barrier.
+    if (threadIdx.x < 7) {
+      const int c = threadIdx.x;
+      double v = 0.0;
+      for (int q = 0; q < TPB; ++q) {
+        const int t = gw.g * TPB + q;
+        if (t >= a.ntiles) break;
+        v += c == 0 ? a.partials[8L * t] + tpart[q][0] : (VIRIAL ? tpart[q][c] : 0.0);
+      }
+      put_partial(a.partials + 8L * TPB * gw.g + c, v);
     }
   }
-  finalize_last_block(a.partials, a.ntiles, a.scale, a.scale, a.flags, a.result, a.done,
-                      reinterpret_cast<double *>(lds), a.pack, a.mirror, a.extra, a.nextra);
+  finalize_last_block(a.partials, (a.ntiles + TPB - 1) / TPB, a.scale, a.scale, a.flags,
+                      a.result, a.done, reinterpret_cast<double *>(lds), a.pack, a.mirror,
+                      a.extra, a.nextra, 8 * TPB, false);
 }
 
 template <typename S>

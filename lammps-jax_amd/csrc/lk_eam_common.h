@@ -352,9 +352,11 @@ __device__ __forceinline__ void put_partial(double *p, double v)
 // 7 * blockDim.x doubles of LDS that is no longer in use. Returns in every block. The energy is
 // scaled by `escale`, the virial by `vscale` (1 when the partials already hold scaled forces).
 //
+// Entry k of the partials starts at partials + stride * k: 0 embedding energy (or the whole
+// energy when !slot7), 1..6 virial, 7 pair energy.
 // Every partial written in the same launch goes out through put_partial (through the XCD's L2
 // to where every XCD reads it), and each wave waits for its own stores before the block counts
-// itself done; the last block takes the acquire (an L2 invalidate) and reads them. No
+// itself done; the last block reads them past its L2. No
 // device-scope release fence: on this multi-XCD device it writes back the XCD's whole L2, and
 // the blocks of an XCD finishing close together queued those write-backs behind each other
 // (6 us at the end of the 131,072-atom force sweep, 12 us in the 262,144-atom LJ sweep).
@@ -364,7 +366,8 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
                                                     double *scratch,
                                                     const FusedPack &pack = FusedPack{},
                                                     StepResult *mirror = nullptr,
-                                                    const double *extra = nullptr, int nextra = 0)
+                                                    const double *extra = nullptr, int nextra = 0,
+                                                    int stride = 8, bool slot7 = true)
 {
   __shared__ int last_block;
   __builtin_amdgcn_s_waitcnt(0);  // this wave's stores (the partials among them) have completed
@@ -372,19 +375,35 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
   if (threadIdx.x == 0) last_block = atomicAdd(done, 1) == static_cast<int>(gridDim.x) - 1;
   __syncthreads();
   if (!last_block) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   const int t = threadIdx.x, nt = blockDim.x;
-  // the pack's counts, loaded while the partials are
+  // At most one entry per thread: agent-scope loads, which read past the XCD's L2, so no
+  // acquire. More: the acquire (an L2 invalidate), then plain loads, several in flight.
+  const bool direct = ntiles <= nt;  // block-uniform
+  if (!direct) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // the pack's counts (written by an earlier launch), loaded while the partials are
   int demand = 0, ghost_flag = 0;
   if (t == 0 && pack.state) {
     demand = pack.state[kDemand];
     ghost_flag = pack.state[kGhostFlag];
   }
   double acc[7] = {0, 0, 0, 0, 0, 0, 0};
-  for (int k = t; k < ntiles; k += nt) {
-    const double *q = partials + 8L * k;
-    acc[0] += q[0] + q[7];
-    for (int c = 1; c < 7; ++c) acc[c] += q[c];
+  if (direct) {
+    if (t < ntiles) {
+      const double *q = partials + static_cast<long>(stride) * t;
+      double v[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        v[c] = c < 7 || slot7 ? __hip_atomic_load(q + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : 0.0;
+      acc[0] = slot7 ? v[0] + v[7] : v[0];
+      for (int c = 1; c < 7; ++c) acc[c] = v[c];
+    }
+  } else {
+    for (int k = t; k < ntiles; k += nt) {
+      const double *q = partials + static_cast<long>(stride) * k;
+      acc[0] += slot7 ? q[0] + q[7] : q[0];
+      for (int c = 1; c < 7; ++c) acc[c] += q[c];
+    }
   }
   if (t == 0)
     for (int k = 0; k < nextra; ++k) acc[0] += extra[k];
