@@ -236,19 +236,15 @@ struct TileBuild {
   unsigned long long *ustat;  // sum of the union sizes (zeroed by k_tile_rows)
 };
 
-// One tile per block: the union of the atoms its entries name (hash set in LDS, then a bitonic
-// sort) and the union index of every entry. The list is read once: the insertion pass leaves
-// each entry's hash slot in the id words, which the last pass turns into union indices.
-__global__ __launch_bounds__(1024) void k_tile_union(TileBuild b)
+// The union of a tile's entries and their union indices, through a hash set in LDS and a bitonic
+// sort: the path of tiles whose atom ids span more than the bitmap holds. It reads the list
+// again; count and fill are block-shared counters.
+__device__ void union_by_hash(const TileBuild &b, int tile, unsigned char *pool, int &count,
+                              int &fill)
 {
-  __shared__ int keys[kTileHash];
-  __shared__ unsigned short rank[kTileHash];
-  __shared__ int sorted[kTileSortN];
-  __shared__ int count, fill;
-  // XCD-grouped: consecutive tiles (neighbours along the curve, sharing list lines) run on one
-  // XCD and meet in its L2
-  const int tile = tile_of_block();
-  if (tile >= b.tiles) return;  // whole block
+  int *keys = reinterpret_cast<int *>(pool);
+  unsigned short *rank = reinterpret_cast<unsigned short *>(pool + 4 * kTileHash);
+  int *sorted = reinterpret_cast<int *>(pool + 6 * kTileHash);
   const int tid = threadIdx.x;
   constexpr uint32_t kMask = kTileHash - 1;
   for (int k = tid; k < kTileHash; k += 1024) keys[k] = -1;
@@ -368,6 +364,167 @@ __global__ __launch_bounds__(1024) void k_tile_union(TileBuild b)
     }
     lid[e] = out;
   }
+}
+
+constexpr int kTileBitmapWords = 8192;  // atom-id bitmap of a tile: ids within 2^18 of its lowest
+constexpr int kTileUnionPool = 4 * kTileHash + 2 * kTileHash + 4 * kTileSortN;
+static_assert(kTileUnionPool >= 4 * kTileBitmapWords + 2 * kTileBitmapWords, "pool holds the bitmap");
+
+// One tile per block (XCD-grouped: consecutive tiles, neighbours along the curve sharing list
+// lines, run on one XCD and meet in its L2): the union of the atoms the tile's entries name,
+// ascending, and every entry's index into it. Thread t holds row t % 128's slot groups t / 128,
+// + 8, ... in registers. When the ids span at most 2^18 (every tile of a spatially ordered
+// engine), a bitmap over [lowest, highest] in LDS: each entry sets its bit, a block scan of the
+// words' popcounts gives each word's first rank, and an entry's index is that rank plus the set
+// bits below its own. No hash, no sort, and the same ascending union as the hash path gives.
+// PER: slot groups per thread (four: rows of up to 128 slots; eight: up to 256), so that the
+// entries held in registers leave two blocks per CU.
+template <int PER>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8))) void k_tile_union(
+    TileBuild b)
+{
+  __shared__ __align__(16) unsigned char pool[kTileUnionPool];
+  __shared__ int count, fill;
+  __shared__ int wred[3][1024 / kWave];
+  const int tile = tile_of_block();
+  if (tile >= b.tiles) return;  // whole block
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wv = tid / kWave;
+  constexpr int kGroupStride = 1024 / kTileRows, kPer = PER;
+  static_assert(kTileMaxSlots / 4 <= 8 * kGroupStride, "eight groups per thread hold a row");
+  const int r = tid % kTileRows;
+  const int p = tile * kTileRows + r;
+  const int nn = b.nn[p], i = b.atom[p];
+  int jv[kPer][4];
+  int lo = INT_MAX, hi = -1;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int g = tid / kTileRows + kGroupStride * k;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int jj = 4 * g + q;
+      int j = -1;
+      if (g < b.groups && jj < nn) {
+        j = b.neighbors[static_cast<long>(jj) * b.stride + i] & kNeighMask;
+        if (j >= b.max_atoms) j = -1;  // cpp:88: the pack skips it
+      }
+      jv[k][q] = j;
+      if (j >= 0) {
+        lo = min(lo, j);
+        hi = max(hi, j);
+      }
+    }
+  }
+  // the block's lowest and highest id
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    lo = min(lo, __shfl_xor(lo, off, kWave));
+    hi = max(hi, __shfl_xor(hi, off, kWave));
+  }
+  if (lane == 0) {
+    wred[0][wv] = lo;
+    wred[1][wv] = hi;
+  }
+  __syncthreads();
+  lo = wred[0][0];
+  hi = wred[1][0];
+  for (int w = 1; w < 1024 / kWave; ++w) {
+    lo = min(lo, wred[0][w]);
+    hi = max(hi, wred[1][w]);
+  }
+  const long span = hi >= lo ? static_cast<long>(hi) - lo + 1 : 0;
+  if (span > 32L * kTileBitmapWords) {  // block-uniform
+    if (tid == 0) {
+      count = 0;
+      fill = 0;
+    }
+    union_by_hash(b, tile, pool, count, fill);
+    return;
+  }
+  uint32_t *bm = reinterpret_cast<uint32_t *>(pool);
+  unsigned short *pre = reinterpret_cast<unsigned short *>(pool + 4 * kTileBitmapWords);
+  const int nw = static_cast<int>((span + 31) >> 5);
+  for (int w = tid; w < nw; w += 1024) bm[w] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = jv[k][q];
+      if (j >= 0) atomicOr(&bm[(j - lo) >> 5], 1u << ((j - lo) & 31));
+    }
+  __syncthreads();
+  // each thread's eight words: their popcounts, a block scan, the words' first ranks
+  constexpr int kWordsPer = kTileBitmapWords / 1024;
+  int wc[kWordsPer];
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < kWordsPer; ++k) {
+    const int w = tid * kWordsPer + k;
+    wc[k] = w < nw ? __popc(bm[w]) : 0;
+    sum += wc[k];
+  }
+  int incl = sum;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int v = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += v;
+  }
+  if (lane == kWave - 1) wred[2][wv] = incl;
+  __syncthreads();
+  int before = 0, U = 0;
+  for (int w = 0; w < 1024 / kWave; ++w) {
+    const int v = wred[2][w];
+    before += w < wv ? v : 0;
+    U += v;
+  }
+  int run = before + incl - sum;
+#pragma unroll
+  for (int k = 0; k < kWordsPer; ++k) {
+    const int w = tid * kWordsPer + k;
+    if (w < nw) pre[w] = static_cast<unsigned short>(run);
+    run += wc[k];
+  }
+  if (tid == 0) atomicAdd(b.ustat, static_cast<unsigned long long>(U));
+  if (U > kTileUnion) {  // block-uniform
+    if (tid == 0) b.ucount[tile] = -1;
+    return;
+  }
+  __syncthreads();
+  // the union, ascending
+  int *uni = b.uni + static_cast<long>(tile) * kTileUnion;
+#pragma unroll
+  for (int k = 0; k < kWordsPer; ++k) {
+    const int w = tid * kWordsPer + k;
+    if (w >= nw) break;
+    uint32_t bits = bm[w];
+    int rk = pre[w];
+    while (bits) {
+      uni[rk++] = lo + 32 * w + __builtin_ctz(bits);
+      bits &= bits - 1u;
+    }
+  }
+  // every entry's union index, four to a word
+  uint64_t *lid = b.lid + static_cast<long>(tile) * b.groups * kTileRows;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int g = tid / kTileRows + kGroupStride * k;
+    if (g >= b.groups) break;
+    uint64_t out = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = jv[k][q];
+      uint32_t id = kNoId;
+      if (j >= 0) {
+        const int d = j - lo;
+        const uint32_t word = bm[d >> 5];
+        id = pre[d >> 5] + __popc(word & ((1u << (d & 31)) - 1u));
+      }
+      out |= static_cast<uint64_t>(id) << (16 * q);
+    }
+    lid[static_cast<long>(g) * kTileRows + r] = out;
+  }
+  if (tid == 0) b.ucount[tile] = U;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -775,7 +932,10 @@ hipError_t build_tile_list(Handle &h, hipStream_t s, const double *x, const int 
   b.lid = T.lid;
   b.tiles = tiles;
   b.ustat = T.ustat;
-  hipLaunchKernelGGL(k_tile_union, dim3(tile_grid(tiles)), dim3(1024), 0, s, b);
+  if (b.groups <= 4 * (1024 / kTileRows))
+    hipLaunchKernelGGL(k_tile_union<4>, dim3(tile_grid(tiles)), dim3(1024), 0, s, b);
+  else
+    hipLaunchKernelGGL(k_tile_union<8>, dim3(tile_grid(tiles)), dim3(1024), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess)
     e = hipMemcpyAsync(T.h_ustat, T.ustat, sizeof(unsigned long long), hipMemcpyDeviceToHost, s);

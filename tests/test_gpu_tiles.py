@@ -51,9 +51,9 @@ def _hilbert_key(q: np.ndarray, bits: int) -> np.ndarray:
     return key
 
 
-def union_sizes(sysm, lst) -> np.ndarray:
-    """The union size of every tile, with the rows in the library's tile order (Hilbert keys of
-    a 32^3 grid over the rows' bounding box, stable sort)."""
+def tile_unions_host(sysm, lst) -> list[np.ndarray]:
+    """The distinct atoms each tile's entries name, with the rows in the library's tile order
+    (Hilbert keys of a 32^3 grid over the rows' bounding box, stable sort)."""
     rows = lst["inum"] + lst["gnum"]
     ilist = lst["ilist"][:rows]
     x = sysm.x[ilist]
@@ -63,14 +63,16 @@ def union_sizes(sysm, lst) -> np.ndarray:
     q = np.clip(c, 0, (1 << GRID_BITS) - 1).astype(np.int64)
     order = np.argsort(_hilbert_key(q, GRID_BITS), kind="stable")
     stride, nb, nn = lst["stride"], lst["neighbors"], lst["numneigh"]
-    sizes = []
+    unions = []
     for t0 in range(0, rows, TILE_ROWS):
-        ids = []
-        for i in ilist[order[t0:t0 + TILE_ROWS]]:
-            js = nb[np.arange(nn[i]) * stride + i] & 0x3FFFFFFF
-            ids.append(js)
-        sizes.append(len(np.unique(np.concatenate(ids))))
-    return np.asarray(sizes)
+        ids = [nb[np.arange(nn[i]) * stride + i] & 0x3FFFFFFF for i in ilist[order[t0:t0 + TILE_ROWS]]]
+        unions.append(np.unique(np.concatenate(ids)))
+    return unions
+
+
+def union_sizes(sysm, lst) -> np.ndarray:
+    """The union size of every tile (tile_unions_host)."""
+    return np.asarray([len(u) for u in tile_unions_host(sysm, lst)])
 
 
 def _long_cutoff_case(seed: int, scramble: bool):
@@ -129,6 +131,37 @@ def test_tiles_over_and_under_the_union_cap(gpu, scramble):
     # the library staged exactly the tiles whose union fits, each with the union size counted
     # here, and sent the others to the gather from memory
     np.testing.assert_array_equal(pj.tile_unions(), np.where(sizes <= UNION_CAP, sizes, -1))
+
+
+def test_union_bitmap_and_hash_builds(gpu):
+    """The union build takes a bitmap over a tile's atom ids when they span at most 2^18, and a
+    hash set with a sort otherwise. An fcc slab of 278,784 owned atoms, thin in z: the tiles at
+    its z faces name ghost images (ids past the owned atoms) beside owned atoms of the lowest ids,
+    a span past 2^18, while the other tiles span less; some tiles of either kind exceed the union
+    cap. Both kinds of build give the union sizes counted here (or mark the tile past the cap),
+    and the step matches the oracle."""
+    wl = systems.make_workload("eam_alloy_131k", cells=(66, 66, 16), seed=14)
+    sysm = wl.system()
+    lst = sysm.build_list(wl.cutoff + wl.skin, kind=harness.LIST_FULL)
+    unions = tile_unions_host(sysm, lst)
+    spans = np.asarray([u[-1] - u[0] + 1 if len(u) else 0 for u in unions])
+    sizes = np.asarray([len(u) for u in unions])
+    wide, fits = spans > 1 << 18, sizes <= UNION_CAP
+    print(f"union build case nlocal={sysm.nlocal} nall={sysm.nall} tiles={len(unions)} "
+          f"wide under the cap={int((wide & fits).sum())} narrow under the cap="
+          f"{int((~wide & fits).sum())} over the cap={int((~fits).sum())}", flush=True)
+    assert (wide & fits).any() and (~wide & fits).any() and (~fits).any()
+    pj = PairJax(sysm, ("eam", wl.tables), precision=8, accumulation="onesided")
+    info = pj.compute()
+    np.testing.assert_array_equal(pj.tile_unions(), np.where(fits, sizes, -1))
+    ref = _oracle(wl, sysm, pj)
+    nl = sysm.nlocal
+    assert info.edge_overflow == 0
+    assert_forces(8, pj.forces()[:nl], ref["forces"][:nl])
+    assert_virial(8, info.virial, ref["virial"])
+    # Summed in another order over 278,784 atoms (-6.4 eV each) the total moves by about 1.6e-14
+    # of itself, which is the per-atom bar of 1e-13: the energy is held to 1e-13 relative here.
+    assert abs(info.energy - ref["energy"]) <= 1e-13 * abs(ref["energy"])
 
 
 def test_tile_lists_reused_until_the_list_changes(gpu):
