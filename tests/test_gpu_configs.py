@@ -150,16 +150,17 @@ def _model_checks(wl, sysm, info, f, ref, rows):
         assert rel_err(f[:rows], f_ref) < F32_REL
 
 
-@pytest.mark.parametrize("precision", [8, 4])
-def test_force_sweep_walking_several_groups(gpu, precision):
-    """One-sided EAM on 157,216 atoms (fcc 34^3): 308 groups of 512 rows, more than the force
-    sweep's blocks (one per CU), so blocks walk two groups and publish their partials through the
-    release fence (the 131,072-atom workload has one group per block, whose partials go out as
-    agent-scope stores). Forces, energy and virial against the oracle, and a second step gives
-    bitwise the same results."""
+@pytest.mark.parametrize("precision,cells", [(8, 34), (4, 34), (4, 52)])
+def test_force_sweep_walking_several_groups(gpu, precision, cells):
+    """One-sided EAM on fcc 34^3 (157,216 atoms: 308 groups of 512 rows) and 52^3 (562,432
+    atoms: 1,099 groups): more groups than the force sweep's blocks (one per CU), so blocks walk
+    two or more groups. Each group's sums go out with agent-scope stores; the last block reads
+    one entry per thread directly for up to 1,024 groups, and past that takes the acquire and
+    reads several per thread. Forces, energy and virial against the oracle, and a second step
+    gives bitwise the same results."""
     import dataclasses
 
-    wl = dataclasses.replace(systems.make_workload("eam_alloy_131k", cells=(34, 34, 34)),
+    wl = dataclasses.replace(systems.make_workload("eam_alloy_131k", cells=(cells,) * 3),
                              precision=precision)
     sysm = wl.system()
     lst = sysm.build_list(wl.cutoff + wl.skin, kind=wl.list_kind)
