@@ -463,6 +463,80 @@ __global__ __launch_bounds__(kWave) void k_inc_tiles_place(ListArgs L, int ntile
   }
 }
 
+// Out-entries through LDS, one wave (block) per 64-row tile, staged compactly: the tile's kept
+// entries in row order, each row's run at the prefix of the rows' out-entry counts, with the row
+// of each entry beside it; then 64 staged entries per store, each to its row's list at its place
+// in the run. A round stages the rows whose runs fit `cap` entries together (one row always
+// fits: cap >= maxneighs); rows past that wait for the next round. The list is read slot-major
+// (eight slots per lane in flight) and the lists written atom-major, both coalesced; sized to
+// the mean run rather than the longest row, the staging leaves more waves per CU when the rows
+// are ragged, and each store writes 64 entries however the rows end.
+__global__ __launch_bounds__(kWave) void k_inc_tiles_place_runs(ListArgs L, int ntiles, int cap)
+{
+  extern __shared__ int stage[];  // [cap] neighbours, [64] run starts, [64] list bases, then
+                                  // [cap] slot numbers (u8), [cap] rows (u8)
+  const int tile = blockIdx.x;
+  const int lane = threadIdx.x;
+  if (tile >= ntiles) return;
+  int *sj = stage;
+  int *rstart = stage + cap;
+  int *rbase = rstart + kWave;
+  unsigned char *sq = reinterpret_cast<unsigned char *>(rbase + kWave);
+  unsigned char *sr = sq + cap;
+  const int ii = tile * kWave + lane;
+  int nn = 0, i = -1;
+  if (ii < L.rows) i = list_row(L, ii, nn);
+  const int c = i >= 0 ? L.deg[i] : 0;  // kept out-entries (k_inc_tiles_count)
+  const int base_own = i >= 0 ? L.loc[i] : 0;
+  int incl = c;  // inclusive prefix of the counts over the tile's rows
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int v = __shfl_up(incl, off, kWave);
+    if (lane >= off) incl += v;
+  }
+  int r0 = 0, staged_before = 0;  // wave-uniform
+  while (r0 < kWave) {
+    const int start = incl - c - staged_before;  // this row's run in this round
+    const uint64_t F = wave_ballot(lane >= r0 && start + c <= cap);
+    const int r1 = 64 - __clzll(F);  // rows r0 .. r1 - 1 (the prefix is nondecreasing)
+    const bool mine = lane >= r0 && lane < r1;
+    if (mine) {
+      rstart[lane] = start;
+      rbase[lane] = base_own;
+      int k = start;
+      constexpr int kBatch = 8;
+      for (int j0 = 0; j0 < nn; j0 += kBatch) {
+        int raw[kBatch];
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q)
+          raw[q] = j0 + q < nn ? L.neighbors[static_cast<long>(j0 + q) * L.stride + i] : 0;
+#pragma unroll
+        for (int q = 0; q < kBatch; ++q) {
+          const int j = raw[q] & kNeighMask;
+          // list_neighbor's filter on the loaded entry
+          if (j0 + q < nn && j < L.max_atoms && !(L.half_filter && j < i)) {
+            sj[k] = j;
+            sq[k] = static_cast<unsigned char>(j0 + q);
+            sr[k] = static_cast<unsigned char>(lane);
+            ++k;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const int total = __shfl(incl, r1 - 1, kWave) - staged_before;
+    for (int e = lane; e < total; e += kWave) {
+      const int r = sr[e];
+      const int q = rbase[r] + (e - rstart[r]);
+      L.inc[q] = sj[e];
+      L.inc_bit[q] = slot_bit(L, tile * kWave + r, sq[e]);
+    }
+    __syncthreads();
+    staged_before += total;
+    r0 = r1;
+  }
+}
+
 // keys of the sort's unused tail [kept, n) (kept read on the device): the pad key, above every atom
 __global__ __launch_bounds__(256) void k_inc_pad_keys(uint32_t *__restrict__ keys,
                                                       const int *__restrict__ kept, int n,
@@ -1406,12 +1480,27 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall, 
   }
   {
     StageTimer timer(h, s, "inc_place");
-    // out-entries staged in LDS per tile when the slot numbers fit a byte, else row by row
+    // out-entries staged in LDS per tile when the slot numbers fit a byte, else row by row. Rows
+    // padded to the longest (pitch), or runs packed at 5/4 of the mean run per row (the list
+    // entries read back for a large list; the longest row at least) when that staging is no
+    // larger: ragged rows. (C4's half list, 48 of 105 slots on average: place 978 -> 785 us a
+    // rebuild with the runs; C5's even rows lost 22 us with them.)
     const int pitch = L.maxneighs | 1;
-    const size_t lds = static_cast<size_t>(kWave) * pitch * (sizeof(int) + 1);
-    if (L.maxneighs <= 255 && lds <= 65536) {
+    const size_t lds_rows = static_cast<size_t>(kWave) * pitch * (sizeof(int) + 1);
+    const long mean_run = kept > 0 && rows > 0 ? (static_cast<long>(kept) + rows - 1) / rows
+                                               : L.maxneighs;
+    const int cap = static_cast<int>(std::max<long>(
+        L.maxneighs, std::min<long>(static_cast<long>(kWave) * L.maxneighs,
+                                    kWave * ((mean_run * 5 + 3) / 4))));
+    const size_t lds_runs = static_cast<size_t>(cap) * (sizeof(int) + 2) + 2 * kWave * sizeof(int);
+    if (L.maxneighs <= 255 && lds_runs <= lds_rows) {
       if (ntiles > 0)
-        hipLaunchKernelGGL(k_inc_tiles_place, dim3(ntiles), dim3(kWave), lds, s, L, ntiles, pitch);
+        hipLaunchKernelGGL(k_inc_tiles_place_runs, dim3(ntiles), dim3(kWave), lds_runs, s, L,
+                           ntiles, cap);
+    } else if (L.maxneighs <= 255 && lds_rows <= 65536) {
+      if (ntiles > 0)
+        hipLaunchKernelGGL(k_inc_tiles_place, dim3(ntiles), dim3(kWave), lds_rows, s, L, ntiles,
+                           pitch);
     } else {
       hipLaunchKernelGGL(k_inc_rows_place, dim3((rows + 255) / 256), dim3(256), 0, s, L);
     }
