@@ -1484,7 +1484,8 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall, 
     // padded to the longest (pitch), or runs packed at 5/4 of the mean run per row (the list
     // entries read back for a large list; the longest row at least) when that staging is no
     // larger: ragged rows. (C4's half list, 48 of 105 slots on average: place 978 -> 785 us a
-    // rebuild with the runs; C5's even rows lost 22 us with them.)
+    // rebuild with the runs; C5's even rows lost 22 us with them.) Either staging stays within
+    // 64 KB of dynamic LDS; a larger one goes row by row.
     const int pitch = L.maxneighs | 1;
     const size_t lds_rows = static_cast<size_t>(kWave) * pitch * (sizeof(int) + 1);
     const long mean_run = kept > 0 && rows > 0 ? (static_cast<long>(kept) + rows - 1) / rows
@@ -1493,7 +1494,7 @@ static hipError_t build_incidence_from_list(Handle &h, hipStream_t s, int nall, 
         L.maxneighs, std::min<long>(static_cast<long>(kWave) * L.maxneighs,
                                     kWave * ((mean_run * 5 + 3) / 4))));
     const size_t lds_runs = static_cast<size_t>(cap) * (sizeof(int) + 2) + 2 * kWave * sizeof(int);
-    if (L.maxneighs <= 255 && lds_runs <= lds_rows) {
+    if (L.maxneighs <= 255 && lds_runs <= lds_rows && lds_runs <= 65536) {
       if (ntiles > 0)
         hipLaunchKernelGGL(k_inc_tiles_place_runs, dim3(ntiles), dim3(kWave), lds_runs, s, L,
                            ntiles, cap);
