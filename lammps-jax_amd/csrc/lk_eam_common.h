@@ -12,6 +12,8 @@ namespace lk {
 
 template <typename S>
 using LdsEntry = std::conditional_t<sizeof(S) == 8, double2, float4>;
+static_assert(sizeof(LdsEntry<double>) == 16 && sizeof(LdsEntry<float>) == 16,
+              "a window entry is one 16-byte load into LDS");
 
 template <typename S>
 struct Coef {
@@ -110,10 +112,21 @@ __device__ __forceinline__ Window<S> fill_window(LdsEntry<S> *lds, int cap_entri
   const int cap_nodes = cap_entries / T;
   w.lo = a.nr > cap_nodes ? a.nr - cap_nodes : 0;
   const int n = (a.nr - w.lo) * T;
-  for (int q = threadIdx.x; q < n; q += blockDim.x) {
-    const int node = w.lo + q / T;
-    lds[q] = a.ltab[static_cast<long>(node) * a.n_rtab + (q % T)];
+  // Loads straight into LDS (global_load_lds_dwordx4): each lane names its own 16-byte entry, and
+  // a wave's 64 entries land at consecutive places from the wave-uniform LDS address; no data
+  // passes through registers, so every load of the fill is in flight at once.
+  const int lane = threadIdx.x & (kWave - 1), nw = blockDim.x / kWave;
+  for (int c = threadIdx.x / kWave; c * kWave < n; c += nw) {
+    const int q = c * kWave + lane;
+    if (q < n) {
+      const int node = w.lo + q / T;
+      const LdsEntry<S> *src = a.ltab + static_cast<long>(node) * a.n_rtab + (q % T);
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void *)(src),
+                                       (__attribute__((address_space(3))) void *)(lds + c * kWave),
+                                       16, 0, 0);
+    }
   }
+  __builtin_amdgcn_s_waitcnt(0);  // the loads have written LDS
   __syncthreads();
   return w;
 }
