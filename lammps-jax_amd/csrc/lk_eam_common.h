@@ -420,18 +420,21 @@ __device__ __forceinline__ void finalize_last_block(const double *partials, int 
   }
   if (t == 0)
     for (int k = 0; k < nextra; ++k) acc[0] += extra[k];
-  // fixed order: a tree of fan-in 16 over the threads' sums, each node adding its inputs in order
+  // fixed order: a tree of fan-in 16 over the threads' sums (the first ntiles when each thread
+  // holds at most one entry), each node adding its inputs in order. Node j of a level takes
+  // inputs j, j + m, j + 2m, ...: the lanes of a wave read consecutive doubles (no LDS bank
+  // conflicts; sixteen inputs apiece put every lane of a wave on the same two banks)
   for (int c = 0; c < 7; ++c) scratch[c * nt + t] = acc[c];
   __syncthreads();
-  for (int n = nt; n > 1;) {
+  for (int n = direct ? max(ntiles, 1) : nt; n > 1;) {
     const int m = (n + 15) / 16;
     double part = 0.0;
     if (t < 7 * m) {
-      const int j = t % m, cnt = min(16, n - 16 * j);
-      const double *v = scratch + (t / m) * nt + 16 * j;
+      const int j = t % m;
+      const double *v = scratch + (t / m) * nt + j;
       double x[16];
 #pragma unroll
-      for (int l = 0; l < 16; ++l) x[l] = l < cnt ? v[l] : 0.0;
+      for (int l = 0; l < 16; ++l) x[l] = j + l * m < n ? v[l * m] : 0.0;
       part = x[0];
 #pragma unroll
       for (int l = 1; l < 16; ++l) part += x[l];
