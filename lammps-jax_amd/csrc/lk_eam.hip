@@ -183,25 +183,54 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
   __shared__ S part[4][TPB][W][kWave];
   __shared__ double vir[TPB][6][W];
   __shared__ double tpart[TPB][7];  // per tile: pair energy, virial 1..6
-  fused_tail_reset(a.pack);
-  const Window<S> win = fill_window<S>(lds, kForceLds, a, a.n_rtab);
+  __shared__ double temb[TPB];      // per tile: the density pass's embedding energy
   const int sub = wave_in_block() / W;
   const int wave = wave_in_block() % W;
   const int lane = threadIdx.x & (kWave - 1);
-  for (GroupWalk gw = group_walk(ngroups); gw.g < gw.g_end; gw.g += gw.step) {
-    const int tile = gw.g * TPB + sub;
+  GroupWalk gw = group_walk(ngroups);
+  // A group's rows: ids, kept counts and slot base, then (once the ids are in) the row atoms'
+  // records and F'; and each tile's embedding energy (slot 0 of its partials, from an earlier
+  // launch), held by thread q < TPB for tile q until the group's sums.
+  int i = -1, cnt = 0;
+  long base = 0;
+  double emb = 0.0;
+  auto load_ids = [&](int g) {
+    const int tile = g * TPB + sub;
     const int ii = tile * kWave + lane;
-    const bool row = ii < a.num_rows;
-    const int i = row ? a.row_atom[ii] : -1;
-    const int cnt = i >= 0 ? a.row_count[ii] : 0;
-    Atom4<S> ai = {S(0), S(0), S(0), S(0)};
-    S fpi = S(0);
+    const bool row = g < gw.g_end && ii < a.num_rows;
+    i = row ? a.row_atom[ii] : -1;
+    const int c = row ? a.row_count[ii] : 0;  // loaded beside the id, kept for a row with an atom
+    cnt = i >= 0 ? c : 0;
+    base = g < gw.g_end && tile * kWave < a.num_rows ? a.tile_off[tile] : 0;
+    const int t = g * TPB + static_cast<int>(threadIdx.x);
+    emb = threadIdx.x < TPB && g < gw.g_end && t < a.ntiles ? a.partials[8L * t] : 0.0;
+  };
+  Atom4<S> ai;
+  S fpi;
+  auto load_atom = [&]() {
+    ai = {S(0), S(0), S(0), S(0)};
+    fpi = S(0);
     if (i >= 0) {
       ai = a.atoms[i];
       fpi = a.fp[i];
     }
+  };
+  // The first group's ids and the tail reset's bounds load before the window's loads, so their
+  // round trips overlap the fill instead of preceding it, and waiting for them does not wait for
+  // the fill (the vector memory counter retires loads in order); the records follow the fill's
+  // issue and arrive with it.
+  const TailBounds tb = tail_bounds(a.pack);
+  load_ids(gw.g);
+  const Window<S> win = fill_window_issue<S>(lds, kForceLds, a, a.n_rtab);
+  fused_tail_reset(a.pack, tb, W * TPB * kWave);
+  load_atom();
+  window_ready();
+  for (bool first = true; gw.g < gw.g_end; gw.g += gw.step, first = false) {
+    if (!first) {
+      load_ids(gw.g);
+      load_atom();
+    }
     const int zi = clamp_species(static_cast<int>(ai.w), a.n_el);
-    const long base = tile * kWave < a.num_rows ? a.tile_off[tile] : 0;
     S fx = S(0), fy = S(0), fz = S(0), ep = S(0);
     double w0 = 0, w1 = 0, w2 = 0, w3 = 0, w4 = 0, w5 = 0;
     struct Rec {
@@ -340,6 +369,7 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
         tpart[sub][1 + lane] = v;
       }
     }
+    if (threadIdx.x < TPB) temb[threadIdx.x] = emb;
     __syncthreads();
     // The group's sums over its tiles in tile order, the density pass's embedding energy of
     // each tile (slot 0 of its partials, from an earlier launch) added to its pair energy,
@@ -351,7 +381,7 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
       for (int q = 0; q < TPB; ++q) {
         const int t = gw.g * TPB + q;
         if (t >= a.ntiles) break;
-        v += c == 0 ? a.partials[8L * t] + tpart[q][0] : (VIRIAL ? tpart[q][c] : 0.0);
+        v += c == 0 ? temb[q] + tpart[q][0] : (VIRIAL ? tpart[q][c] : 0.0);
       }
       put_partial(a.partials + 8L * TPB * gw.g + c, v);
     }

@@ -35,18 +35,37 @@ __device__ __forceinline__ Coef<double> coef_from(double2 e0, double2 e1)
 
 // ResetEdgeTailFunctor of a fused pack: the slots past this pack's count that held the previous
 // pack's edges, [min(demand, max_edges), previous live count), return to the padding.
-__device__ __forceinline__ void fused_tail_reset(const FusedPack &fp)
+// The reset's bounds (the new count, the previous step's live end), loaded ahead of the reset
+struct TailBounds {
+  long count = 0, end = 0;
+};
+
+__device__ __forceinline__ TailBounds tail_bounds(const FusedPack &fp)
 {
-  if (!fp.state) return;
+  TailBounds b;
+  if (!fp.state) return b;
   const long c = fp.state[kDemand];
-  const long count = c < fp.max_edges ? c : fp.max_edges;
-  const long reset_end = fp.state[kPrevLive];
-  for (long e = count + static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < reset_end;
-       e += static_cast<long>(gridDim.x) * blockDim.x) {
+  b.count = c < fp.max_edges ? c : fp.max_edges;
+  b.end = fp.state[kPrevLive];
+  return b;
+}
+
+// nthreads: the block's size, a constant where the caller knows it (blockDim.x may compile to a
+// vector load of the dispatch's group size, whose wait would also wait for every load before it)
+__device__ __forceinline__ void fused_tail_reset(const FusedPack &fp, const TailBounds &b,
+                                                 int nthreads)
+{
+  for (long e = b.count + static_cast<long>(blockIdx.x) * nthreads + threadIdx.x; e < b.end;
+       e += static_cast<long>(gridDim.x) * nthreads) {
     fp.senders[e] = fp.pad;
     fp.receivers[e] = fp.pad;
     fp.mask[e] = 0;
   }
+}
+
+__device__ __forceinline__ void fused_tail_reset(const FusedPack &fp)
+{
+  fused_tail_reset(fp, tail_bounds(fp), static_cast<int>(blockDim.x));
 }
 
 template <typename S>
@@ -101,10 +120,13 @@ struct Window {
   int lo;  // first node in LDS
 };
 
-// Copies the window into LDS (all threads of the block) and returns it.
+// Issues the loads that copy the window into LDS (all threads of the block) and returns it;
+// window_ready() waits for them. A caller may issue loads of its own in between: they overlap
+// the fill, and those issued before it are waited for without waiting for the fill (the vector
+// memory counter retires loads in order).
 template <typename S>
-__device__ __forceinline__ Window<S> fill_window(LdsEntry<S> *lds, int cap_entries,
-                                                 const EamArgs<S> &a, int T)
+__device__ __forceinline__ Window<S> fill_window_issue(LdsEntry<S> *lds, int cap_entries,
+                                                       const EamArgs<S> &a, int T)
 {
   Window<S> w;
   w.lds = lds;
@@ -126,8 +148,22 @@ __device__ __forceinline__ Window<S> fill_window(LdsEntry<S> *lds, int cap_entri
                                        16, 0, 0);
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);  // the loads have written LDS
+  return w;
+}
+
+__device__ __forceinline__ void window_ready()
+{
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have written LDS
   __syncthreads();
+}
+
+// Copies the window into LDS (all threads of the block) and returns it.
+template <typename S>
+__device__ __forceinline__ Window<S> fill_window(LdsEntry<S> *lds, int cap_entries,
+                                                 const EamArgs<S> &a, int T)
+{
+  const Window<S> w = fill_window_issue<S>(lds, cap_entries, a, T);
+  window_ready();
   return w;
 }
 
