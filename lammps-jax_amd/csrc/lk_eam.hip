@@ -38,7 +38,7 @@ __global__ __launch_bounds__(W * TPB * 64) LK_EIGHT_WAVES void k_eam_density_row
 {
   __shared__ LdsEntry<S> lds[kDensLds];
   __shared__ S part[TPB][W][kWave];
-  const Window<S> win = fill_window<S>(lds, kDensLds, a, a.n_el);
+  const Window<S> win = fill_window<S>(lds, kDensLds, a, a.n_el, W * TPB * kWave);
   const int sub = wave_in_block() / W;
   const int wave = wave_in_block() % W;
   const int lane = threadIdx.x & (kWave - 1);
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(W * TPB * 64) void k_eam_force_rows(EamArgs<S> a, i
   // issue and arrive with it.
   const TailBounds tb = tail_bounds(a.pack);
   load_ids(gw.g);
-  const Window<S> win = fill_window_issue<S>(lds, kForceLds, a, a.n_rtab);
+  const Window<S> win = fill_window_issue<S>(lds, kForceLds, a, a.n_rtab, W * TPB * kWave);
   fused_tail_reset(a.pack, tb, W * TPB * kWave);
   load_atom();
   window_ready();

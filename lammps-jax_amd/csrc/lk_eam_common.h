@@ -63,10 +63,6 @@ __device__ __forceinline__ void fused_tail_reset(const FusedPack &fp, const Tail
   }
 }
 
-__device__ __forceinline__ void fused_tail_reset(const FusedPack &fp)
-{
-  fused_tail_reset(fp, tail_bounds(fp), static_cast<int>(blockDim.x));
-}
 
 template <typename S>
 struct EamArgs {
@@ -124,9 +120,11 @@ struct Window {
 // window_ready() waits for them. A caller may issue loads of its own in between: they overlap
 // the fill, and those issued before it are waited for without waiting for the fill (the vector
 // memory counter retires loads in order).
+// nthreads: the block's size (a constant at every caller: blockDim.x can compile to a vector load
+// of the dispatch's group size, and its wait to a wait for every load issued before it).
 template <typename S>
 __device__ __forceinline__ Window<S> fill_window_issue(LdsEntry<S> *lds, int cap_entries,
-                                                       const EamArgs<S> &a, int T)
+                                                       const EamArgs<S> &a, int T, int nthreads)
 {
   Window<S> w;
   w.lds = lds;
@@ -137,7 +135,7 @@ __device__ __forceinline__ Window<S> fill_window_issue(LdsEntry<S> *lds, int cap
   // Loads straight into LDS (global_load_lds_dwordx4): each lane names its own 16-byte entry, and
   // a wave's 64 entries land at consecutive places from the wave-uniform LDS address; no data
   // passes through registers, so every load of the fill is in flight at once.
-  const int lane = threadIdx.x & (kWave - 1), nw = blockDim.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1), nw = nthreads / kWave;
   for (int c = threadIdx.x / kWave; c * kWave < n; c += nw) {
     const int q = c * kWave + lane;
     if (q < n) {
@@ -160,9 +158,9 @@ __device__ __forceinline__ void window_ready()
 // Copies the window into LDS (all threads of the block) and returns it.
 template <typename S>
 __device__ __forceinline__ Window<S> fill_window(LdsEntry<S> *lds, int cap_entries,
-                                                 const EamArgs<S> &a, int T)
+                                                 const EamArgs<S> &a, int T, int nthreads)
 {
-  const Window<S> w = fill_window_issue<S>(lds, cap_entries, a, T);
+  const Window<S> w = fill_window_issue<S>(lds, cap_entries, a, T, nthreads);
   window_ready();
   return w;
 }
@@ -280,7 +278,7 @@ struct HWindow {
 };
 
 __device__ __forceinline__ HWindow fill_hwindow(float *lds, int cap_floats, const float *htab,
-                                                int W, int nr)
+                                                int W, int nr, int nthreads)
 {
   HWindow w;
   w.lds = lds;
@@ -289,8 +287,16 @@ __device__ __forceinline__ HWindow fill_hwindow(float *lds, int cap_floats, cons
   w.lo = nr > cap_nodes ? nr - cap_nodes : 0;
   const int n = (nr - w.lo) * W;
   const float *src = htab + static_cast<long>(w.lo) * W;
-  for (int q = threadIdx.x; q < n; q += blockDim.x) lds[q] = src[q];
-  __syncthreads();
+  // loads straight into LDS, one float per lane (rows of W floats need not align to 16 bytes)
+  const int lane = threadIdx.x & (kWave - 1), nw = nthreads / kWave;
+  for (int c = threadIdx.x / kWave; c * kWave < n; c += nw) {
+    const int q = c * kWave + lane;
+    if (q < n)
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void *)(src + q),
+                                       (__attribute__((address_space(3))) void *)(lds + c * kWave),
+                                       4, 0, 0);
+  }
+  window_ready();
   return w;
 }
 

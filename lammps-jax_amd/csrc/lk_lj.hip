@@ -43,7 +43,7 @@ __global__ __launch_bounds__(W * 64) void k_lj_rows(LjArgs<S> a)
   __shared__ double vir[6][W];
   __shared__ double scratch[7 * W * kWave];
   // No early exit: every block counts itself in for the last-block reduction.
-  fused_tail_reset(a.pack);
+  fused_tail_reset(a.pack, tail_bounds(a.pack), W * kWave);
   const int tile = tile_of_block();
   const bool has_rows = tile * kWave < a.num_rows;
   const int wave = wave_in_block();

@@ -145,7 +145,7 @@ void k_step_pack(StepPack p, EamArgs<S> a, int ngroups)
   __shared__ int sbase[TPB];
 
   Window<S> win{};
-  if constexpr (EAM) win = fill_window<S>(lds, kStepLds, a, a.n_el);
+  if constexpr (EAM) win = fill_window<S>(lds, kStepLds, a, a.n_el, W * TPB * kWave);
   if constexpr (!EAM && sizeof(S) == 8) {
     // the atom records for the sweeps (cpp:35-52: x as is, species = type - 1)
     if (p.atoms_out)

@@ -839,8 +839,11 @@ __global__ __launch_bounds__(kRowBlock) void k_eam_density_inc(EamArgs<S> m, Two
   constexpr int kLds = PAIR ? kIncLds : kIncDensLds;
   constexpr int APB = kRowBlock / G;  // atoms per block
   __shared__ LdsEntry<S> lds[kLds];
-  fused_tail_reset(t.pack);
-  const Window<S> win = fill_window<S>(lds, kLds, m, PAIR ? m.n_rtab : m.n_el);
+  // the tail reset's bounds load before the window's loads and its stores go out after them
+  const TailBounds tb = tail_bounds(t.pack);
+  const Window<S> win = fill_window_issue<S>(lds, kLds, m, PAIR ? m.n_rtab : m.n_el, kRowBlock);
+  fused_tail_reset(t.pack, tb, kRowBlock);
+  window_ready();
   const int g = threadIdx.x / G, gl = threadIdx.x % G;
   const int nsb = (t.nall + APB - 1) / APB;
   for (int blk = blockIdx.x; blk < nsb; blk += gridDim.x) {
@@ -1016,9 +1019,10 @@ __device__ __forceinline__ void eam_force_inc_rows(const EamArgs<S> &m, const Tw
   Window<S> win{};
   HWindow hw{};
   if constexpr (sizeof(S) == 4)
-    hw = fill_hwindow(reinterpret_cast<float *>(lds), lds_entries * 4, m.htab, m.htab_w, m.nr);
+    hw = fill_hwindow(reinterpret_cast<float *>(lds), lds_entries * 4, m.htab, m.htab_w, m.nr,
+                      kRowBlock);
   else
-    win = fill_window<S>(lds, lds_entries, m, m.n_rtab);
+    win = fill_window<S>(lds, lds_entries, m, m.n_rtab, kRowBlock);
   const int g = threadIdx.x / G, gl = threadIdx.x % G;
   const int erows = energy_rows(t, HALF);
   const int nsb = (t.nall + APB - 1) / APB;
@@ -1228,7 +1232,7 @@ void k_lj_inc(LjModel<S> m, TwoSided t)
   __shared__ double vt[6][APB];
   __shared__ double et[APB];
   __shared__ double scratch[7 * kRowBlock];
-  fused_tail_reset(t.pack);
+  fused_tail_reset(t.pack, tail_bounds(t.pack), kRowBlock);
   const int g = threadIdx.x / G, gl = threadIdx.x % G;
   const int erows = energy_rows(t, false);
   const S tiny = static_cast<S>(1.0e-12);
@@ -1734,7 +1738,7 @@ template <typename S, bool NEWTON>
 __global__ __launch_bounds__(kRowBlock) void k_eam_edge_force(EamArgs<S> m, EdgeOut<S> o)
 {
   __shared__ LdsEntry<S> lds[kIncLds];
-  const Window<S> win = fill_window<S>(lds, kIncLds, m, m.n_rtab);
+  const Window<S> win = fill_window<S>(lds, kIncLds, m, m.n_rtab, kRowBlock);
   const long ne = live_edges(o);
   const long stride = static_cast<long>(gridDim.x) * blockDim.x;
   for (long e = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; e < ne; e += stride) {
