@@ -33,9 +33,7 @@ __device__ __forceinline__ Coef<double> coef_from(double2 e0, double2 e1)
   return c;
 }
 
-// ResetEdgeTailFunctor of a fused pack: the slots past this pack's count that held the previous
-// pack's edges, [min(demand, max_edges), previous live count), return to the padding.
-// The reset's bounds (the new count, the previous step's live end), loaded ahead of the reset
+// The tail reset's bounds (the new count, the previous step's live end), loaded ahead of it
 struct TailBounds {
   long count = 0, end = 0;
 };
@@ -50,8 +48,10 @@ __device__ __forceinline__ TailBounds tail_bounds(const FusedPack &fp)
   return b;
 }
 
-// nthreads: the block's size, a constant where the caller knows it (blockDim.x may compile to a
-// vector load of the dispatch's group size, whose wait would also wait for every load before it)
+// ResetEdgeTailFunctor of a fused pack: the slots past this pack's count that held the previous
+// pack's edges, [min(demand, max_edges), previous live count), return to the padding.
+// nthreads: the block's size, a constant at every caller (blockDim.x may compile to a vector
+// load of the dispatch's group size, whose wait would also wait for every load before it)
 __device__ __forceinline__ void fused_tail_reset(const FusedPack &fp, const TailBounds &b,
                                                  int nthreads)
 {
@@ -62,7 +62,6 @@ __device__ __forceinline__ void fused_tail_reset(const FusedPack &fp, const Tail
     fp.mask[e] = 0;
   }
 }
-
 
 template <typename S>
 struct EamArgs {
