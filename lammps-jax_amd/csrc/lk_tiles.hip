@@ -593,6 +593,16 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
     const int tile = gw.g;
     const int U = t.ucount[tile];
     const bool staged = U >= 0;  // block-uniform
+    // the tile's rows, loaded first so that their round trips overlap the union's staging
+    const int pos = tile * kTileRows + sub * kWave + lane;
+    const int i = t.atom[pos];
+    const int nn = t.nn[pos];
+    double xi0 = 0.0, xi1 = 0.0, xi2 = 0.0;
+    if (i >= 0) {
+      xi0 = p.x[3L * i + 0];
+      xi1 = p.x[3L * i + 1];
+      xi2 = p.x[3L * i + 2];
+    }
     if (staged) {
       for (int u = threadIdx.x; u < U; u += blockDim.x) {
         const int g = t.uni[static_cast<long>(tile) * kTileUnion + u];
@@ -605,15 +615,6 @@ void k_step_tiles(TileStep p, EamArgs<double> a, TileView t)
     }
     for (int k = threadIdx.x; k < kBitWords; k += blockDim.x) (&sbits[0][0][0])[k] = 0u;
     __syncthreads();
-    const int pos = tile * kTileRows + sub * kWave + lane;
-    const int i = t.atom[pos];
-    const int nn = t.nn[pos];
-    double xi0 = 0.0, xi1 = 0.0, xi2 = 0.0;
-    if (i >= 0) {
-      xi0 = p.x[3L * i + 0];
-      xi1 = p.x[3L * i + 1];
-      xi2 = p.x[3L * i + 2];
-    }
     const int nmax = wave_max_int(nn);  // the sub-tile's longest row
     int cnt = 0;
     double rho = 0.0;
