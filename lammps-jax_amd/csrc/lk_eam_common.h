@@ -121,6 +121,7 @@ struct Window {
 // memory counter retires loads in order).
 // nthreads: the block's size (a constant at every caller: blockDim.x can compile to a vector load
 // of the dispatch's group size, and its wait to a wait for every load issued before it).
+// lds must point into a __shared__ array: the loads take it as an LDS address.
 template <typename S>
 __device__ __forceinline__ Window<S> fill_window_issue(LdsEntry<S> *lds, int cap_entries,
                                                        const EamArgs<S> &a, int T, int nthreads)
@@ -286,7 +287,8 @@ __device__ __forceinline__ HWindow fill_hwindow(float *lds, int cap_floats, cons
   w.lo = nr > cap_nodes ? nr - cap_nodes : 0;
   const int n = (nr - w.lo) * W;
   const float *src = htab + static_cast<long>(w.lo) * W;
-  // loads straight into LDS, one float per lane (rows of W floats need not align to 16 bytes)
+  // loads straight into LDS (lds: a __shared__ array), one float per lane (rows of W floats need
+// not align to 16 bytes)
   const int lane = threadIdx.x & (kWave - 1), nw = nthreads / kWave;
   for (int c = threadIdx.x / kWave; c * kWave < n; c += nw) {
     const int q = c * kWave + lane;
